@@ -1,0 +1,230 @@
+"""Benchmark of the softhier-ops hot path on one MI355X: the SigLIP-B encoder layer (
+B=32, S=256, D=768, 12 heads, FFN 3072, fp16, weights N(0, 0.02), biases zero, x ~ N(0, 1), seeded).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--sequence fused|reference] [--no-cpu] [--no-rowops]
+
+A step is one forward pass of the layer over the batch through libshops.so (inputs resident in HBM). Prints ONE
+JSON line with the whole-job TFLOP/s, the roofline of the dominant kernel (HIP events around its launches in
+the timed region, on the library stream = the legacy null stream torch also uses), the per-op breakdown, the
+row-op HBM bandwidths at the batched shapes (cold: rotating buffer sets of >= 512 MiB) and the numpy CPU
+baseline (the oracle's restatement, timed on this host).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "encoder-layer TFLOP/s fp16 (S=256,D=768,B=32); % MFMA peak; rowops HBM GB/s"
+PEAK_TFLOPS = 2500.0        # MI355X dense fp16 MFMA
+PEAK_GBS = 8000.0           # MI355X HBM3E
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--sequence", default="fused", choices=["fused", "reference"])
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--seq", type=int, default=256)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the numpy CPU baseline")
+    ap.add_argument("--no-rowops", action="store_true", help="skip the row-op bandwidth measurement")
+    return ap.parse_args()
+
+
+def rowops_bandwidth(lib, torch, B: int, S: int, D: int, F: int, H: int, reps: int = 3) -> dict:
+    """Row ops at the batched shapes, cold: buffer sets rotated so that >= 512 MiB is touched between reuses
+    (MI355X Infinity Cache = 256 MiB). Algorithmic bytes: each input read once, the output written once."""
+    from softhier_mlir_amd import shops
+    A = shops.addr
+    M = B * S
+    ops = {
+        "layernorm": ((M, D), 2 * (2 * M * D + 2 * D)),
+        "softmax": ((H * M, S), 2 * 2 * H * M * S),
+        "gelu": ((M, F), 2 * 2 * M * F),
+        "add": ((M, D), 2 * 3 * M * D),
+        "add_bias": ((M, D), 2 * (2 * M * D + D)),
+        "transpose": ((M, D), 2 * 2 * M * D),
+    }
+    out = {}
+    g = torch.ones((1, max(D, F)), dtype=torch.float16, device="cuda")
+    be = torch.zeros((1, max(D, F)), dtype=torch.float16, device="cuda")
+    for name, ((r, c), nbytes) in ops.items():
+        per_set = nbytes
+        nsets = max(2, int((512 << 20) // per_set) + 1)
+        sets = []
+        for _ in range(nsets):
+            x = torch.randn((r, c), dtype=torch.float16, device="cuda")
+            y = torch.empty((c, r) if name == "transpose" else (r, c), dtype=torch.float16, device="cuda")
+            b = torch.randn((r, c), dtype=torch.float16, device="cuda") if name == "add" else None
+            sets.append((x, y, b))
+
+        def run(x, y, b):
+            if name == "layernorm":
+                lib.sh_layernorm(A(y), A(x), A(g), A(be), r, c, c, 1e-6, shops.SH_ALL)
+            elif name == "softmax":
+                lib.sh_softmax_rows(A(y), A(x), r, c, c, 0.125, shops.SH_ALL)
+            elif name == "gelu":
+                lib.sh_gelu(A(y), A(x), r, c, c, shops.SH_ALL)
+            elif name == "add":
+                lib.sh_add(A(y), A(x), A(b), r, c, c, shops.SH_ALL)
+            elif name == "add_bias":
+                lib.sh_add_bias(A(y), A(x), A(g), r, c, c, shops.SH_ALL)
+            else:
+                lib.sh_transpose(A(y), A(x), r, c, c, r, shops.SH_ALL)
+
+        for s in sets:
+            run(*s)
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(reps):
+            for s in sets:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                run(*s)
+                e1.record()
+                times.append((e0, e1))
+        torch.cuda.synchronize()
+        ms = sorted(a.elapsed_time(b) for a, b in times)
+        med = ms[len(ms) // 2]
+        gbs = nbytes / (med * 1e-3) / 1e9
+        out[name] = {"shape": [r, c], "bytes": nbytes, "us": round(med * 1e3, 2), "GB/s": round(gbs, 1),
+                     "frac": round(gbs / PEAK_GBS, 3)}
+        del sets
+        torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(B: int, S: int, D: int, F: int, H: int, p: dict, x) -> dict:
+    """The oracle's numpy restatement of one encoder layer, timed on this host's cores (median of 5)."""
+    import numpy as np
+
+    from oracle import refs
+    threads = None
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=None)
+    except Exception:
+        pass
+    Bs = min(B, 8)                                   # bounded sample: 8 of the 32 sequences
+    xs = x[: Bs * S]
+    refs.encoder_layer(xs, p, H, B=Bs)               # warm-up
+    ts = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        refs.encoder_layer(xs, p, H, B=Bs)
+        ts.append(time.perf_counter() - t0)
+    med = sorted(ts)[2]
+    from softhier_mlir_amd.encoder import flops_per_layer
+    value = flops_per_layer(Bs, S, D, F) / med / 1e12
+    return {"value": round(value, 4), "unit": "TFLOP/s", "cores": threads or os.cpu_count(), "kind": "port",
+            "sample": f"numpy fp32 oracle of one layer on {Bs} of the {B} sequences (S={S}), median of 5 runs "
+                      f"({med:.3f} s each); host cpu_count={os.cpu_count()} affinity={len(os.sched_getaffinity(0))}"}
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build (the path shards by "
+              f"sequence across GPUs; see DESIGN.md)", file=sys.stderr)
+        return 2
+    import numpy as np
+    import torch
+
+    from softhier_mlir_amd import data, encoder, shops
+
+    lib = shops.load()
+    lib.sh_init()
+    B, S, D, F, H = args.batch, args.seq, 768, 3072, 12
+    p = data.encoder_params(D, F, seed=100)
+    xh = data.normal((B * S, D), 7)
+    x = torch.from_numpy(xh).cuda()
+    out = torch.empty_like(x)
+    enc = encoder.Encoder(D, F, H)
+    lp = encoder.LayerParams.from_host(p)
+    step = enc.layer_fused if args.sequence == "fused" else enc.layer_reference
+
+    for _ in range(args.warmup):
+        step(x, out, lp, B, S)
+    torch.cuda.synchronize()
+
+    # timed region: K steps, HIP events around every op of every step (fused sequence)
+    events: dict = {}
+
+    class Tap:
+        def __init__(self, name):
+            self.name = name
+
+        def __enter__(self):
+            self.e0 = torch.cuda.Event(enable_timing=True)
+            self.e1 = torch.cuda.Event(enable_timing=True)
+            self.e0.record()
+
+        def __exit__(self, *exc):
+            self.e1.record()
+            events.setdefault(self.name, []).append((self.e0, self.e1))
+            return False
+
+    enc.tap = Tap if args.sequence == "fused" else None
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(x, out, lp, B, S)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    enc.tap = None
+    ms_per_step = elapsed * 1e3 / args.steps
+    flop = encoder.flops_per_layer(B, S, D, F)
+    value = flop / (elapsed / args.steps) / 1e12
+
+    costs = encoder.Encoder.op_costs(B, S, D, F, H)
+    breakdown = {}
+    for name, evs in events.items():
+        us = sum(a.elapsed_time(b) for a, b in evs) / len(evs) * 1e3
+        c = costs[name]
+        entry = {"us": round(us, 2)}
+        if c["flop"]:
+            entry["TFLOP/s"] = round(c["flop"] / (us * 1e-6) / 1e12, 1)
+            entry["mfma_frac"] = round(c["flop"] / (us * 1e-6) / 1e12 / PEAK_TFLOPS, 3)
+        entry["GB/s"] = round(c["bytes"] / (us * 1e-6) / 1e9, 1)
+        breakdown[name] = entry
+    roofline = None
+    if breakdown:
+        dom = max(breakdown, key=lambda k: breakdown[k]["us"])
+        c = costs[dom]
+        us = breakdown[dom]["us"]
+        if c["flop"]:
+            ach = c["flop"] / (us * 1e-6) / 1e12
+            roofline = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(ach / PEAK_TFLOPS, 4), "traffic": None,
+                        "algorithmic_flop_per_launch": c["flop"], "avg_launch_us": us}
+        else:
+            ach = c["bytes"] / (us * 1e-6) / 1e9
+            roofline = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                        "frac": round(ach / PEAK_GBS, 4), "traffic": None, "avg_launch_us": us}
+
+    rowops = None if args.no_rowops else rowops_bandwidth(lib, torch, B, S, D, F, H)
+    cpu = None if args.no_cpu else cpu_baseline(B, S, D, F, H, p, xh)
+
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp16", "data": "synthetic (seeded N(0,0.02) weights, N(0,1) input)",
+        "config": {"workload": f"SigLIP-B encoder layer forward, {args.sequence} op sequence", "global_batch": B,
+                   "seq_len": S, "d_model": D, "ffn": F, "heads": H, "layers": 1, "parallelism": "single GPU"},
+        "mfma_frac_of_peak": round(value / PEAK_TFLOPS, 4),
+        "roofline": roofline, "breakdown": breakdown, "rowops": rowops, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,187 @@
+/* softhier-ops for MI355X (gfx950): the C ABI.
+ *
+ * This header re-exports the hot-path subset of the reference's operator library header
+ * (runwangdl/softhier-mlir runtime/sh_ops.h) with the same names, argument order, types and error codes,
+ * so the same op sequence (emitted programs, C test drivers, ctypes callers) runs unchanged. Each
+ * declaration cites the reference line it replaces.
+ *
+ * Execution model (differs from the reference's SPMD model, same observable results):
+ *  - One host thread calls each op once. The op validates its arguments on the host, then enqueues HIP
+ *    kernels on the library stream (sh_set_stream; default: the legacy null stream, which is ordered with
+ *    PyTorch's default stream). Ops are stream-ordered and asynchronous; sh_barrier_global() drains them.
+ *  - Tensors are fp16 row-major in GPU memory, addressed by 64-bit byte addresses (device pointers:
+ *    a torch tensor's data_ptr(), sh_hbm_addr() or sh_hbm_malloc()). Leading dimensions are in elements.
+ *  - `cluster` is accepted for source compatibility and ignored: the op always runs on the whole GPU.
+ *    sh_cluster_id() == 0, sh_is_first_core() == 1 and sh_num_clusters() == 1, so guards such as
+ *    `if (sh_cluster_id() == 0 && sh_is_first_core())` in emitted code fire exactly once.
+ *  - Constraint checks mirror the reference (same conditions, same return codes, same budgets: the
+ *    reference's 1 MiB cluster TCDM, reported by sh_l1_size()), so a call fails here exactly when it
+ *    fails there. The additive entry points at the end carry no TCDM budget.
+ *  - A HIP runtime failure makes an int op return SH_EHIP (-3, additive) and records the message
+ *    (sh_last_error / sh_last_error_str); void ops record it the same way.
+ *  - Not re-entrant across host threads.
+ */
+#ifndef SH_OPS_H
+#define SH_OPS_H
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- runtime wrappers (reference runtime/sh_ops.h:19-37, runtime/sh_rt.inc.c:2-29) ---------------------- */
+void     sh_init(void);                 /* sh_ops.h:20   picks up the current HIP device; idempotent */
+void     sh_barrier_global(void);       /* sh_ops.h:21   drains the library stream */
+void     sh_barrier_cluster(void);      /* sh_ops.h:22   same as sh_barrier_global */
+uint32_t sh_cluster_id(void);           /* sh_ops.h:23   0 */
+uint32_t sh_core_id(void);              /* sh_ops.h:24   0 */
+int      sh_is_first_core(void);        /* sh_ops.h:25   1 */
+int      sh_is_dm_core(void);           /* sh_ops.h:26   1 */
+uint32_t sh_num_clusters(void);         /* sh_ops.h:27   1: the GPU is one cluster */
+void     sh_timer_start(void);          /* sh_ops.h:28   HIP event on the library stream */
+void     sh_timer_end(void);            /* sh_ops.h:29   prints "[Performance Counter]: Execution period is N ns", restarts */
+void     sh_eoc(uint32_t val);          /* sh_ops.h:30   drains the stream, flushes stdout, records val */
+uint32_t sh_cycles(void);               /* sh_ops.h:31   ns since sh_init (1 GHz equivalence), read after the stream drains */
+void     sh_printf(const char *fmt, ...);                /* sh_ops.h:32 */
+uint64_t sh_hbm_addr(uint64_t byte_offset);             /* sh_ops.h:33   arena base + offset (arena: SH_HBM_ARENA_BYTES, default 1 GiB, lazy) */
+uint64_t sh_hbm_malloc(uint32_t bytes);                 /* sh_ops.h:34   separate device allocation, 256 B aligned */
+uint32_t sh_l1_size(void);                              /* sh_ops.h:35   the reference cluster's TCDM bytes (0x100000) */
+void     sh_preload_wait(uint64_t sentinel);            /* sh_ops.h:36   drains the stream (data is resident) */
+void     sh_call_on_core_stack(void (*fn)(void), uint32_t bytes_per_core);   /* sh_ops.h:48   calls fn() */
+
+#define SH_ALL 0xFFFFFFFFu                              /* sh_ops.h:39 */
+#define SH_CORE_STACK_BYTES 40960u                      /* sh_ops.h:47 */
+#define SH_SELF (sh_cluster_id())                       /* sh_ops.h:308 */
+
+/* ---- formats (sh_ops.h:51) -------------------------------------------------------------------------- */
+enum sh_fmt { SH_FP16 = 0, SH_FP8 = 1, SH_INT16 = 2, SH_INT8 = 3 };
+
+/* ---- GEMM: Z[M,N] (+)= X[M,K] . W[K,N] (sh_ops.h:53-88, runtime/sh_gemm.inc.c:12-189) ------------------
+ * fp16 operands, fp32 accumulation on MFMA, fp16 result (RNE). tm/tn/tk are the caller's tile hints: they set
+ * the divisibility rule exactly as in the reference (0 -> 256); the GPU tile is chosen by the library. */
+typedef struct {
+    uint32_t tm, tn, tk;     /* tile; 0 -> 256 */
+    uint32_t pipeline;       /* accepted (the GPU kernels always double-buffer) */
+    uint32_t accumulate;     /* 1: Z += X.W (Z read first); 0: Z = X.W */
+    uint32_t fmt;            /* enum sh_fmt; only SH_FP16 computes (others: -1) */
+    uint32_t l1_base;        /* counts towards the TCDM budget exactly as in the reference */
+} sh_gemm_cfg;               /* sh_ops.h:54-60 */
+
+/* sh_ops.h:66-67 (sh_gemm.inc.c:53-117): -1 when M%tm, N%tn or K%tk != 0 (or fmt != SH_FP16, or a NULL
+ * address), -2 when sh_gemm_l1_bytes() exceeds the reference TCDM, SH_EHIP on a HIP failure, else 0. */
+int sh_gemm(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
+            uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg, uint32_t cluster);
+
+/* sh_ops.h:72-73 (sh_gemm.inc.c:127-189): SUMMA mode over a virtual SH_MESH_P x SH_MESH_P mesh of output
+ * tiles (the reference's 4 x 4 cluster mesh). Same constraints and codes: tm == tn, M == N == P * tm,
+ * K % tk == 0 (-1), TCDM budget (-2). Mesh row py owns X row-panel py; its workgroups run on one XCD so the
+ * panel is fetched from HBM once into that XCD's L2 and re-read from there by the whole row. */
+#define SH_MESH_P 4u
+int sh_gemm_mesh(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
+                 uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg);
+
+/* sh_ops.h:88 (sh_gemm.inc.c:24-30): l1_base + (pipeline ? 2 : 1) * (tm*tk + tk*tn) * 2 + tm*tn*2. */
+uint32_t sh_gemm_l1_bytes(uint32_t M, uint32_t N, uint32_t K, const sh_gemm_cfg *cfg);
+
+/* ---- row-wise / elementwise ops (sh_ops.h:90-100, runtime/sh_rowops.inc.c:383-465) -------------------
+ * fp16 in/out, fp32 arithmetic, one pass over HBM. Parameter rows (gamma, beta, bias) are fp16 rows. */
+void sh_layernorm(uint64_t y, uint64_t x, uint64_t gamma, uint64_t beta, uint32_t rows, uint32_t cols, uint32_t ld, float eps, uint32_t cluster);  /* sh_ops.h:94 */
+void sh_softmax_rows(uint64_t y, uint64_t x, uint32_t rows, uint32_t cols, uint32_t ld, float scale, uint32_t cluster);  /* sh_ops.h:95 */
+void sh_gelu(uint64_t y, uint64_t x, uint32_t rows, uint32_t cols, uint32_t ld, uint32_t cluster);                     /* sh_ops.h:96 tanh form */
+void sh_add(uint64_t y, uint64_t a, uint64_t b, uint32_t rows, uint32_t cols, uint32_t ld, uint32_t cluster);          /* sh_ops.h:97 */
+void sh_add_bias(uint64_t y, uint64_t x, uint64_t bias_row, uint32_t rows, uint32_t cols, uint32_t ld, uint32_t cluster); /* sh_ops.h:98 */
+void sh_scale(uint64_t y, uint64_t x, uint32_t rows, uint32_t cols, uint32_t ld, float s, uint32_t cluster);           /* sh_ops.h:99 */
+void sh_transpose(uint64_t dst, uint64_t src, uint32_t rows, uint32_t cols, uint32_t ld_src, uint32_t ld_dst, uint32_t cluster); /* sh_ops.h:100 bit-exact */
+
+/* ---- fused attention (sh_ops.h:102-127, runtime/sh_attention.inc.c:55-243) ----------------------------
+ * o = softmax(scale * q k^T) v per head; head h = columns [h*dh, (h+1)*dh). Flash-style on the GPU (online
+ * softmax over key blocks, scores never leave the CU), so sq only has to satisfy the reference's rules. */
+int sh_attention_head(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t S, uint32_t dh,
+                      uint32_t ldq, uint32_t ldk, uint32_t ldv, uint32_t ldo, float scale, uint32_t cluster);   /* sh_ops.h:109-110 */
+int sh_attention_q(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t S, uint32_t D, uint32_t H,
+                   uint32_t ldq, uint32_t ldk, uint32_t ldv, uint32_t ldo, float scale, uint32_t cluster, uint32_t sq); /* sh_ops.h:114-115 */
+int sh_attention(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t S, uint32_t D, uint32_t H,
+                 uint32_t ldq, uint32_t ldk, uint32_t ldv, uint32_t ldo, float scale, uint32_t cluster);      /* sh_ops.h:116-117 */
+uint32_t sh_attention_l1_bytes_q(uint32_t S, uint32_t dh, uint32_t sq);   /* sh_ops.h:118 */
+uint32_t sh_attention_l1_bytes(uint32_t S, uint32_t dh);                  /* sh_ops.h:119 */
+uint32_t sh_attention_q_block(uint32_t S, uint32_t dh, uint32_t H, uint32_t P);   /* sh_ops.h:123 same rule */
+/* sh_ops.h:127: ns stamps of the last attention call: 7 entry, 0 kernel start, 1..5 = 0, 6 kernel end. */
+uint32_t sh_attention_profile(uint32_t S, uint32_t dh, uint32_t phase);
+
+/* ---- test helpers (sh_ops.h:220-240, runtime/sh_test.inc.c, runtime/sh_rt.inc.c:31-59) ----------------
+ * Fills run as GPU kernels (LCG jump-ahead per element, identical values to the sequential loop); dumps
+ * gather on the GPU and print on the host in the reference's "<tag> r c hex" format. */
+void sh_test_fill_int_fp16(uint64_t a, uint32_t rows, uint32_t cols, uint32_t ld, uint32_t seed, int lo, int hi);              /* sh_ops.h:223 */
+void sh_test_fill_fp16(uint64_t a, uint32_t rows, uint32_t cols, uint32_t ld, uint32_t seed, int lo, int hi, float scale);     /* sh_ops.h:224 */
+void sh_test_dump_samples(uint64_t a, uint32_t rows, uint32_t cols, uint32_t ld, uint32_t seed, uint32_t nsamples, const char *tag); /* sh_ops.h:226 */
+void sh_test_dump_samples_idx(uint64_t a, uint32_t rows, uint32_t cols, uint32_t ld, uint32_t seed, uint32_t nsamples, const char *tag, uint32_t idx); /* sh_ops.h:227 */
+uint32_t sh_test_check_gemm(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
+                            uint32_t ldx, uint32_t ldw, uint32_t ldz, uint32_t nsamples, float tol,
+                            float z0, const char *tag);                                                                        /* sh_ops.h:230-232 */
+void     sh_test_fill_const_fp16(uint64_t a, uint32_t rows, uint32_t cols, uint32_t ld, uint32_t bits);                        /* sh_ops.h:234 */
+void     sh_test_fill_colparity_fp16(uint64_t a, uint32_t rows, uint32_t cols, uint32_t ld, uint32_t even, uint32_t odd);      /* sh_ops.h:235 */
+uint32_t sh_test_check_const_fp16(uint64_t a, uint32_t rows, uint32_t cols, uint32_t ld, uint32_t bits, uint32_t tol, const char *tag); /* sh_ops.h:236 */
+void sh_test_dump_all(uint64_t a, uint32_t rows, uint32_t cols, uint32_t ld, const char *tag);                                  /* sh_ops.h:183 */
+void sh_test_dump_all_idx(uint64_t a, uint32_t rows, uint32_t cols, uint32_t ld, const char *tag, uint32_t idx);                /* sh_ops.h:184 */
+float    sh_fp16_to_f32(uint16_t h);    /* sh_ops.h:239 IEEE binary16 -> binary32, exact */
+uint16_t sh_f32_to_fp16(float f);       /* sh_ops.h:240 RNE; overflow -> Inf; NaN -> 0x7E00 | sign */
+
+/* sh_ops.h:249-258 hardware register conversions: portable equivalents on the host (low 16 bits used). */
+static inline float    sh_h2f(uint32_t h) { return sh_fp16_to_f32((uint16_t)(h & 0xFFFFu)); }
+static inline uint32_t sh_f2h(float f)    { return 0xFFFF0000u | sh_f32_to_fp16(f); }
+
+/* ====================================================================================================
+ * Additive entry points (no counterpart in the reference's ABI; existing layouts are unchanged).
+ * ==================================================================================================== */
+#define SH_EHIP (-3)                     /* an int op's return code for a HIP runtime failure */
+
+int         sh_last_error(void);         /* 0, or the code of the last failure (-1 args, SH_EHIP HIP); cleared on read */
+const char *sh_last_error_str(void);     /* message of the last failure ("" if none) */
+void        sh_set_stream(uint64_t stream);   /* hipStream_t to enqueue on (0 = legacy null stream) */
+uint64_t    sh_get_stream(void);
+double      sh_timer_last_ns(void);      /* the period sh_timer_end() printed last */
+/* Text capture for in-process callers: while on, everything the library prints (sh_printf, sample dumps,
+ * timer lines) is appended to an internal buffer instead of stdout. sh_captured copies it out (NUL
+ * terminated, truncated to cap - 1) and returns its full length; turning capture on clears it. */
+void        sh_capture(int on);
+uint64_t    sh_captured(char *buf, uint64_t cap);
+
+/* Split-K GEMM: K is cut into `splits` contiguous ranges computed by separate workgroups into an fp32
+ * workspace owned by the library, then reduced in a fixed order (deterministic) and rounded once to fp16.
+ * Shape/tile checks as sh_gemm (-1/-2); splits == 0 lets the library choose. */
+int sh_gemm_splitk(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
+                   uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg, uint32_t splits, uint32_t cluster);
+
+/* Fused GEMM epilogue: z = act(X.W [+ z_old if cfg->accumulate] + bias) rounded to fp16, then
+ * [+ residual, rounded again]. bias: 0 or an fp16 (SH_BIAS_FP16) / fp32 (SH_BIAS_FP32) row of N values.
+ * residual: 0 or an fp16 [M,N] tensor with leading dim ldr (may alias z). No tile-divisibility rule and no
+ * TCDM budget; M, N, K >= 1. splits: as sh_gemm_splitk (1 = no split, 0 = library choice). */
+enum { SH_ACT_NONE = 0, SH_ACT_GELU = 1 };
+enum { SH_BIAS_FP16 = 0, SH_BIAS_FP32 = 1 };
+typedef struct {
+    uint64_t bias;        /* 0: none */
+    uint32_t bias_fmt;    /* SH_BIAS_FP16 | SH_BIAS_FP32 */
+    uint32_t act;         /* SH_ACT_NONE | SH_ACT_GELU (tanh form, as sh_gelu) */
+    uint64_t residual;    /* 0: none */
+    uint32_t ldr;         /* leading dim of residual (elements) */
+    uint32_t splits;      /* 1: none; 0: library choice */
+} sh_gemm_epi;
+int sh_gemm_ex(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
+               uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg, const sh_gemm_epi *epi);
+
+/* Batched multi-head attention (the reference has no batch dimension): sequence b uses q + b*bsq*2 bytes,
+ * likewise k/v/o with their own batch strides in elements (e.g. S*ld for rows stacked as [B*S, ld]).
+ * Constraints as sh_attention_q except the TCDM budget; sq == 0 -> the library's choice. */
+int sh_attention_batched(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, uint32_t D, uint32_t H,
+                         uint32_t ldq, uint32_t ldk, uint32_t ldv, uint32_t ldo,
+                         uint64_t bsq, uint64_t bsk, uint64_t bsv, uint64_t bso, float scale, uint32_t sq);
+
+/* LayerNorm with separate input / output leading dims (fused residual stream layouts). */
+void sh_layernorm_ld(uint64_t y, uint64_t x, uint64_t gamma, uint64_t beta, uint32_t rows, uint32_t cols,
+                     uint32_t ldy, uint32_t ldx, float eps);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SH_OPS_H */

@@ -1,0 +1,388 @@
+// Fused multi-head attention (reference runtime/sh_attention.inc.c:55-243, semantics of
+// tests/gvsoc/run.py:921-934): o_h = softmax(scale * q_h k_h^T) v_h, head h = columns [h*dh, (h+1)*dh).
+//
+// Flash-style on gfx950: a 256-thread workgroup owns 128 queries of one (sequence, head); each wavefront
+// owns 32 of them and walks the keys in blocks of 64 with an online softmax (running max m and sum l per
+// query), so the S x S scores never leave the CU and S is unbounded.
+//  - Scores are computed transposed, S^T[key, q] = K . Q^T, with v_mfma_f32_32x32x16_f16: A = K rows
+//    (64 keys as two 32-row tiles, dh contiguous, staged in LDS), B = Q^T (each lane keeps its query's
+//    dh values in registers for the whole kernel). The accumulator then gives every lane 16 keys of one
+//    query per tile, so max / sum statistics are lane-local plus one exchange with lane ^ 32.
+//  - O^T[d, q] = V^T . P^T: the softmax numerators P (fp16) are the B operand straight from the score
+//    accumulators; V is transposed into LDS (8 x 8 register transposes) with its keys stored in the order
+//    that matches the accumulator layout (within 16 keys: 0-3, 8-11, 4-7, 12-15), so every MFMA operand is
+//    one 16-byte LDS read.
+//  - K/V blocks are double-buffered in LDS; the next block is loaded from HBM while the current one is used.
+//  - exp is 2^(c s - m) with c = scale * log2(e) on the hardware exp2; O is normalised by 1/l at the end,
+//    staged in LDS and written as 16-byte row chunks.
+// Heads with dh <= 128 use this kernel (dh padded to 64 or 128 with zeros); wider heads use a simple
+// per-query kernel.
+#include "sh_common.h"
+#include <chrono>
+
+namespace {
+
+constexpr int KB = 64;           // keys per block
+constexpr int QPW = 32;          // queries per wavefront
+constexpr int QPB = 128;         // queries per workgroup
+
+struct AttnArgs {
+    const uint16_t *q, *k, *v;
+    uint16_t *o;
+    uint64_t ldq, ldk, ldv, ldo;
+    uint64_t bsq, bsk, bsv, bso;    // batch strides (elements)
+    uint32_t S, dh;
+    float c;                        // scale * log2(e)
+};
+
+template <int DH>
+__device__ __forceinline__ uint32_t kswz(uint32_t r) {
+    if (DH == 128) return r & 15u;
+    return (r ^ (r >> 3)) & 7u;
+}
+__device__ __forceinline__ uint32_t vswz(uint32_t r) { return (r ^ (r >> 3)) & 7u; }
+__device__ __forceinline__ uint32_t comp4(const uint4 &q, int i) { return i == 0 ? q.x : i == 1 ? q.y : i == 2 ? q.z : q.w; }
+
+// 8 halves of row r starting at column c of a [*, ld] matrix; zero outside rows < rmax, cols < cmax.
+template <bool VEC>
+__device__ __forceinline__ uint4 ld8(const uint16_t *p, uint64_t ld, uint32_t r, uint32_t c, uint32_t rmax, uint32_t cmax) {
+    if (VEC) {
+        if (r < rmax && c < cmax) return *(const uint4 *)(p + (uint64_t)r * ld + c);
+        return make_uint4(0, 0, 0, 0);
+    }
+    uint32_t h[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = (r < rmax && c + e < cmax) ? p[(uint64_t)r * ld + c + e] : 0u;
+    return make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+}
+
+template <int DH, bool VEC>
+__global__ __launch_bounds__(256) void k_flash(AttnArgs a) {
+    constexpr int DC = DH / 8;                 // 16-byte chunks per K row
+    constexpr int NS = DH / 16;                // QK k-substeps
+    constexpr int DT = DH / 32;                // O^T row tiles
+    constexpr int K_PER_T = KB * DC / 256;     // K chunks per thread per block
+    constexpr int K_ELEMS = KB * DC;           // uint4 per K stage
+    constexpr int V_ELEMS = DH * 8;            // uint4 per V^T stage (DH rows x 8 chunks)
+    __shared__ uint4 smem[2 * (K_ELEMS + V_ELEMS)];
+
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = lane >> 5, r32 = lane & 31;
+    const uint32_t b = blockIdx.z, h = blockIdx.y;
+    const uint32_t S = a.S, dh = a.dh;
+    const uint16_t *Q = a.q + b * a.bsq + (uint64_t)h * dh;
+    const uint16_t *Kp = a.k + b * a.bsk + (uint64_t)h * dh;
+    const uint16_t *Vp = a.v + b * a.bsv + (uint64_t)h * dh;
+    uint16_t *O = a.o + b * a.bso + (uint64_t)h * dh;
+    const uint32_t qw0 = blockIdx.x * QPB + wave * QPW;    // first query of this wavefront
+    const uint32_t myq = qw0 + r32;
+
+    // Q^T operand: substep s, lane group g -> dh [16 s + 8 g, +8)
+    sh_h8 qf[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) qf[s] = __builtin_bit_cast(sh_h8, ld8<VEC>(Q, a.ldq, myq, 16 * s + 8 * g, S, dh));
+
+    sh_f16v oacc[DT];
+#pragma unroll
+    for (int i = 0; i < DT; ++i) oacc[i] = sh_f16v{};
+    float m_run = -INFINITY, l_run = 0.f;
+
+    uint4 rk[K_PER_T], rv[8];
+    const bool vload = t < DH;                 // V: one (8 keys x 8 dh) block per thread
+    const int vkc = t & 7, vdc = t >> 3;
+    const uint32_t nkb = (S + KB - 1) / KB;
+
+    auto gload = [&](uint32_t kb) {
+        const uint32_t k0 = kb * KB;
+#pragma unroll
+        for (int i = 0; i < K_PER_T; ++i) {
+            const int c = t + 256 * i, key = c / DC, kc = c % DC;
+            rk[i] = ld8<VEC>(Kp, a.ldk, k0 + key, 8 * kc, S, dh);
+        }
+        if (vload) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {      // key-chunk vkc = 2 * b16 + gg holds keys 16 b16 + 4 gg + {0..3, 8..11}
+                const int key = 16 * (vkc >> 1) + 4 * (vkc & 1) + (i & 3) + 8 * (i >> 2);
+                rv[i] = ld8<VEC>(Vp, a.ldv, k0 + key, 8 * vdc, S, dh);
+            }
+        }
+    };
+    auto sstore = [&](int st) {
+        uint4 *sk = smem + st * (K_ELEMS + V_ELEMS);
+        uint4 *sv = sk + K_ELEMS;
+#pragma unroll
+        for (int i = 0; i < K_PER_T; ++i) {
+            const int c = t + 256 * i, key = c / DC, kc = c % DC;
+            sk[key * DC + (kc ^ kswz<DH>(key))] = rk[i];
+        }
+        if (vload) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {      // V^T row d = 8 vdc + j: column j of the 8 loaded rows
+                uint32_t o4[4];
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    const uint32_t lo = comp4(rv[2 * p], j >> 1), hi = comp4(rv[2 * p + 1], j >> 1);
+                    o4[p] = (j & 1) ? ((lo >> 16) | (hi & 0xFFFF0000u)) : ((lo & 0xFFFFu) | (hi << 16));
+                }
+                const int d = 8 * vdc + j;
+                sv[d * 8 + (vkc ^ vswz(d))] = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+            }
+        }
+    };
+
+    if (nkb > 0) {
+        gload(0);
+        sstore(0);
+    }
+    __syncthreads();
+    for (uint32_t kb = 0; kb < nkb; ++kb) {
+        const int st = kb & 1;
+        if (kb + 1 < nkb) gload(kb + 1);
+        const uint4 *sk = smem + st * (K_ELEMS + V_ELEMS);
+        const uint4 *sv = sk + K_ELEMS;
+
+        // S^T tiles: keys [32 tt, 32 tt + 32) of this block x this wavefront's 32 queries
+        sh_f16v sacc[2];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            sacc[tt] = sh_f16v{};
+            const uint32_t key = 32 * tt + r32;
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const sh_h8 kf = __builtin_bit_cast(sh_h8, sk[key * DC + ((2 * s + g) ^ kswz<DH>(key))]);
+                sacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], sacc[tt], 0, 0, 0);
+            }
+        }
+        // lane (q, g) holds key 64 kb + 32 tt + 8 (r / 4) + 4 g + r % 4 in sacc[tt][r]
+        const bool masked = (kb + 1) * KB > S;   // last block of a ragged S: keys >= S take no weight
+        if (masked) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (kb * KB + 32 * tt + 8 * (r >> 2) + 4 * g + (r & 3) >= S) sacc[tt][r] = a.c >= 0.f ? -INFINITY : INFINITY;
+        }
+        float mb;
+        if (a.c >= 0.f) {
+            mb = -INFINITY;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mb = fmaxf(mb, sacc[tt][r]);
+            mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+        } else {
+            mb = INFINITY;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mb = fminf(mb, sacc[tt][r]);
+            mb = fminf(mb, __shfl_xor(mb, 32, 64));
+        }
+        const float m_new = fmaxf(m_run, a.c * mb);
+        const float alpha = sh_fast_exp2(m_run - m_new);
+        m_run = m_new;
+        float psum = 0.f;
+        sh_h8 pf[4];                           // P^T operand of PV substep s' (keys [16 s', 16 s' + 16))
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float p = sh_fast_exp2(fmaf(sacc[tt][r], a.c, -m_new));
+                if (masked && kb * KB + 32 * tt + 8 * (r >> 2) + 4 * g + (r & 3) >= S) p = 0.f;
+                psum += p;
+                pf[2 * tt + (r >> 3)][r & 7] = (_Float16)p;
+            }
+        l_run = l_run * alpha + psum;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const uint32_t d = 32 * dt + r32;
+#pragma unroll
+            for (int sp = 0; sp < 4; ++sp) {
+                const sh_h8 vf = __builtin_bit_cast(sh_h8, sv[d * 8 + ((2 * sp + g) ^ vswz(d))]);
+                oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[sp], oacc[dt], 0, 0, 0);
+            }
+        }
+        if (kb + 1 < nkb) sstore((kb + 1) & 1);
+        __syncthreads();
+    }
+
+    // normalise and write: lane (q, g) holds O[q][32 dt + 8 (r / 4) + 4 g + r % 4] in oacc[dt][r]
+    const float l = l_run + __shfl_xor(l_run, 32, 64);
+    const float inv = 1.f / l;
+    uint16_t *so = (uint16_t *)smem + wave * (QPW * DH);     // [32 q][DH] per wavefront, chunk c at c ^ (q & 7)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const int d0 = 32 * dt + 8 * rb + 4 * g;
+            const uint32_t lo = (uint32_t)sh_dev_f2h(oacc[dt][4 * rb] * inv) | ((uint32_t)sh_dev_f2h(oacc[dt][4 * rb + 1] * inv) << 16);
+            const uint32_t hi = (uint32_t)sh_dev_f2h(oacc[dt][4 * rb + 2] * inv) | ((uint32_t)sh_dev_f2h(oacc[dt][4 * rb + 3] * inv) << 16);
+            const int ch = (d0 >> 3) ^ (r32 & 7);
+            *(uint2 *)(so + r32 * DH + ch * 8 + (d0 & 7)) = make_uint2(lo, hi);
+        }
+    __syncthreads();
+    for (int c = lane; c < QPW * DC; c += 64) {
+        const int row = c / DC, ch = c % DC;
+        const uint32_t qq = qw0 + row, col = 8 * ch;
+        if (qq >= S || col >= dh) continue;
+        const uint4 val = ((const uint4 *)so)[row * DC + (ch ^ (row & 7))];
+        if (VEC) {
+            *(uint4 *)(O + (uint64_t)qq * a.ldo + col) = val;
+        } else {
+            for (int e = 0; e < 8 && col + e < dh; ++e) O[(uint64_t)qq * a.ldo + col + e] = (uint16_t)(comp4(val, e >> 1) >> (16 * (e & 1)));
+        }
+    }
+}
+
+// Any dh: one 256-thread block per (query, head, sequence); scores of the row in LDS (S <= 16384).
+__global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
+    extern __shared__ float sc[];
+    __shared__ float red[4];
+    const uint32_t qi = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const uint16_t *Q = a.q + b * a.bsq + (uint64_t)h * a.dh + (uint64_t)qi * a.ldq;
+    const uint16_t *Kp = a.k + b * a.bsk + (uint64_t)h * a.dh;
+    const uint16_t *Vp = a.v + b * a.bsv + (uint64_t)h * a.dh;
+    uint16_t *O = a.o + b * a.bso + (uint64_t)h * a.dh + (uint64_t)qi * a.ldo;
+    float mx = -INFINITY;
+    for (uint32_t j = threadIdx.x; j < a.S; j += 256) {
+        float s = 0.f;
+        for (uint32_t d = 0; d < a.dh; ++d) s += sh_dev_h2f(Q[d]) * sh_dev_h2f(Kp[(uint64_t)j * a.ldk + d]);
+        s *= a.c;
+        sc[j] = s;
+        mx = fmaxf(mx, s);
+    }
+    mx = sh_wave_max(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float sum = 0.f;
+    for (uint32_t j = threadIdx.x; j < a.S; j += 256) { const float p = sh_fast_exp2(sc[j] - mx); sc[j] = p; sum += p; }
+    sum = sh_wave_sum(sum);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sum;
+    __syncthreads();
+    const float inv = 1.f / (red[0] + red[1] + red[2] + red[3]);
+    for (uint32_t d = threadIdx.x; d < a.dh; d += 256) {
+        float acc = 0.f;
+        for (uint32_t j = 0; j < a.S; ++j) acc += sc[j] * sh_dev_h2f(Vp[(uint64_t)j * a.ldv + d]);
+        O[d] = sh_dev_f2h(acc * inv);
+    }
+}
+
+// ---- host side ---------------------------------------------------------------------------------------
+struct AttnProfile { hipEvent_t e0 = nullptr, e1 = nullptr; bool valid = false; uint32_t entry_ns = 0; };
+AttnProfile g_prof;
+
+uint32_t l1_bytes_q(uint32_t S, uint32_t dh, uint32_t sq) {     // sh_attention.inc.c:43-51 (uint32 arithmetic)
+    const uint32_t kb = S * dh * 2, qb = sq * dh * 2, sb = sq * S * 2;
+    return 0x1000u + qb + kb + kb + sb + kb + qb + sq * 4 + 8 * 4;
+}
+
+int check_ref(uint32_t S, uint32_t dh, uint32_t sq) {          // sh_attention.inc.c:198-205
+    if ((S & 3) || (dh & 3) || sq == 0 || (sq & 3) || S % sq || l1_bytes_q(S, dh, sq) > SH_REF_TCDM_BYTES) {
+        sh_set_error(-1, "[sh_attention] S=%u dh=%u sq=%u: need S %% 4 == 0, dh %% 4 == 0, sq | S, sq %% 4 == 0, L1 %u <= %u",
+                     S, dh, sq, l1_bytes_q(S, dh, sq ? sq : 1), SH_REF_TCDM_BYTES);
+        return -1;
+    }
+    return 0;
+}
+
+int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, uint32_t dh, uint32_t H,
+        uint32_t ldq, uint32_t ldk, uint32_t ldv, uint32_t ldo, uint64_t bsq, uint64_t bsk, uint64_t bsv, uint64_t bso, float scale) {
+    if (!q || !k || !v || !o) { sh_set_error(-1, "[sh_attention] NULL tensor address"); return -1; }
+    if (B == 0 || S == 0 || H == 0 || dh == 0) return 0;
+    if (H > 65535 || B > 65535) { sh_set_error(-1, "[sh_attention] H=%u or B=%u above 65535", H, B); return -1; }
+    AttnArgs a{(const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)v, (uint16_t *)o,
+               ldq, ldk, ldv, ldo, bsq, bsk, bsv, bso, S, dh, scale * 1.4426950408889634f};
+    hipStream_t st = sh_stream();
+    if (!g_prof.e0) {
+        if (!sh_hip_ok(hipEventCreate(&g_prof.e0), "hipEventCreate") || !sh_hip_ok(hipEventCreate(&g_prof.e1), "hipEventCreate")) return SH_EHIP;
+    }
+    g_prof.entry_ns = 0;
+    (void)hipEventRecord(g_prof.e0, st);
+    const bool vec = dh % 8 == 0 && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 8 == 0 &&
+                     bsq % 8 == 0 && bsk % 8 == 0 && bsv % 8 == 0 && bso % 8 == 0 &&
+                     sh_aligned16(q) && sh_aligned16(k) && sh_aligned16(v) && sh_aligned16(o);
+    if (dh <= 128) {
+        const dim3 grid(sh_cdiv(S, QPB), H, B), block(256);
+        if (dh <= 64) {
+            if (vec) hipLaunchKernelGGL((k_flash<64, true>), grid, block, 0, st, a);
+            else hipLaunchKernelGGL((k_flash<64, false>), grid, block, 0, st, a);
+        } else {
+            if (vec) hipLaunchKernelGGL((k_flash<128, true>), grid, block, 0, st, a);
+            else hipLaunchKernelGGL((k_flash<128, false>), grid, block, 0, st, a);
+        }
+    } else {
+        if (S > 16384) { sh_set_error(-1, "[sh_attention] dh=%u > 128 supports S <= 16384", dh); return -1; }
+        static bool attr = false;
+        if (!attr) { (void)hipFuncSetAttribute((const void *)k_attn_rows, hipFuncAttributeMaxDynamicSharedMemorySize, 16384 * 4); attr = true; }
+        hipLaunchKernelGGL(k_attn_rows, dim3(S, H, B), dim3(256), S * sizeof(float), st, a);
+    }
+    if (!sh_launch_ok("sh_attention")) return SH_EHIP;
+    (void)hipEventRecord(g_prof.e1, st);
+    g_prof.valid = true;
+    return 0;
+}
+
+uint32_t q_block_rule(uint32_t S, uint32_t dh, uint32_t H, uint32_t P) {   // sh_attention.inc.c:55-65
+    const uint32_t cand[4] = {S, 256, 128, 64};
+    uint32_t best = 0, best_rows = 0;
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t sq = cand[i];
+        if (sq == 0 || sq > S || S % sq || sq % 4 || l1_bytes_q(S, dh, sq) > SH_REF_TCDM_BYTES) continue;
+        const uint32_t items = H * (S / sq), rows = ((items + P - 1) / P) * sq;
+        if (!best || rows < best_rows) { best = sq; best_rows = rows; }
+    }
+    return best;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint32_t sh_attention_l1_bytes_q(uint32_t S, uint32_t dh, uint32_t sq) { return l1_bytes_q(S, dh, sq ? sq : S); }
+uint32_t sh_attention_l1_bytes(uint32_t S, uint32_t dh) { return sh_attention_l1_bytes_q(S, dh, S); }
+uint32_t sh_attention_q_block(uint32_t S, uint32_t dh, uint32_t H, uint32_t P) { return q_block_rule(S, dh, H, P ? P : 1); }
+
+int sh_attention_head(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t S, uint32_t dh,
+                      uint32_t ldq, uint32_t ldk, uint32_t ldv, uint32_t ldo, float scale, uint32_t) {
+    const uint32_t sq = q_block_rule(S, dh, 1, 1);
+    if (check_ref(S, dh, sq)) return -1;
+    return run(q, k, v, o, 1, S, dh, 1, ldq, ldk, ldv, ldo, 0, 0, 0, 0, scale);
+}
+
+int sh_attention_q(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t S, uint32_t D, uint32_t H,
+                   uint32_t ldq, uint32_t ldk, uint32_t ldv, uint32_t ldo, float scale, uint32_t cluster, uint32_t sq) {
+    const uint32_t dh = H ? D / H : 0;
+    if (H == 0 || dh * H != D) { sh_set_error(-1, "[sh_attention] D=%u not divisible by H=%u", D, H); return -1; }
+    if (!sq) sq = q_block_rule(S, dh, H, cluster == SH_ALL ? 16 : 1);
+    if (check_ref(S, dh, sq)) return -1;
+    return run(q, k, v, o, 1, S, dh, H, ldq, ldk, ldv, ldo, 0, 0, 0, 0, scale);
+}
+
+int sh_attention(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t S, uint32_t D, uint32_t H,
+                 uint32_t ldq, uint32_t ldk, uint32_t ldv, uint32_t ldo, float scale, uint32_t cluster) {
+    return sh_attention_q(q, k, v, o, S, D, H, ldq, ldk, ldv, ldo, scale, cluster, 0);
+}
+
+int sh_attention_batched(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, uint32_t D, uint32_t H,
+                         uint32_t ldq, uint32_t ldk, uint32_t ldv, uint32_t ldo,
+                         uint64_t bsq, uint64_t bsk, uint64_t bsv, uint64_t bso, float scale, uint32_t sq) {
+    const uint32_t dh = H ? D / H : 0;
+    if (H == 0 || dh * H != D) { sh_set_error(-1, "[sh_attention_batched] D=%u not divisible by H=%u", D, H); return -1; }
+    if (sq && S % sq) { sh_set_error(-1, "[sh_attention_batched] sq=%u does not divide S=%u", sq, S); return -1; }
+    return run(q, k, v, o, B, S, dh, H, ldq, ldk, ldv, ldo, bsq, bsk, bsv, bso, scale);
+}
+
+uint32_t sh_attention_profile(uint32_t, uint32_t, uint32_t phase) {
+    if (!g_prof.valid) return 0;
+    phase &= 7;
+    if (phase != 6) return 0;      // entry (7), start (0) and the unsplit phases 1..5 read 0
+    if (hipEventSynchronize(g_prof.e1) != hipSuccess) return 0;
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, g_prof.e0, g_prof.e1) != hipSuccess) return 0;
+    return (uint32_t)((double)ms * 1e6 + 0.5);
+}
+
+}  // extern "C"

@@ -1,0 +1,83 @@
+// Internal declarations shared by the softhier-ops HIP sources (not part of the C ABI).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+#include "sh_ops.h"
+
+typedef _Float16 sh_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 sh_h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 sh_h2 __attribute__((ext_vector_type(2)));
+typedef float sh_f16v __attribute__((ext_vector_type(16)));
+typedef float sh_f4v __attribute__((ext_vector_type(4)));
+
+// The reference cluster's TCDM bytes (ARCH_CLUSTER_TCDM_SIZE, softhier_mlir/sim/gvsoc.py:56): every
+// budget check the reference makes is made against this number so calls fail here exactly when they fail there.
+#define SH_REF_TCDM_BYTES 0x100000u
+
+// ---- runtime services (sh_rt.hip) -------------------------------------------------------------------
+hipStream_t sh_stream();                       // the library stream (after sh_init)
+void sh_ensure_init();                         // sh_init() on first use
+int sh_num_cus();                              // compute units of the current device
+int sh_num_xcds();                             // XCDs (8 on MI355X); dispatch is round-robin over them
+// Record a failure: prints "[tag] message" on stderr once per call site and sets sh_last_error.
+void sh_set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// Check a HIP call; on failure records SH_EHIP and returns false.
+bool sh_hip_ok(hipError_t e, const char *what);
+// Check the last kernel launch.
+bool sh_launch_ok(const char *what);
+// Library-owned device workspace of at least `bytes` (grown on demand, freed at exit).
+void *sh_workspace(size_t bytes);
+
+// ---- device helpers ---------------------------------------------------------------------------------
+__device__ __forceinline__ float sh_dev_h2f(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+__device__ __forceinline__ uint16_t sh_dev_f2h(float f) {   // v_cvt_f16_f32: round to nearest even
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+__device__ __forceinline__ float sh_fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float sh_fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float sh_fast_rsq(float x) { return __builtin_amdgcn_rsqf(x); }
+
+// tanh-form GELU: 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3), written as x / (1 + e^{-2u})
+// = x / (1 + 2^{x (k0 + k1 x^2)}) with k0 = -2 sqrt(2/pi) log2(e), k1 = 0.044715 k0. The exponent is
+// clamped so 2^t stays finite (x / (1 + 2^126) is 0 to fp16 precision for every x that reaches it).
+#define SH_GELU_K0 (-2.3022082f)
+#define SH_GELU_K1 (-0.10294324f)
+__device__ __forceinline__ float sh_gelu_f(float x) {
+    float t = x * (SH_GELU_K0 + SH_GELU_K1 * x * x);
+    t = fminf(fmaxf(t, -126.f), 126.f);
+    return x * sh_fast_rcp(1.f + sh_fast_exp2(t));
+}
+
+__device__ __forceinline__ float sh_wave_sum(float v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float sh_wave_max(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+static inline bool sh_aligned16(uint64_t p) { return (p & 15u) == 0; }
+static inline uint32_t sh_cdiv(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
+
+// Division of a 32-bit index by a runtime-invariant divisor d >= 1 with one multiply-high (Granlund and
+// Montgomery, "Division by invariant integers using multiplication", 1994, fig. 4.1): with l = ceil(log2 d)
+// and m = floor(2^32 (2^l - d) / d) + 1, n / d = (t + ((n - t) >> 1)) >> (l - 1), t = mulhi(m, n), l >= 1.
+struct ShDiv { uint32_t d, mul, l; };
+static inline ShDiv sh_make_div(uint32_t d) {
+    ShDiv f{d, 0, 0};
+    if (d <= 1) return f;
+    uint32_t l = 0;
+    while ((1ull << l) < d) ++l;
+    f.l = l;
+    f.mul = (uint32_t)((((1ull << l) - d) << 32) / d + 1);
+    return f;
+}
+__device__ __forceinline__ uint32_t sh_div(uint32_t n, ShDiv f) {
+    if (f.d <= 1) return n;
+    const uint32_t t = __umulhi(n, f.mul);
+    return (t + ((n - t) >> 1)) >> (f.l - 1);
+}

@@ -1,0 +1,164 @@
+"""SigLIP-B/ViT pre-LN encoder layer as a sequence of softhier-ops calls (the caller side of the boundary).
+
+The op sequence is the reference's (softhier_mlir/frontend/siglip.py:133-168; the same calls a generated
+main.c makes, tests/gvsoc/siglip_layer/main.c:64-127), on B sequences stacked as [B*S, D] rows:
+
+    LN1 -> Q/K/V GEMM + bias -> 12-head attention -> out-proj GEMM + bias -> residual add -> LN2
+        -> FFN-up GEMM + bias -> GELU -> FFN-down GEMM + bias -> residual add
+
+`sequence="reference"` issues exactly those library calls (sh_layernorm, sh_gemm, sh_add_bias, sh_attention per
+sequence, sh_add, sh_gelu). `sequence="fused"` computes the same layer with the additive entry points:
+one QKV GEMM against the concatenated [D, 3D] weight with the bias in its epilogue, one batched attention
+over q/k/v views of the QKV buffer (ld = 3D), and GEMM epilogues that add the bias, apply GELU or add the
+residual, which removes five row-op round trips through HBM. Both match the numpy oracle within the fp16
+tolerance (the fused epilogue rounds once where the reference rounds twice).
+
+Buffers are torch tensors (allocation only); every computation is a libshops.so call.
+"""
+from __future__ import annotations
+
+import contextlib
+import math
+from dataclasses import dataclass
+
+import torch
+
+from softhier_mlir_amd import shops
+
+PARAM_NAMES = ("wq", "wk", "wv", "wo", "w1", "w2", "bq", "bk", "bv", "bo", "b1", "b2", "g1", "be1", "g2", "be2")
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        code, msg = shops.last_error()
+        raise RuntimeError(f"{what} failed with {rc}: {msg}")
+
+
+@dataclass
+class LayerParams:
+    """fp16 device tensors of one layer; `wqkv` / `bqkv` are the concatenated Q|K|V weight and bias."""
+    t: dict
+
+    @classmethod
+    def from_host(cls, p: dict, device: str = "cuda") -> "LayerParams":
+        t = {nm: torch.as_tensor(p[nm]).to(device=device, dtype=torch.float16).contiguous() for nm in PARAM_NAMES}
+        t["wqkv"] = torch.cat([t["wq"], t["wk"], t["wv"]], dim=1).contiguous()
+        t["bqkv"] = torch.cat([t["bq"], t["bk"], t["bv"]], dim=1).contiguous()
+        return cls(t)
+
+    def __getitem__(self, k):
+        return self.t[k]
+
+
+class Encoder:
+    """Runs layers on a [B*S, D] fp16 activation buffer; scratch buffers are allocated once per (B, S)."""
+
+    def __init__(self, D: int = 768, F: int = 3072, H: int = 12, eps: float = 1e-6, device: str = "cuda"):
+        self.D, self.F, self.H, self.eps, self.device = D, F, H, eps, device
+        self.lib = shops.load()
+        self.lib.sh_init()
+        self._bufs: dict = {}
+        self.gemm_cfg = shops.cfg()          # tile hints 256^3 (library default), as the reference's default policy
+        self.tap = None                      # optional tap(name) -> context manager around each op (timing)
+
+    def _op(self, name: str):
+        return self.tap(name) if self.tap is not None else contextlib.nullcontext()
+
+    def buffers(self, rows: int) -> dict:
+        if self._bufs.get("rows") != rows:
+            z = lambda c: torch.empty((rows, c), dtype=torch.float16, device=self.device)  # noqa: E731
+            D, F = self.D, self.F
+            self._bufs = {"rows": rows, "ln1": z(D), "qkv": z(3 * D), "q": z(D), "k": z(D), "v": z(D), "o": z(D),
+                          "ao": z(D), "h": z(D), "ln2": z(D), "f1": z(F), "g": z(F), "f2": z(D)}
+        return self._bufs
+
+    # -- the reference's call sequence (siglip.py:133-168) ------------------------------------------------
+    def layer_reference(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int) -> torch.Tensor:
+        L, A = self.lib, shops.addr
+        D, F, H, rows = self.D, self.F, self.H, B * S
+        b = self.buffers(rows)
+        ALL = shops.SH_ALL
+        cfg = self.gemm_cfg
+        L.sh_layernorm(A(b["ln1"]), A(x), A(p["g1"]), A(p["be1"]), rows, D, D, self.eps, ALL)
+        for dst, w, bias in (("q", "wq", "bq"), ("k", "wk", "bk"), ("v", "wv", "bv")):
+            _check(L.sh_gemm(A(b["ln1"]), A(p[w]), A(b[dst]), rows, D, D, D, D, D, cfg, ALL), "sh_gemm " + dst)
+            L.sh_add_bias(A(b[dst]), A(b[dst]), A(p[bias]), rows, D, D, ALL)
+        scale = 1.0 / math.sqrt(D // H)
+        for s in range(B):                   # the reference has no batch: one sh_attention call per sequence
+            off = s * S * D
+            _check(L.sh_attention(A(b["q"], off), A(b["k"], off), A(b["v"], off), A(b["o"], off), S, D, H, D, D, D, D, scale, ALL),
+                   "sh_attention")
+        _check(L.sh_gemm(A(b["o"]), A(p["wo"]), A(b["ao"]), rows, D, D, D, D, D, cfg, ALL), "sh_gemm wo")
+        L.sh_add_bias(A(b["ao"]), A(b["ao"]), A(p["bo"]), rows, D, D, ALL)
+        L.sh_add(A(b["h"]), A(x), A(b["ao"]), rows, D, D, ALL)
+        L.sh_layernorm(A(b["ln2"]), A(b["h"]), A(p["g2"]), A(p["be2"]), rows, D, D, self.eps, ALL)
+        _check(L.sh_gemm(A(b["ln2"]), A(p["w1"]), A(b["f1"]), rows, F, D, D, F, F, cfg, ALL), "sh_gemm w1")
+        L.sh_add_bias(A(b["f1"]), A(b["f1"]), A(p["b1"]), rows, F, F, ALL)
+        L.sh_gelu(A(b["g"]), A(b["f1"]), rows, F, F, ALL)
+        _check(L.sh_gemm(A(b["g"]), A(p["w2"]), A(b["f2"]), rows, D, F, F, D, D, cfg, ALL), "sh_gemm w2")
+        L.sh_add_bias(A(b["f2"]), A(b["f2"]), A(p["b2"]), rows, D, D, ALL)
+        L.sh_add(A(out), A(b["h"]), A(b["f2"]), rows, D, D, ALL)
+        return out
+
+    # -- fused sequence (additive entry points) ------------------------------------------------------------
+    def layer_fused(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int) -> torch.Tensor:
+        L, A = self.lib, shops.addr
+        D, F, H, rows = self.D, self.F, self.H, B * S
+        b = self.buffers(rows)
+        cfg = self.gemm_cfg
+        D3 = 3 * D
+        with self._op("ln1"):
+            L.sh_layernorm(A(b["ln1"]), A(x), A(p["g1"]), A(p["be1"]), rows, D, D, self.eps, shops.SH_ALL)
+        with self._op("qkv"):
+            e = shops.epi(bias=A(p["bqkv"]))
+            _check(L.sh_gemm_ex(A(b["ln1"]), A(p["wqkv"]), A(b["qkv"]), rows, D3, D, D, D3, D3, cfg, e), "sh_gemm_ex qkv")
+        qkv = b["qkv"]
+        with self._op("attention"):
+            _check(L.sh_attention_batched(A(qkv), A(qkv, D), A(qkv, 2 * D), A(b["o"]), B, S, D, H, D3, D3, D3, D,
+                                          S * D3, S * D3, S * D3, S * D, 1.0 / math.sqrt(D // H), 0), "sh_attention_batched")
+        with self._op("out_proj"):
+            e = shops.epi(bias=A(p["bo"]), residual=A(x), ldr=D)
+            _check(L.sh_gemm_ex(A(b["o"]), A(p["wo"]), A(b["h"]), rows, D, D, D, D, D, cfg, e), "sh_gemm_ex wo")
+        with self._op("ln2"):
+            L.sh_layernorm(A(b["ln2"]), A(b["h"]), A(p["g2"]), A(p["be2"]), rows, D, D, self.eps, shops.SH_ALL)
+        with self._op("ffn_up"):
+            e = shops.epi(bias=A(p["b1"]), act=shops.SH_ACT_GELU)
+            _check(L.sh_gemm_ex(A(b["ln2"]), A(p["w1"]), A(b["g"]), rows, F, D, D, F, F, cfg, e), "sh_gemm_ex w1")
+        with self._op("ffn_down"):
+            e = shops.epi(bias=A(p["b2"]), residual=A(b["h"]), ldr=D)
+            _check(L.sh_gemm_ex(A(b["g"]), A(p["w2"]), A(out), rows, D, F, F, D, D, cfg, e), "sh_gemm_ex w2")
+        return out
+
+    @staticmethod
+    def op_costs(B: int, S: int, D: int = 768, F: int = 3072, H: int = 12) -> dict:
+        """Algorithmic FLOP and HBM bytes of each op of layer_fused (fp16 = 2 bytes; weights read once)."""
+        M = B * S
+        g = lambda m, n, k: 2 * m * n * k  # noqa: E731
+        return {
+            "ln1": {"flop": 0, "bytes": 2 * (2 * M * D + 2 * D)},
+            "qkv": {"flop": g(M, 3 * D, D), "bytes": 2 * (M * D + D * 3 * D + 3 * D + M * 3 * D)},
+            "attention": {"flop": 4 * B * H * S * S * (D // H), "bytes": 2 * 4 * M * D},
+            "out_proj": {"flop": g(M, D, D), "bytes": 2 * (M * D + D * D + D + 2 * M * D)},
+            "ln2": {"flop": 0, "bytes": 2 * (2 * M * D + 2 * D)},
+            "ffn_up": {"flop": g(M, F, D), "bytes": 2 * (M * D + D * F + F + M * F)},
+            "ffn_down": {"flop": g(M, D, F), "bytes": 2 * (M * F + F * D + D + 2 * M * D)},
+        }
+
+    def forward(self, x: torch.Tensor, params: list[LayerParams], B: int, S: int, sequence: str = "fused",
+                out: torch.Tensor | None = None) -> torch.Tensor:
+        """len(params) layers; layer l reads layer l-1's output (siglip.py:168). Returns the last output."""
+        step = self.layer_fused if sequence == "fused" else self.layer_reference
+        n = len(params)
+        out = out if out is not None else torch.empty_like(x)
+        tmp = torch.empty_like(x) if n > 1 else None
+        cur = x
+        for i, p in enumerate(params):          # ping-pong so that the last layer writes `out`
+            dst = out if (n - 1 - i) % 2 == 0 else tmp
+            step(cur, dst, p, B, S)
+            cur = dst
+        return out
+
+
+def flops_per_layer(B: int, S: int, D: int = 768, F: int = 3072) -> int:
+    """2 B (4 S D^2 + 2 S D F + 2 S^2 D) (reference tests/gvsoc/run.py:315, counted as 2 FLOP per MAC)."""
+    return 2 * B * (4 * S * D * D + 2 * S * D * F + 2 * S * S * D)

@@ -1,0 +1,117 @@
+"""The C ABI without a GPU: libshops.so loads, exports every function include/sh_ops.h declares, and its
+host-only functions (codec, budgets, q-block rule, argument validation) behave as the reference's."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from softhier_mlir_amd import shops
+
+
+def test_library_exports_every_header_function(lib):
+    names = shops.header_functions()
+    assert len(names) >= 55
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert missing == []
+    # every bound signature names a header function (no stale bindings)
+    assert set(shops._SIGS) | shops._UNTYPED <= set(names)
+
+
+def test_struct_layouts_match_the_reference():
+    assert C.sizeof(shops.sh_gemm_cfg) == 28            # 7 x uint32 (reference runtime/sh_ops.h:54-60)
+    assert [f for f, _ in shops.sh_gemm_cfg._fields_] == ["tm", "tn", "tk", "pipeline", "accumulate", "fmt", "l1_base"]
+    assert shops.SH_ALL == 0xFFFFFFFF
+
+
+def test_host_fp16_codec_exhaustive(lib):
+    h = np.arange(65536, dtype=np.uint16)
+    want = h.view(np.float16).astype(np.float32)
+    got = np.array([lib.sh_fp16_to_f32(int(v)) for v in h], np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    assert np.isnan(got[nan]).all()
+
+
+def test_host_fp16_encode(lib):
+    rng = np.random.default_rng(3)
+    u = rng.integers(0, 2 ** 32, 50_000, dtype=np.uint64).astype(np.uint32)
+    u[1::2] = (u[1::2] & 0x807FFFFF) | (((u[1::2] >> 8) % 40 + 100) << 23)
+    u[3::8] = (u[3::8] & ~np.uint32(0x1FFF)) | np.uint32(0x1000)          # ties at the rounding bit
+    f = u.view(np.float32)
+    f = f[~np.isnan(f)]
+    with np.errstate(over="ignore"):
+        want = f.astype(np.float16).view(np.uint16)
+    got = np.array([lib.sh_f32_to_fp16(float(v)) for v in f], np.uint16)
+    assert np.array_equal(got, want)
+    assert lib.sh_f32_to_fp16(float("nan")) == 0x7E00   # canonical quiet NaN (reference sh_rt.inc.c:47)
+
+
+def test_runtime_identity_functions(lib):
+    assert lib.sh_cluster_id() == 0 and lib.sh_core_id() == 0
+    assert lib.sh_is_first_core() == 1 and lib.sh_is_dm_core() == 1
+    assert lib.sh_num_clusters() == 1
+    assert lib.sh_l1_size() == 0x100000
+
+
+def test_gemm_l1_bytes_formula(lib):
+    # sh_gemm.inc.c:24-30: l1_base + (pipeline ? 2 : 1) * (tm tk + tk tn) * 2 + tm tn * 2, defaults 256
+    assert lib.sh_gemm_l1_bytes(256, 256, 256, None) == 2 * (2 * 256 * 256 * 2) + 256 * 256 * 2
+    c = shops.cfg(256, 256, 64, pipeline=1)
+    assert lib.sh_gemm_l1_bytes(256, 256, 64, c) == 2 * (256 * 64 * 2 + 64 * 256 * 2) + 256 * 256 * 2
+    c = shops.cfg(128, 64, 32, pipeline=0, l1_base=4096)
+    assert lib.sh_gemm_l1_bytes(1, 1, 1, c) == 4096 + (128 * 32 * 2 + 32 * 64 * 2) + 128 * 64 * 2
+
+
+def test_attention_budget_and_q_block_match_the_reference_log(lib):
+    # tests/gvsoc/attention/last_run.log: "l1=300064 B", "q block 64 rows: 48 work items" (S=256, dh=64, H=12, 16 clusters)
+    assert lib.sh_attention_l1_bytes(256, 64) == 300064
+    assert lib.sh_attention_q_block(256, 64, 12, 16) == 64
+    assert lib.sh_attention_q_block(256, 64, 1, 1) == 256
+    assert lib.sh_attention_q_block(1024, 64, 12, 16) == 256    # S=1024 fits with sq=256 (961 KB, sh_attention.inc.c:7)
+    assert lib.sh_attention_l1_bytes_q(1024, 64, 256) < 0x100000 < lib.sh_attention_l1_bytes_q(1024, 64, 1024)
+    assert lib.sh_attention_q_block(4096, 64, 12, 16) == 0      # nothing fits the reference TCDM
+
+
+def test_gemm_argument_errors_without_gpu(lib):
+    one = 1 << 20                                               # never dereferenced: validation fails first
+    assert lib.sh_gemm(one, one, one, 100, 256, 256, 256, 256, 256, None, shops.SH_ALL) == -1   # M % 256
+    assert shops.last_error()[0] == -1
+    c = shops.cfg(512, 512, 512)
+    assert lib.sh_gemm(one, one, one, 512, 512, 512, 512, 512, 512, c, 0) == -2                # TCDM budget
+    assert shops.last_error()[0] == -2
+    c = shops.cfg(256, 128, 256)
+    assert lib.sh_gemm_mesh(one, one, one, 1024, 1024, 1024, 1024, 1024, 1024, c) == -1         # tm != tn
+    c = shops.cfg(256, 256, 256)
+    assert lib.sh_gemm_mesh(one, one, one, 512, 512, 512, 512, 512, 512, c) == -1              # M != 4 tm
+    assert lib.sh_gemm(0, one, one, 256, 256, 256, 256, 256, 256, None, 0) == -1                # NULL
+    c = shops.cfg(fmt=shops.SH_FP8)
+    assert lib.sh_gemm(one, one, one, 256, 256, 256, 256, 256, 256, c, 0) == -1                # fp8 not implemented
+    e = shops.epi(residual=one, ldr=10)
+    assert lib.sh_gemm_ex(one, one, one, 16, 32, 16, 16, 32, 32, None, e) == -1                 # ldr < N
+
+
+def test_attention_argument_errors_without_gpu(lib):
+    one = 1 << 20
+    assert lib.sh_attention(one, one, one, one, 256, 768, 7, 768, 768, 768, 768, 0.125, shops.SH_ALL) == -1  # D % H
+    assert lib.sh_attention_q(one, one, one, one, 256, 768, 12, 768, 768, 768, 768, 0.125, 0, 96) == -1    # sq ∤ S
+    assert lib.sh_attention_q(one, one, one, one, 258, 768, 12, 768, 768, 768, 768, 0.125, 0, 0) == -1     # S % 4
+    assert lib.sh_attention_head(one, one, one, one, 4096, 64, 64, 64, 64, 64, 0.125, 0) == -1          # budget
+    assert lib.sh_attention_batched(one, one, one, one, 2, 256, 768, 5, 768, 768, 768, 768, 0, 0, 0, 0, 0.125, 0) == -1
+
+
+def test_rowop_argument_errors_without_gpu(lib):
+    lib.sh_last_error()
+    lib.sh_layernorm(0, 1 << 20, 1 << 20, 1 << 20, 4, 8, 8, 1e-6, 0)
+    assert shops.last_error()[0] == -1
+    lib.sh_transpose(1 << 20, 1 << 20, 4, 8, 4, 4, 0)           # ld_src < cols
+    assert shops.last_error()[0] == -1
+    lib.sh_add(1 << 20, 1 << 20, 1 << 20, 0, 8, 8, 0)           # zero rows: nothing to do, no error
+    assert shops.last_error()[0] == 0
+
+
+def test_capture_collects_library_text(lib):
+    with shops.capture() as cap:
+        lib.sh_printf(b"hello %d\n", C.c_int(7))
+    assert cap.text == "hello 7\n"

@@ -1,0 +1,122 @@
+"""Fused attention on the GPU: the reference's logged device outputs (tests/golden), the oracle on the
+BASELINE config-4 shapes (B=32 S=256 and B=8 S=1024, 12 heads of 64), QKV-buffer views (ld = 2304,
+attention_translate.mlir:23-25), ragged S, other head widths, element-wise paths and scale edge cases."""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from conftest import to_dev, to_np
+from oracle import lcg, refs
+from softhier_mlir_amd import data, shops
+
+pytestmark = pytest.mark.gpu
+A = shops.addr
+ALL = shops.SH_ALL
+GOLDEN = Path(__file__).resolve().parent / "golden" / "attention_s256_d768_h12.json"
+
+
+def _zeros(rows, cols):
+    import torch
+    return torch.zeros((rows, cols), dtype=torch.float16, device="cuda")
+
+
+def test_reference_log_through_the_library(lib, gpu):
+    """attention/main.c end to end on the GPU: inputs filled by sh_test_fill_fp16 (seeds 21/22/23), output
+    poisoned with 7.0 (seed 24), sh_attention_q(..., SH_ALL, 0), then the O0 / O sample dumps."""
+    S, D, H = 256, 768, 12
+    q, k, v, o = _zeros(S, D), _zeros(S, D), _zeros(S, D), _zeros(S, D)
+    lib.sh_test_fill_fp16(A(q), S, D, D, 21, -8, 8, 0.125)
+    lib.sh_test_fill_fp16(A(k), S, D, D, 22, -8, 8, 0.125)
+    lib.sh_test_fill_fp16(A(v), S, D, D, 23, -16, 16, 0.125)
+    lib.sh_test_fill_fp16(A(o), S, D, D, 24, 7, 7, 1.0)
+    assert lib.sh_attention_q(A(q), A(k), A(v), A(o), S, D, H, D, D, D, D, 0.125, ALL, 0) == 0, shops.last_error()
+    with shops.capture() as cap:
+        lib.sh_test_dump_samples(A(o), S, D // H, D, 301, 256, b"O0")
+        lib.sh_test_dump_samples(A(o), S, D, D, 302, 256, b"O")
+    got = lcg.parse_samples(cap.text)
+    fx = json.loads(GOLDEN.read_text())
+    ref = refs.attention_reference_lcg(S, D, H)
+    for tag, arr in (("O0", ref[:, :64]), ("O", ref)):
+        logged = [(r, c, float(np.array([int(h, 16)], np.uint16).view(np.float16)[0])) for r, c, h in fx["samples"][tag]]
+        assert [(r, c) for r, c, _ in got[tag]] == [(r, c) for r, c, _ in logged]
+        dev_ref = np.zeros_like(arr)
+        for r, c, val in logged:
+            dev_ref[r, c] = val
+        assert lcg.compare_samples(got[tag], dev_ref, 0.05, 0.05)[0] == 0      # vs the reference device, its tolerance
+        assert lcg.compare_samples(got[tag], arr, 2e-2, 1e-2)[0] == 0          # vs the oracle
+    bad, err, _ = refs.close(to_np(o), ref)
+    assert bad == 0, err
+
+
+def test_qkv_views_and_q_block(lib, gpu):
+    """q/k/v as column views of one [256 x 2304] QKV buffer (ld 2304), o with ld 768; q_block 64 and 0."""
+    S, D, H = 256, 768, 12
+    qkv = data.normal((S, 3 * D), 1)
+    QKV = to_dev(qkv)
+    for sq in (64, 0):
+        O = _zeros(S, D)
+        rc = lib.sh_attention_q(A(QKV), A(QKV, D), A(QKV, 2 * D), A(O), S, D, H, 3 * D, 3 * D, 3 * D, D, 0.125, ALL, sq)
+        assert rc == 0
+        want = refs.attention(qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:], H, 0.125)
+        bad, err, _ = refs.close(to_np(O), want)
+        assert bad == 0, err
+    O = _zeros(S, 64)
+    assert lib.sh_attention_head(A(QKV, 64), A(QKV, D + 64), A(QKV, 2 * D + 64), A(O), S, 64, 3 * D, 3 * D, 3 * D, 64, 0.125, 3) == 0
+    want = refs.attention(qkv[:, 64:128], qkv[:, D + 64:D + 128], qkv[:, 2 * D + 64:2 * D + 128], 1, 0.125)
+    assert refs.close(to_np(O), want)[0] == 0
+
+
+@pytest.mark.parametrize("B,S", [(32, 256), (8, 1024)])
+def test_baseline_config4_batched(lib, gpu, B, S):
+    D, H = 768, 12
+    q, k, v = data.normal((B * S, D), 11), data.normal((B * S, D), 12), data.normal((B * S, D), 13)
+    O = _zeros(B * S, D)
+    rc = lib.sh_attention_batched(A(to_dev(q)), A(to_dev(k)), A(to_dev(v)), A(O), B, S, D, H, D, D, D, D,
+                                  S * D, S * D, S * D, S * D, 0.125, 64)
+    assert rc == 0, shops.last_error()
+    want = refs.attention_batched(q, k, v, B, H, 0.125)
+    bad, err, _ = refs.close(to_np(O), want)
+    assert bad == 0, err
+
+
+@pytest.mark.parametrize("S,D,H", [(100, 128, 2), (260, 384, 6), (36, 96, 3), (512, 1536, 12), (64, 576, 12), (20, 72, 2)])
+def test_shapes_ragged_and_head_widths(lib, gpu, S, D, H):
+    """Ragged S (masked last key block), dh = 64 / 32 / 128 / 48 (padded) / 36 (element-wise path)."""
+    q, k, v = data.normal((S, D), S), data.normal((S, D), S + 1), data.normal((S, D), S + 2)
+    O = _zeros(S, D)
+    rc = lib.sh_attention_batched(A(to_dev(q)), A(to_dev(k)), A(to_dev(v)), A(O), 1, S, D, H, D, D, D, D, 0, 0, 0, 0, 0.125, 0)
+    assert rc == 0, shops.last_error()
+    bad, err, _ = refs.close(to_np(O), refs.attention(q, k, v, H, 0.125))
+    assert bad == 0, err
+
+
+def test_wide_heads_row_kernel(lib, gpu):
+    S, D, H = 96, 512, 2            # dh = 256 > 128: per-query kernel
+    q, k, v = data.normal((S, D), 5), data.normal((S, D), 6), data.normal((S, D), 7)
+    O = _zeros(S, D)
+    assert lib.sh_attention(A(to_dev(q)), A(to_dev(k)), A(to_dev(v)), A(O), S, D, H, D, D, D, D, 1 / 16, ALL) == 0
+    bad, err, _ = refs.close(to_np(O), refs.attention(q, k, v, H, 1 / 16))
+    assert bad == 0, err
+
+
+@pytest.mark.parametrize("scale", [-0.125, 0.0, 0.6])
+def test_scale_edge_cases(lib, gpu, scale):
+    S, D, H = 192, 256, 4
+    q, k, v = data.normal((S, D), 8), data.normal((S, D), 9), data.normal((S, D), 10)
+    O = _zeros(S, D)
+    assert lib.sh_attention(A(to_dev(q)), A(to_dev(k)), A(to_dev(v)), A(O), S, D, H, D, D, D, D, scale, ALL) == 0
+    bad, err, _ = refs.close(to_np(O), refs.attention(q, k, v, H, scale))
+    assert bad == 0, err
+
+
+def test_profile_reports_the_kernel_time(lib, gpu):
+    S, D, H = 256, 768, 12
+    q = to_dev(data.normal((S, D), 1))
+    O = _zeros(S, D)
+    assert lib.sh_attention(A(q), A(q), A(q), A(O), S, D, H, D, D, D, D, 0.125, ALL) == 0
+    lib.sh_barrier_global()
+    assert lib.sh_attention_profile(S, 64, 6) > lib.sh_attention_profile(S, 64, 7) == 0

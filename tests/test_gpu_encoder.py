@@ -1,0 +1,48 @@
+"""The SigLIP-B encoder layer through the library (softhier_mlir_amd.encoder) against the oracle: the
+reference's LCG layer (siglip_ref.py seeds, S=256) with both call sequences, BASELINE config 5 at B=32
+(1 layer) and a 12-layer stack."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import to_dev, to_np
+from oracle import refs
+from softhier_mlir_amd import data, encoder
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("sequence", ["reference", "fused"])
+def test_reference_lcg_layer(lib, gpu, sequence):
+    S, D, F, H = 256, 768, 3072, 12
+    p = refs.siglip_params_lcg(D, F)
+    x = refs.siglip_input_lcg(S, D)
+    enc = encoder.Encoder(D, F, H)
+    out = enc.forward(to_dev(x), [encoder.LayerParams.from_host(p)], B=1, S=S, sequence=sequence)
+    want = refs.encoder_layer(x, p, H)
+    bad, err, _ = refs.close(to_np(out), want)
+    assert bad == 0, err
+
+
+@pytest.mark.parametrize("sequence", ["fused", "reference"])
+def test_baseline_config5_b32(lib, gpu, sequence):
+    B, S, D, F, H = 32, 256, 768, 3072, 12
+    p = data.encoder_params(D, F, seed=100)
+    x = data.normal((B * S, D), 7)
+    enc = encoder.Encoder(D, F, H)
+    out = enc.forward(to_dev(x), [encoder.LayerParams.from_host(p)], B=B, S=S, sequence=sequence)
+    want = refs.encoder_layer(x, p, H, B=B)
+    bad, err, _ = refs.close(to_np(out), want)
+    assert bad == 0, err
+
+
+def test_twelve_layer_stack(lib, gpu):
+    B, S, D, F, H = 2, 256, 768, 3072, 12
+    ps = [data.encoder_params(D, F, seed=200 + 20 * i) for i in range(12)]
+    x = data.normal((B * S, D), 8)
+    enc = encoder.Encoder(D, F, H)
+    out = enc.forward(to_dev(x), [encoder.LayerParams.from_host(p) for p in ps], B=B, S=S, sequence="fused")
+    want = refs.encoder_stack(x, ps, H, B=B)
+    bad, err, _ = refs.close(to_np(out), want)
+    assert bad == 0, err

@@ -1,0 +1,242 @@
+"""sh_gemm / sh_gemm_splitk / sh_gemm_mesh / sh_gemm_ex on the GPU against the numpy oracle.
+
+Cases follow the reference's GEMM tests: run.py DEFAULT_GEMM shapes and fills (run.py:54-56, 87-93; small
+integers, exact), REAL_DATA fills (gemm/main.c:18-20), the gemm_seq pattern with strided head slices
+(gemm_seq/main.c:29-50), the SUMMA known answer (examples/gemm1024_summa.mlir:5), and the BASELINE config-1/2
+shapes. Tolerance for real-valued data: |got - want| <= 2e-2 + 1e-2 |want| against the fp32 product.
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+
+from conftest import codes, to_dev, to_np
+from oracle import lcg, refs
+from softhier_mlir_amd import data, shops
+
+pytestmark = pytest.mark.gpu
+A = shops.addr
+
+
+def _run_gemm(lib, x, w, z0=None, cfg=None, M=None, N=None, K=None, splits=None):
+    import torch
+    M, K = x.shape
+    N = w.shape[1]
+    X, W = to_dev(x), to_dev(w)
+    Z = to_dev(z0) if z0 is not None else torch.zeros((M, N), dtype=torch.float16, device="cuda")
+    if splits is None:
+        rc = lib.sh_gemm(A(X), A(W), A(Z), M, N, K, K, N, N, cfg, shops.SH_ALL)
+    else:
+        rc = lib.sh_gemm_splitk(A(X), A(W), A(Z), M, N, K, K, N, N, cfg, splits, shops.SH_ALL)
+    assert rc == 0, shops.last_error()
+    return X, W, Z
+
+
+def _parse(shape: str):
+    dims, _, rest = shape.partition(":")
+    M, N, K = (int(v) for v in dims.split("x"))
+    o = rest.split(",") if rest else []
+    tm, tn, tk = (int(v) for v in (o + ["0", "0", "0"])[:3])
+    pipe = int(o[3]) if len(o) > 3 else 1
+    acc = int(o[4]) if len(o) > 4 else 0
+    return M, N, K, shops.cfg(tm, tn, tk, pipe, acc), acc
+
+
+DEFAULT_GEMM = ["256x256x256", "256x768x192:256,256,192", "512x768x768:256,256,256", "256x256x256:256,256,256,0",
+                "256x256x512:256,256,256,1,1", "1024x768x768:256,256,256,1,0", "1024x3072x768:256,256,256,1,0"]
+
+
+@pytest.mark.parametrize("shape", DEFAULT_GEMM)
+def test_reference_default_shapes_exact(lib, gpu, shape):
+    M, N, K, cfg, acc = _parse(shape)
+    x = lcg.fill_fp16(M, K, 1, -1, 1)
+    w = lcg.fill_fp16(K, N, 2, -2, 2)
+    z0 = lcg.fill_fp16(M, N, 3, 3 if acc else 0, 3 if acc else 0)
+    X, W, Z = _run_gemm(lib, x, w, z0, cfg)
+    want = refs.gemm(x, w, z0 if acc else None)
+    assert np.array_equal(to_np(Z).astype(np.float32), want)          # integers below 2048: exact in fp16
+    with shops.capture() as cap:
+        bad = lib.sh_test_check_gemm(A(X), A(W), A(Z), M, N, K, K, N, N, 256, 0.5, 3.0 if acc else 0.0, b"[gemm]")
+    assert bad == 0 and "bad=0" in cap.text and "PASS" in cap.text
+
+
+def test_real_data_fills(lib, gpu):
+    M, N, K = 512, 768, 768
+    x = lcg.fill_fp16(M, K, 1, 0, 64, 1 / 4096)
+    w = lcg.fill_fp16(K, N, 2, -16, 16, 0.125)
+    _, _, Z = _run_gemm(lib, x, w)
+    bad, err, _ = refs.close(to_np(Z), refs.gemm(x, w))
+    assert bad == 0, err
+
+
+@pytest.mark.parametrize("cfg_index", range(6))
+def test_every_tile_config(lib, gpu, cfg_index, monkeypatch):
+    """Each compiled tile shape on a problem with partial tiles in M, N and a K tail (K % 64 != 0)."""
+    monkeypatch.setenv("SH_GEMM_CFG", str(cfg_index))
+    M, N, K = 328, 200, 136
+    x = data.normal((M, K), 11)
+    w = data.normal((K, N), 12, std=1 / np.sqrt(K))
+    import torch
+    X, W = to_dev(x), to_dev(w)
+    Z = torch.full((M + 3, 208), 7.0, dtype=torch.float16, device="cuda")           # ldz = 208 > N, poison
+    rc = lib.sh_gemm_ex(A(X), A(W), A(Z), M, N, K, K, N, 208, None, None)
+    assert rc == 0, shops.last_error()
+    z = to_np(Z)
+    bad, err, _ = refs.close(z[:M, :N], refs.gemm(x, w))
+    assert bad == 0, err
+    assert (z[:M, N:] == 7.0).all() and (z[M:] == 7.0).all()                       # nothing outside the view
+
+
+def test_scalar_path_unaligned_views(lib, gpu):
+    """Odd N and K, and operands starting one element into their buffers (no 16-byte alignment)."""
+    import torch
+    M, N, K = 70, 45, 37
+    x = data.normal((M, K + 1), 21)
+    w = data.normal((K + 1, N + 3), 22, std=0.2)
+    X, W = to_dev(x), to_dev(w)
+    Z = torch.zeros((M, N + 2), dtype=torch.float16, device="cuda")
+    rc = lib.sh_gemm_ex(A(X, 1), A(W, 1), A(Z, 1), M, N, K, K + 1, N + 3, N + 2, None, None)
+    assert rc == 0, shops.last_error()
+    want = refs.gemm(x[:, 1:], w[:K, 1:N + 1])
+    bad, err, _ = refs.close(to_np(Z)[:, 1:N + 1], want)
+    assert bad == 0, err
+
+
+def test_fused_epilogue_bias_gelu_residual(lib, gpu):
+    import torch
+    M, N, K = 384, 576, 320
+    x = data.normal((M, K), 31)
+    w = data.normal((K, N), 32, std=1 / np.sqrt(K))
+    b32 = (np.random.default_rng(33).random((1, N), dtype=np.float32) * 0.2 - 0.1)
+    r = data.normal((M, N), 34)
+    X, W, R = to_dev(x), to_dev(w), to_dev(r)
+    B32 = torch.from_numpy(b32).cuda()
+    Z = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    e = shops.epi(bias=A(B32), bias_fmt=shops.SH_BIAS_FP32, act=shops.SH_ACT_GELU, residual=A(R), ldr=N)
+    assert lib.sh_gemm_ex(A(X), A(W), A(Z), M, N, K, K, N, N, None, e) == 0, shops.last_error()
+    want = refs.r16(refs.gelu(refs.gemm(x, w) + b32)) + r.astype(np.float32)
+    bad, err, _ = refs.close(to_np(Z), want)
+    assert bad == 0, err
+    # residual aliasing the output (z = z + act(XW + b)), fp16 bias, split into 3
+    Z2 = to_dev(r)
+    B16 = to_dev(b32.astype(np.float16))
+    e = shops.epi(bias=A(B16), bias_fmt=shops.SH_BIAS_FP16, residual=A(Z2), ldr=N, splits=3)
+    assert lib.sh_gemm_ex(A(X), A(W), A(Z2), M, N, K, K, N, N, None, e) == 0, shops.last_error()
+    want = refs.gemm(x, w) + b32.astype(np.float16).astype(np.float32) + r.astype(np.float32)
+    bad, err, _ = refs.close(to_np(Z2), want)
+    assert bad == 0, err
+
+
+def test_splitk_matches_and_is_deterministic(lib, gpu):
+    """BASELINE config 2 FFN-down: M=256, K=3072, N=768, split-K = 4."""
+    M, N, K = 256, 768, 3072
+    x = data.uniform(M, K, 41)
+    w = (data.uniform(K, N, 42).astype(np.float32) / np.sqrt(K)).astype(np.float16)
+    _, _, Z1 = _run_gemm(lib, x, w, splits=4)
+    _, _, Z2 = _run_gemm(lib, x, w, splits=4)
+    _, _, Z0 = _run_gemm(lib, x, w, splits=1)
+    want = refs.gemm(x, w)
+    for Z in (Z1, Z0):
+        bad, err, _ = refs.close(to_np(Z), want)
+        assert bad == 0, err
+    assert np.array_equal(codes(Z1), codes(Z2))
+    # accumulate through split-K: Z = Z0 + XW
+    z0 = data.normal((M, N), 43)
+    _, _, Z3 = _run_gemm(lib, x, w, z0=z0, cfg=shops.cfg(accumulate=1), splits=3)
+    bad, err, _ = refs.close(to_np(Z3), want + z0.astype(np.float32))
+    assert bad == 0, err
+
+
+def test_mesh_known_answer_and_lcg(lib, gpu):
+    import torch
+    M = N = K = 1024
+    X = torch.ones((M, K), dtype=torch.float16, device="cuda")
+    W = torch.full((K, N), 1 / 1024, dtype=torch.float16, device="cuda")
+    Z = torch.zeros((M, N), dtype=torch.float16, device="cuda")
+    c = shops.cfg(256, 256, 256, 1, 0)
+    assert lib.sh_gemm_mesh(A(X), A(W), A(Z), M, N, K, K, N, N, c) == 0, shops.last_error()
+    assert (to_np(Z) == 1.0).all()                                   # examples/gemm1024_summa.mlir:5
+    x = data.uniform(M, K, 51)
+    w = (data.uniform(K, N, 52).astype(np.float32) / 32).astype(np.float16)
+    Xd, Wd = to_dev(x), to_dev(w)
+    assert lib.sh_gemm_mesh(A(Xd), A(Wd), A(Z), M, N, K, K, N, N, c) == 0
+    bad, err, _ = refs.close(to_np(Z), refs.gemm(x, w))
+    assert bad == 0, err
+
+
+def test_gemm_seq_strided_head_slices(lib, gpu):
+    """gemm_seq/main.c: mixed tiles back to back, 64-column head slices of 768-wide W/Z (ld = 768), and the
+    in-place softmax(P) . V slice on real data; the rest of the sliced Z keeps its poison."""
+    import torch
+    f = lcg.fill_fp16
+    xa, wa = f(256, 64, 1, -1, 1), f(64, 256, 2, -2, 2)
+    xb, wb = f(256, 256, 3, -1, 1), f(256, 64, 4, -2, 2)
+    xd, wd, zd = f(256, 256, 7, -1, 1), f(256, 768, 8, -2, 2), f(256, 768, 9, 7, 7)
+    xe, we = f(256, 256, 10, -32, 32, 0.125), f(256, 768, 11, -16, 16, 0.125)
+    Xa, Wa, Za = to_dev(xa), to_dev(wa), torch.zeros((256, 256), dtype=torch.float16, device="cuda")
+    Xb, Wb, Zb = to_dev(xb), to_dev(wb), torch.zeros((256, 64), dtype=torch.float16, device="cuda")
+    Xd, Wd, Zd = to_dev(xd), to_dev(wd), to_dev(zd)
+    Xe, We, Ze = to_dev(xe), to_dev(we), torch.zeros((256, 768), dtype=torch.float16, device="cuda")
+    a = shops.cfg(256, 256, 64, 1)
+    b = shops.cfg(256, 64, 256, 1)
+    lib.sh_softmax_rows(A(Xe), A(Xe), 256, 256, 256, 0.125, 0)
+    assert lib.sh_gemm(A(Xa), A(Wa), A(Za), 256, 256, 64, 64, 256, 256, a, 0) == 0
+    assert lib.sh_gemm(A(Xb), A(Wb), A(Zb), 256, 64, 256, 256, 64, 64, b, 0) == 0
+    assert lib.sh_gemm(A(Xd), A(Wd, 6 * 64), A(Zd, 6 * 64), 256, 64, 256, 256, 768, 768, b, 0) == 0
+    assert lib.sh_gemm(A(Xe), A(We), A(Ze), 256, 64, 256, 256, 768, 768, b, 0) == 0
+    assert np.array_equal(to_np(Za).astype(np.float32), refs.gemm(xa, wa))
+    assert np.array_equal(to_np(Zb).astype(np.float32), refs.gemm(xb, wb))
+    zd_got = to_np(Zd)
+    assert np.array_equal(zd_got[:, 384:448].astype(np.float32), refs.gemm(xd, wd[:, 384:448]))
+    assert (np.delete(zd_got, np.s_[384:448], axis=1) == 7.0).all()
+    p = refs.r16(refs.softmax(xe, 0.125))
+    bad, err, _ = refs.close(to_np(Ze)[:, :64], refs.gemm(p.astype(np.float16), we[:, :64]))
+    assert bad == 0, err
+    assert (to_np(Ze)[:, 64:] == 0).all()
+
+
+@pytest.mark.parametrize("M,N,K,epi", [(256, 2304, 768, "bias"), (256, 3072, 768, "bias_gelu"), (256, 768, 3072, "splitk4")])
+def test_baseline_config2_shapes(lib, gpu, M, N, K, epi):
+    import torch
+    x = data.uniform(M, K, 61)
+    w = (data.uniform(K, N, 62).astype(np.float32) / np.sqrt(K)).astype(np.float16)
+    b32 = (data.uniform(1, N, 63).astype(np.float32) * 0.1)
+    X, W = to_dev(x), to_dev(w)
+    Z = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    if epi == "splitk4":
+        assert lib.sh_gemm_splitk(A(X), A(W), A(Z), M, N, K, K, N, N, None, 4, shops.SH_ALL) == 0
+        want = refs.gemm(x, w)
+    else:
+        # library call sequence of the reference: sh_gemm then sh_add_bias (fp16 bias row) [then sh_gelu]
+        B16 = to_dev(b32.astype(np.float16))
+        assert lib.sh_gemm(A(X), A(W), A(Z), M, N, K, K, N, N, shops.cfg(256, 256, 256), shops.SH_ALL) == 0
+        lib.sh_add_bias(A(Z), A(Z), A(B16), M, N, N, shops.SH_ALL)
+        want = refs.r16(refs.gemm(x, w)) + b32.astype(np.float16).astype(np.float32)
+        if epi == "bias_gelu":
+            lib.sh_gelu(A(Z), A(Z), M, N, N, shops.SH_ALL)
+            want = refs.gelu(refs.r16(want))
+    bad, err, _ = refs.close(to_np(Z), want)
+    assert bad == 0, err
+
+
+def test_config1_single_gemm(lib, gpu):
+    x = data.uniform(256, 256, 1)
+    w = data.uniform(256, 256, 2)
+    _, _, Z = _run_gemm(lib, x, w)
+    bad, err, _ = refs.close(to_np(Z), refs.gemm(x, w))
+    assert bad == 0, err
+
+
+def test_large_encoder_shape_property(lib, gpu):
+    """M = 8192 (B = 32 rows of the encoder): a known-answer check at full size. W = I (identity blocks)
+    reproduces X exactly; a row-sum W gives each row's fp32 sum."""
+    import torch
+    M, K = 8192, 768
+    x = data.normal((M, K), 71)
+    X = to_dev(x)
+    I = torch.eye(K, dtype=torch.float16, device="cuda")
+    Z = torch.empty((M, K), dtype=torch.float16, device="cuda")
+    assert lib.sh_gemm(A(X), A(I), A(Z), M, K, K, K, K, K, None, shops.SH_ALL) == 0
+    assert np.array_equal(codes(Z), x.view(np.uint16))

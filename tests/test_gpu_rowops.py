@@ -1,0 +1,173 @@
+"""Row ops on the GPU against the oracle: the reference's rowops test (run.py:136-173 inputs and formulas,
+rowops/main.c op arguments), BASELINE config-3 shapes, strided views, the element-wise paths, rows wider than
+the register-resident kernels, in-place calls, and bit-exact transposes (NaN payloads included)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import codes, to_dev, to_np
+from oracle import lcg, refs
+from softhier_mlir_amd import data, shops
+
+pytestmark = pytest.mark.gpu
+A = shops.addr
+ALL = shops.SH_ALL
+
+
+def _empty(rows, cols, fill=7.0):
+    import torch
+    return torch.full((rows, cols), fill, dtype=torch.float16, device="cuda")
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 96), (256, 768), (33, 40)])
+def test_reference_rowops(lib, gpu, rows, cols):
+    """run.py run_rowops: LN eps 1e-5, softmax 0.5, gelu, add, add_bias (be row), scale 0.3, transpose."""
+    x = lcg.fill_fp16(rows, cols, 11, -16, 16, 0.125)
+    b = lcg.fill_fp16(rows, cols, 12, -16, 16, 0.125)
+    g = lcg.fill_fp16(1, cols, 13, 1, 8, 0.25)
+    be = lcg.fill_fp16(1, cols, 14, -4, 4, 0.25)
+    X, Bt, G, BE = to_dev(x), to_dev(b), to_dev(g), to_dev(be)
+    out = {k: _empty(rows, cols) for k in ("LN", "SM", "GELU", "ADD", "BIAS", "SCALE")}
+    T = _empty(cols, rows)
+    lib.sh_layernorm(A(out["LN"]), A(X), A(G), A(BE), rows, cols, cols, 1e-5, ALL)
+    lib.sh_softmax_rows(A(out["SM"]), A(X), rows, cols, cols, 0.5, ALL)
+    lib.sh_gelu(A(out["GELU"]), A(X), rows, cols, cols, ALL)
+    lib.sh_add(A(out["ADD"]), A(X), A(Bt), rows, cols, cols, ALL)
+    lib.sh_add_bias(A(out["BIAS"]), A(X), A(BE), rows, cols, cols, ALL)
+    lib.sh_scale(A(out["SCALE"]), A(X), rows, cols, cols, 0.3, ALL)
+    lib.sh_transpose(A(T), A(X), rows, cols, cols, rows, ALL)
+    want = {"LN": refs.layernorm(x, g, be, 1e-5), "SM": refs.softmax(x, 0.5), "GELU": refs.gelu(x),
+            "ADD": refs.add(x, b), "BIAS": refs.add_bias(x, be), "SCALE": refs.scale(x, 0.3)}
+    for k, w in want.items():
+        bad, err, _ = refs.close(to_np(out[k]), w)
+        assert bad == 0, (k, err)
+    assert np.array_equal(codes(T), refs.transpose(x.view(np.uint16)))
+    # the reference's sampled-dump comparison at its own tolerance (run.py:168)
+    with shops.capture() as cap:
+        lib.sh_test_dump_samples(A(out["LN"]), rows, cols, cols, 101, 64, b"LN")
+    s = lcg.parse_samples(cap.text)["LN"]
+    assert [(r, c) for r, c, _ in s] == lcg.sample_positions(rows, cols, 101, 64)
+    assert lcg.compare_samples(s, want["LN"], 2e-2, 2e-2)[0] == 0
+
+
+def test_baseline_config3(lib, gpu):
+    # layernorm [256 x 768], eps 1e-6, gamma ~ N(1, .02), beta ~ N(0, .02)
+    x = data.normal((256, 768), 1)
+    g, be = data.normal((1, 768), 2, 1.0, 0.02), data.normal((1, 768), 3, 0.0, 0.02)
+    Y = _empty(256, 768)
+    lib.sh_layernorm(A(Y), A(to_dev(x)), A(to_dev(g)), A(to_dev(be)), 256, 768, 768, 1e-6, ALL)
+    assert refs.close(to_np(Y), refs.layernorm(x, g, be, 1e-6))[0] == 0
+    # softmax over the last dim of [12 x 256 x 256], scale 1/8, x ~ N(0, 3)
+    s = data.normal((12 * 256, 256), 4, 0.0, 3.0)
+    Y = _empty(12 * 256, 256)
+    lib.sh_softmax_rows(A(Y), A(to_dev(s)), 12 * 256, 256, 256, 0.125, ALL)
+    assert refs.close(to_np(Y), refs.softmax(s, 0.125))[0] == 0
+    # tanh-GELU [256 x 3072]
+    f = data.normal((256, 3072), 5)
+    Y = _empty(256, 3072)
+    lib.sh_gelu(A(Y), A(to_dev(f)), 256, 3072, 3072, ALL)
+    assert refs.close(to_np(Y), refs.gelu(f))[0] == 0
+    # residual add and add_bias [256 x 768]
+    a, b, bias = data.normal((256, 768), 6), data.normal((256, 768), 7), data.normal((1, 768), 8)
+    Y = _empty(256, 768)
+    lib.sh_add(A(Y), A(to_dev(a)), A(to_dev(b)), 256, 768, 768, ALL)
+    assert refs.close(to_np(Y), refs.add(a, b))[0] == 0
+    lib.sh_add_bias(A(Y), A(to_dev(a)), A(to_dev(bias)), 256, 768, 768, ALL)
+    assert refs.close(to_np(Y), refs.add_bias(a, bias))[0] == 0
+    # transpose [768 x 256] taken from a strided view (a 768 x 256 block at column 128 of a 768 x 1024 buffer)
+    big = data.normal((768, 1024), 9)
+    Big = to_dev(big)
+    T = _empty(256, 800)                          # ld_dst = 800 > 768
+    lib.sh_transpose(A(T), A(Big, 128), 768, 256, 1024, 800, ALL)
+    t = codes(T)
+    assert np.array_equal(t[:, :768], big[:, 128:384].view(np.uint16).T)
+    assert (t[:, 768:] == np.float16(7.0).view(np.uint16)).all()
+
+
+def test_strided_views_and_in_place(lib, gpu):
+    """ld > cols on a 64-column head slice (loop_translate.mlir:33), and y == x (softmax in place, gemm_seq)."""
+    x = data.normal((256, 768), 11)
+    X = to_dev(x)
+    lib.sh_gelu(A(X, 128), A(X, 128), 256, 64, 768, ALL)
+    got = to_np(X)
+    assert refs.close(got[:, 128:192], refs.gelu(x[:, 128:192]))[0] == 0
+    assert np.array_equal(np.delete(got, np.s_[128:192], 1).view(np.uint16), np.delete(x, np.s_[128:192], 1).view(np.uint16))
+    s = data.normal((300, 256), 12, 0.0, 3.0)
+    S = to_dev(s)
+    lib.sh_softmax_rows(A(S), A(S), 300, 256, 256, 0.125, ALL)
+    assert refs.close(to_np(S), refs.softmax(s, 0.125))[0] == 0
+    n = data.normal((50, 768), 13)
+    N = to_dev(n)
+    g, be = data.normal((1, 768), 14, 1.0, 0.1), data.normal((1, 768), 15, 0.0, 0.1)
+    lib.sh_layernorm(A(N), A(N), A(to_dev(g)), A(to_dev(be)), 50, 768, 768, 1e-6, ALL)
+    assert refs.close(to_np(N), refs.layernorm(n, g, be, 1e-6))[0] == 0
+
+
+@pytest.mark.parametrize("cols", [77, 5, 520, 1100, 8192, 10000])
+def test_widths_and_elementwise_paths(lib, gpu, cols):
+    """cols % 8 != 0 (element-wise path), register-resident widths up to 8192, wider rows (loop kernel)."""
+    rows = 37
+    x = data.normal((rows, cols), cols, 0.0, 2.0)
+    g, be = data.normal((1, cols), 1, 1.0, 0.1), data.normal((1, cols), 2, 0.0, 0.1)
+    b = data.normal((rows, cols), 3)
+    X, G, BE, Bt = to_dev(x), to_dev(g), to_dev(be), to_dev(b)
+    Y = _empty(rows, cols)
+    lib.sh_layernorm(A(Y), A(X), A(G), A(BE), rows, cols, cols, 1e-6, ALL)
+    assert refs.close(to_np(Y), refs.layernorm(x, g, be, 1e-6))[0] == 0
+    lib.sh_softmax_rows(A(Y), A(X), rows, cols, cols, -0.7, ALL)
+    assert refs.close(to_np(Y), refs.softmax(x, -0.7))[0] == 0
+    lib.sh_add(A(Y), A(X), A(Bt), rows, cols, cols, ALL)
+    assert refs.close(to_np(Y), refs.add(x, b))[0] == 0
+    lib.sh_add_bias(A(Y), A(X), A(BE), rows, cols, cols, ALL)
+    assert refs.close(to_np(Y), refs.add_bias(x, be))[0] == 0
+    lib.sh_scale(A(Y), A(X), rows, cols, cols, -1.75, ALL)
+    assert refs.close(to_np(Y), refs.scale(x, -1.75))[0] == 0
+    lib.sh_gelu(A(Y), A(X), rows, cols, cols, ALL)
+    assert refs.close(to_np(Y), refs.gelu(x))[0] == 0
+
+
+def test_unaligned_base(lib, gpu):
+    """Views starting one element into the buffer (no 16-byte alignment) take the element-wise path."""
+    x = data.normal((20, 97), 21)
+    X = to_dev(x)
+    Y = _empty(20, 97)
+    g, be = np.ones((1, 97), np.float16), np.zeros((1, 97), np.float16)
+    G, BE = to_dev(g), to_dev(be)
+    lib.sh_layernorm(A(Y, 1), A(X, 1), A(G, 1), A(BE, 1), 20, 96, 97, 1e-6, ALL)
+    assert refs.close(to_np(Y)[:, 1:], refs.layernorm(x[:, 1:], g[:, 1:], be[:, 1:], 1e-6))[0] == 0
+    lib.sh_scale(A(Y, 1), A(X, 1), 20, 96, 97, 2.0, ALL)
+    assert refs.close(to_np(Y)[:, 1:], refs.scale(x[:, 1:], 2.0))[0] == 0
+
+
+@pytest.mark.parametrize("rows,cols", [(768, 256), (256, 768), (136, 264), (13, 29), (1, 1), (3000, 8)])
+def test_transpose_bit_exact(lib, gpu, rows, cols):
+    rng = np.random.default_rng(rows * 7 + cols)
+    c = rng.integers(0, 65536, (rows, cols), dtype=np.uint16)
+    c[::3, ::5] = 0x7C01 + (np.arange(c[::3, ::5].size).reshape(c[::3, ::5].shape) % 0x3FE).astype(np.uint16)  # NaN payloads
+    X = to_dev(c)
+    T = _empty(cols, rows)
+    lib.sh_transpose(A(T), A(X), rows, cols, cols, rows, ALL)
+    assert np.array_equal(codes(T), c.T)
+
+
+def test_large_rows_batched_hbm_shapes(lib, gpu):
+    """The ×32 batched shapes of the measured configuration, checked through exact invariants at full size:
+    LN of x and of (a x + b) agree (scale/shift invariance), softmax rows sum to 1, add is exact on integers."""
+    rows, cols = 8192, 768
+    x = data.normal((rows, cols), 31)
+    X = to_dev(x)
+    g, be = np.ones((1, cols), np.float16), np.zeros((1, cols), np.float16)
+    Y = _empty(rows, cols)
+    lib.sh_layernorm(A(Y), A(X), A(to_dev(g)), A(to_dev(be)), rows, cols, cols, 1e-6, ALL)
+    y = to_np(Y).astype(np.float32)
+    assert np.abs(y.mean(1)).max() < 2e-3 and np.abs(y.var(1) - 1).max() < 5e-3
+    sm = data.normal((12 * 256 * 32, 256), 32, 0.0, 3.0)
+    SM = to_dev(sm)
+    lib.sh_softmax_rows(A(SM), A(SM), sm.shape[0], 256, 256, 0.125, ALL)
+    p = to_np(SM).astype(np.float32)
+    assert np.abs(p.sum(1) - 1).max() < 2e-2 and (p >= 0).all()
+    ints = lcg.fill_fp16(rows, cols, 33, -512, 512)
+    I = to_dev(ints)
+    lib.sh_add(A(Y), A(I), A(I), rows, cols, cols, ALL)
+    assert np.array_equal(to_np(Y), (2 * ints.astype(np.float32)).astype(np.float16))
