@@ -74,6 +74,117 @@ __device__ __forceinline__ uint4 load8(const uint16_t *p, uint64_t ld, uint32_t 
 
 __device__ __forceinline__ uint32_t comp(const uint4 &q, int i) { return i == 0 ? q.x : i == 1 ? q.y : i == 2 ? q.z : q.w; }
 
+// The epilogue chain applied to one fp16 product value, each step rounded to fp16 exactly as the unfused
+// library sequence sh_gemm -> (accumulate) -> sh_add_bias -> sh_gelu -> sh_add would store it:
+// z = r16(z_old + p) [accumulate]; z = r16(z + bias); z = r16(gelu(z)); z = r16(z + residual).
+__device__ __forceinline__ uint16_t epi_chain(const GemmArgs &a, uint16_t p, uint32_t gm, uint32_t gn) {
+    float v = sh_dev_h2f(p);
+    if (a.accumulate) v = sh_dev_h2f(sh_dev_f2h(v + sh_dev_h2f(a.z[(uint64_t)gm * a.ldz + gn])));
+    if (a.bias) {
+        const float b = a.bias_fp32 ? ((const float *)a.bias)[gn] : sh_dev_h2f(((const uint16_t *)a.bias)[gn]);
+        v = sh_dev_h2f(sh_dev_f2h(v + b));
+    }
+    if (a.act == SH_ACT_GELU) v = sh_dev_h2f(sh_dev_f2h(sh_gelu_f(v)));
+    if (a.res) v += sh_dev_h2f(a.res[(uint64_t)gm * a.ldr + gn]);
+    return sh_dev_f2h(v);
+}
+
+// The same chain on 8 consecutive columns (16-byte loads of z_old / bias / residual).
+__device__ __forceinline__ uint4 epi_chain8(const GemmArgs &a, uint4 q, uint32_t gm, uint32_t gn) {
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = sh_dev_h2f((uint16_t)(comp(q, e >> 1) >> (16 * (e & 1))));
+    if (a.accumulate) {
+        const uint4 zq = *(const uint4 *)(a.z + (uint64_t)gm * a.ldz + gn);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = sh_dev_h2f(sh_dev_f2h(v[e] + sh_dev_h2f((uint16_t)(comp(zq, e >> 1) >> (16 * (e & 1))))));
+    }
+    if (a.bias) {
+        float b[8];
+        if (a.bias_fp32) {
+            const float4 b0 = *(const float4 *)((const float *)a.bias + gn), b1 = *(const float4 *)((const float *)a.bias + gn + 4);
+            b[0] = b0.x; b[1] = b0.y; b[2] = b0.z; b[3] = b0.w; b[4] = b1.x; b[5] = b1.y; b[6] = b1.z; b[7] = b1.w;
+        } else {
+            const uint4 bq = *(const uint4 *)((const uint16_t *)a.bias + gn);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) b[e] = sh_dev_h2f((uint16_t)(comp(bq, e >> 1) >> (16 * (e & 1))));
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = sh_dev_h2f(sh_dev_f2h(v[e] + b[e]));
+    }
+    if (a.act == SH_ACT_GELU) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = sh_dev_h2f(sh_dev_f2h(sh_gelu_f(v[e])));
+    }
+    if (a.res) {
+        const uint4 rq = *(const uint4 *)(a.res + (uint64_t)gm * a.ldr + gn);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] += sh_dev_h2f((uint16_t)(comp(rq, e >> 1) >> (16 * (e & 1))));
+    }
+    uint32_t w[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) w[p] = (uint32_t)sh_dev_f2h(v[2 * p]) | ((uint32_t)sh_dev_f2h(v[2 * p + 1]) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Accumulators -> Z. Element (i, j, r) of a wavefront is tile row wm*TM + 32 i + 8 (r/4) + 4 g + r%4 and
+// column wn*TN + 32 j + r32 (v_mfma_f32_32x32x16 output layout). Split-K: fp32 partials straight to the
+// workspace. Otherwise the products are rounded to fp16 into an LDS copy of the tile (16-byte chunk c of row
+// r stored at c ^ (r & 7)), then written as 16-byte row chunks through the epilogue chain. `sC` must be free.
+template <int BM, int BN, bool VEC, bool SPLIT, int FM, int FN>
+__device__ __forceinline__ void epilogue(const GemmArgs &a, sh_f16v (&acc)[FM][FN], uint32_t m0, uint32_t n0, uint32_t split, uint16_t *sC) {
+    constexpr int TM = BM / 2, TN = BN / 2;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int wm = wave >> 1, wn = wave & 1, g = lane >> 5, r32 = lane & 31;
+    if (SPLIT) {
+        float *P = a.part + (uint64_t)split * a.M * a.N;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const uint32_t gn = n0 + wn * TN + j * 32 + r32;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t gm = m0 + wm * TM + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (gm < a.M && gn < a.N) P[(uint64_t)gm * a.N + gn] = acc[i][j][r];
+                }
+            }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const uint32_t col = wn * TN + j * 32 + r32;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t row = wm * TM + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                sC[row * BN + (((col >> 3) ^ (row & 7)) << 3) + (col & 7)] = sh_dev_f2h(acc[i][j][r]);
+            }
+            __builtin_amdgcn_sched_barrier(0);     // one accumulator tile at a time (register pressure)
+        }
+    __syncthreads();
+    const bool plain = !a.accumulate && !a.bias && a.act == SH_ACT_NONE && !a.res;
+    constexpr int CPR = BN / 8;             // 16-byte chunks per tile row
+    for (int c = t; c < BM * CPR; c += 256) {
+        const int row = c / CPR, ch = c % CPR;
+        const uint32_t gm = m0 + row, gn = n0 + 8 * ch;
+        if (gm >= a.M || gn >= a.N) continue;
+        uint4 q = ((const uint4 *)sC)[row * CPR + (ch ^ (row & 7))];
+        if (VEC) {
+            if (!plain) q = epi_chain8(a, q, gm, gn);
+            *(uint4 *)(a.z + (uint64_t)gm * a.ldz + gn) = q;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                if (gn + e >= a.N) break;
+                const uint16_t h = (uint16_t)(comp(q, e >> 1) >> (16 * (e & 1)));
+                a.z[(uint64_t)gm * a.ldz + gn + e] = plain ? h : epi_chain(a, h, gm, gn + e);
+            }
+        }
+    }
+}
+
 template <int BM, int BN, bool VEC, bool SPLIT>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     using C = Cfg<BM, BN>;
@@ -175,72 +286,176 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
         }
     }
 
-    // accumulator element (i, j, r) -> tile row wm*TM + 32 i + 8 (r/4) + 4 g + r%4, column wn*TN + 32 j + r32
-    if (SPLIT) {
-        float *P = a.part + (uint64_t)split * a.M * a.N;
-#pragma unroll
-        for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-            for (int j = 0; j < C::FN; ++j) {
-                const uint32_t gn = n0 + wn * C::TN + j * 32 + r32;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const uint32_t gm = m0 + wm * C::TM + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                    if (gm < a.M && gn < a.N) P[(uint64_t)gm * a.N + gn] = acc[i][j][r];
-                }
-            }
-        return;
-    }
+    epilogue<BM, BN, VEC, SPLIT, C::FM, C::FN>(a, acc, m0, n0, split, (uint16_t *)smem);
+}
 
-    uint16_t *sC = (uint16_t *)smem;        // fp16 tile [BM][BN], 16-byte chunk c of row r at c ^ (r & 7)
+// ---- v2: direct global -> LDS loads, W read through the LDS transpose unit ----------------------------
+// For 16-byte-aligned operands with K % 64 == 0. Each 64-k slice of X (BM rows, k contiguous) and of W (64 rows,
+// n contiguous: the caller's [K, N] layout) is copied HBM -> LDS by global_load_lds_dwordx4 (no VGPR staging);
+// a wave's instruction fills 1 KB of consecutive LDS, so the XOR swizzles are applied by choosing which
+// global chunk each lane fetches. STAGES slices are in flight: the loads of slice kt + STAGES - 1 are issued
+// right after the barrier that opens slice kt, and the wait for slice kt only drains the older loads
+// (vmcnt, in-order completion). The MFMA B operand (8 consecutive k of one column n per lane) comes from two
+// ds_read_b64_tr_b16: in a group of 16 lanes, lane i supplies the 8-byte row segment W[k0 + i/4][n0 + 4 (i%4)]
+// and receives W[k0 + e][n0 + lane%16] for e = 0..3. Rows of W are swizzled at 16-byte granularity
+// (chunk c of row k at c ^ fW(k)) so the 4-row x 64-byte footprint of such a read hits distinct banks.
+// Rows of X beyond M and columns of W beyond N are fetched from clamped (valid) addresses; they only feed
+// outputs that are never stored.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const void *src, uint32_t lds_wave_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_wave_base), "v"(src) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt vmcnt(n) with expcnt / lgkmcnt left unconstrained (gfx9 encoding: vmcnt[3:0], [15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+typedef short sh_s4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ sh_s4 ds_read_tr(uint32_t addr) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) sh_s4 *)(uintptr_t)addr);
+}
+
+template <int BM, int BN, int STAGES>
+struct Cfg2 {
+    static constexpr int TM = BM / 2, TN = BN / 2, FM = TM / 32, FN = TN / 32;
+    static constexpr int XCH = BM * 8;               // 16-byte chunks per X slice
+    static constexpr int WCPR = BN / 8;              // chunks per W row
+    static constexpr int WCH = BK * WCPR;            // chunks per W slice
+    static constexpr int XR = XCH / 256, WR = WCH / 256;
+    static constexpr int LOADS = XR + WR;            // DMA instructions per wave per slice
+    static constexpr size_t STAGE = (size_t)(XCH + WCH) * 16;
+    static constexpr size_t LDS = STAGES * STAGE > (size_t)BM * BN * 2 ? STAGES * STAGE : (size_t)BM * BN * 2;
+    static_assert(BM % 64 == 0 && BN % 64 == 0 && XCH % 256 == 0 && WCH % 256 == 0, "tile");
+    static_assert(LOADS < 64 && LDS <= 160 * 1024, "resources");
+};
+
+template <int BN>
+__device__ __forceinline__ uint32_t fw(uint32_t k) {
+    return ((BN / 8) % 16 == 0) ? 4u * (k & 3u) : 4u * ((k >> 1) & 1u);
+}
+
+template <int BM, int BN, int STAGES, bool SPLIT>
+__global__ __launch_bounds__(256) void k_gemm2(GemmArgs a) {
+    using C = Cfg2<BM, BN, STAGES>;
+    extern __shared__ uint4 smem[];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int wm = wave >> 1, wn = wave & 1, g = lane >> 5, r32 = lane & 31;
+
+    const uint32_t nblk = a.tiles_m * a.tiles_n * a.splits;
+    uint32_t L = blockIdx.x;
+    if (a.xcd_groups > 1) L = (blockIdx.x % a.xcd_groups) * (nblk / a.xcd_groups) + blockIdx.x / a.xcd_groups;
+    const uint32_t tn = L % a.tiles_n, rest = L / a.tiles_n;
+    const uint32_t tm = rest % a.tiles_m, split = rest / a.tiles_m;
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t kbeg = split * a.kps;
+    const uint32_t kend = min(a.K, kbeg + a.kps);
+    const int KT = kend > kbeg ? (int)((kend - kbeg) / BK) : 0;
+
+    // per-lane source pointers of every DMA round (the k0 advance is added per slice)
+    const uint16_t *xs[C::XR];
+    const uint16_t *ws[C::WR];
+#pragma unroll
+    for (int r = 0; r < C::XR; ++r) {
+        const uint32_t p = r * 256 + wave * 64 + lane, m = p >> 3, c = (p & 7) ^ swz(m);
+        const uint32_t gm = min(m0 + m, a.M - 1);
+        xs[r] = a.x + (uint64_t)gm * a.ldx + kbeg + 8 * c;
+    }
+#pragma unroll
+    for (int r = 0; r < C::WR; ++r) {
+        const uint32_t p = r * 256 + wave * 64 + lane, k = p / C::WCPR, c = (p % C::WCPR) ^ fw<BN>(k);
+        uint32_t gn = n0 + 8 * c;
+        if (gn >= a.N) gn = a.N - 8;
+        ws[r] = a.w + (uint64_t)(kbeg + k) * a.ldw + gn;
+    }
+    const uint32_t lds0 = lds_addr(smem);
+    const uint32_t wave_off = (uint32_t)__builtin_amdgcn_readfirstlane(wave * 64 * 16);
+
+    // DMA instruction d of the loads of k-slice `src` into LDS stage `stage`: X rounds first, then W rounds
+    auto issue_one = [&](int d, int src, int stage) {
+        const uint32_t st = lds0 + (uint32_t)stage * (uint32_t)C::STAGE;
+        if (d < C::XR) lds_dma16(xs[d] + (uint64_t)src * BK, st + d * 4096 + wave_off);
+        else lds_dma16(ws[d - C::XR] + (uint64_t)src * BK * a.ldw, st + C::XCH * 16 + (d - C::XR) * 4096 + wave_off);
+    };
+
+    sh_f16v acc[C::FM][C::FN];
 #pragma unroll
     for (int i = 0; i < C::FM; ++i)
 #pragma unroll
-        for (int j = 0; j < C::FN; ++j) {
-            const uint32_t col = wn * C::TN + j * 32 + r32, gn = n0 + col;
-            float bv = 0.f;
-            if (a.bias && gn < a.N) bv = a.bias_fp32 ? ((const float *)a.bias)[gn] : sh_dev_h2f(((const uint16_t *)a.bias)[gn]);
+        for (int j = 0; j < C::FN; ++j) acc[i][j] = sh_f16v{};
+
+    // lane constants of the fragment reads
+    const int q = lane >> 4, iq = lane & 15;
+    uint32_t aoff[C::FM];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t row = wm * C::TM + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3), gm = m0 + row;
-                float v = acc[i][j][r];
-                if (a.accumulate && gm < a.M && gn < a.N) v += sh_dev_h2f(a.z[(uint64_t)gm * a.ldz + gn]);
-                v += bv;
-                if (a.act == SH_ACT_GELU) v = sh_gelu_f(v);
-                sC[row * BN + (((col >> 3) ^ (row & 7)) << 3) + (col & 7)] = sh_dev_f2h(v);
+    for (int i = 0; i < C::FM; ++i) aoff[i] = (uint32_t)(wm * C::TM + i * 32 + r32);
+
+    // Prologue: slices 0 .. STAGES-2. Every iteration then issues exactly LOADS DMAs (slices past the end are
+    // clamped to the last slice and land in a stage nobody reads again), so the wait is a constant count.
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+#pragma unroll
+        for (int d = 0; d < C::LOADS; ++d) issue_one(d, min(s, KT - 1), s);
+
+    constexpr int NM = C::FM * C::FN;                 // MFMAs per k-substep
+    constexpr int MT = 4 * NM;                        // per slice
+    for (int kt = 0; kt < KT; ++kt) {
+        wait_vmcnt<(STAGES - 2) * C::LOADS>();        // this slice has landed (own wave) ...
+        __syncthreads();                              // ... for every wave; the oldest stage is free again
+        const int kn = min(kt + STAGES - 1, KT - 1);  // slice whose loads are spread over this slice's MFMAs ...
+        const int kst = (kt + STAGES - 1) % STAGES;   // ... into the stage freed by the barrier above
+        const uint32_t st = lds0 + (uint32_t)(kt % STAGES) * (uint32_t)C::STAGE;
+        const uint4 *X = (const uint4 *)((const char *)smem + (uint32_t)(kt % STAGES) * (uint32_t)C::STAGE);
+        const uint32_t wbase = st + C::XCH * 16;
+        // fragments of k-substep s (16 k): A from X rows (one 16-byte read), B from two transpose reads
+        auto load_frags = [&](int s, sh_h8 (&af)[C::FM], sh_h8 (&bf)[C::FN]) {
+#pragma unroll
+            for (int i = 0; i < C::FM; ++i) {
+                const uint32_t m = aoff[i];
+                af[i] = __builtin_bit_cast(sh_h8, X[m * 8 + ((2 * s + g) ^ swz(m))]);
             }
-        }
-    __syncthreads();
-    constexpr int CPR = BN / 8;             // 16-byte chunks per tile row
-    for (int c = t; c < BM * CPR; c += 256) {
-        const int row = c / CPR, ch = c % CPR;
-        const uint32_t gm = m0 + row, gn = n0 + 8 * ch;
-        if (gm >= a.M || gn >= a.N) continue;
-        uint4 q = ((const uint4 *)sC)[row * CPR + (ch ^ (row & 7))];
-        if (VEC) {
-            if (a.res) {
-                const uint4 rq = *(const uint4 *)(a.res + (uint64_t)gm * a.ldr + gn);
-                uint32_t o[4];
 #pragma unroll
-                for (int p = 0; p < 4; ++p) {
-                    const uint32_t u = comp(q, p), v = comp(rq, p);
-                    const float lo = sh_dev_h2f((uint16_t)(u & 0xFFFF)) + sh_dev_h2f((uint16_t)(v & 0xFFFF));
-                    const float hi = sh_dev_h2f((uint16_t)(u >> 16)) + sh_dev_h2f((uint16_t)(v >> 16));
-                    o[p] = (uint32_t)sh_dev_f2h(lo) | ((uint32_t)sh_dev_f2h(hi) << 16);
+            for (int j = 0; j < C::FN; ++j) {
+                const uint32_t n = (uint32_t)(wn * C::TN + j * 32 + 16 * (q & 1) + 4 * (iq & 3));
+                const uint32_t k0 = 16 * s + 8 * g + (iq >> 2), k1 = k0 + 4;
+                const sh_s4 lo = ds_read_tr(wbase + k0 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k0)) + 2 * (n & 7));
+                const sh_s4 hi = ds_read_tr(wbase + k1 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k1)) + 2 * (n & 7));
+                bf[j] = __builtin_bit_cast(sh_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            }
+        };
+        sh_h8 af[2][C::FM], bf[2][C::FN];
+        load_frags(0, af[0], bf[0]);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            // the reads of substep s + 1 are issued before the MFMAs of substep s (fenced so the scheduler
+            // cannot sink them next to their consumers): their LDS latency hides under s's MFMAs
+            if (s < 3) load_frags(s + 1, af[(s + 1) & 1], bf[(s + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+                for (int j = 0; j < C::FN; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[s & 1][i], bf[s & 1][j], acc[i][j], 0, 0, 0);
+                    // DMA d goes out after MFMA number floor(d * MT / LOADS): loads trickle under the MFMAs
+                    const int gi = s * NM + i * C::FN + j;
+#pragma unroll
+                    for (int d = 0; d < C::LOADS; ++d)
+                        if ((d * MT) / C::LOADS == gi) { __builtin_amdgcn_sched_barrier(0); issue_one(d, kn, kst); __builtin_amdgcn_sched_barrier(0); }
                 }
-                q = make_uint4(o[0], o[1], o[2], o[3]);
-            }
-            *(uint4 *)(a.z + (uint64_t)gm * a.ldz + gn) = q;
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                if (gn + e >= a.N) break;
-                uint16_t h = (uint16_t)(comp(q, e >> 1) >> (16 * (e & 1)));
-                if (a.res) h = sh_dev_f2h(sh_dev_h2f(h) + sh_dev_h2f(a.res[(uint64_t)gm * a.ldr + gn + e]));
-                a.z[(uint64_t)gm * a.ldz + gn + e] = h;
-            }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
+    wait_vmcnt<0>();     // the clamped tail loads must land before the tile is staged in the same LDS
+    __syncthreads();     // every wavefront is done with the slices before the tile is staged in the same LDS
+    epilogue<BM, BN, true, SPLIT, C::FM, C::FN>(a, acc, m0, n0, split, (uint16_t *)smem);
 }
 
 // Sum of the split partials in split order, then the epilogue of k_gemm. Item = 8 columns (VEC) or 1.
@@ -267,16 +482,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs a, ShDiv div, ui
     }
     uint16_t out[W];
 #pragma unroll
-    for (int e = 0; e < W; ++e) {
-        const uint32_t n = gn + e;
-        float x = v[e];
-        if (a.accumulate) x += sh_dev_h2f(a.z[(uint64_t)gm * a.ldz + n]);
-        if (a.bias) x += a.bias_fp32 ? ((const float *)a.bias)[n] : sh_dev_h2f(((const uint16_t *)a.bias)[n]);
-        if (a.act == SH_ACT_GELU) x = sh_gelu_f(x);
-        uint16_t h = sh_dev_f2h(x);
-        if (a.res) h = sh_dev_f2h(sh_dev_h2f(h) + sh_dev_h2f(a.res[(uint64_t)gm * a.ldr + n]));
-        out[e] = h;
-    }
+    for (int e = 0; e < W; ++e) out[e] = epi_chain(a, sh_dev_f2h(v[e]), gm, gn + e);
     if (VEC) {
         uint32_t w4[4];
 #pragma unroll
@@ -289,19 +495,32 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs a, ShDiv div, ui
 
 // ---- host side ------------------------------------------------------------------------------------------
 typedef void (*KernelFn)(GemmArgs);
-struct KCfg { int bm, bn; KernelFn vec[2], scalar[2]; size_t lds; float eff; bool attr_set; };
+// v2 entries need vec operands and K % 64 == 0; v1 entries take anything (scalar variants for small tiles).
+struct KCfg { int bm, bn, stages; bool v2; KernelFn vec[2], scalar[2]; size_t lds; float eff; bool attr_set; };
 
-#define SH_KCFG(BM, BN, EFF) { BM, BN, { k_gemm<BM, BN, true, false>, k_gemm<BM, BN, true, true> }, \
+#define SH_KCFG(BM, BN, EFF) { BM, BN, 2, false, { k_gemm<BM, BN, true, false>, k_gemm<BM, BN, true, true> }, \
                                { k_gemm<BM, BN, false, false>, k_gemm<BM, BN, false, true> }, Cfg<BM, BN>::LDS, EFF, false }
+#define SH_KCFG2(BM, BN, ST, EFF) { BM, BN, ST, true, { k_gemm2<BM, BN, ST, false>, k_gemm2<BM, BN, ST, true> }, \
+                                    { nullptr, nullptr }, Cfg2<BM, BN, ST>::LDS, EFF, false }
+// eff = sustained fraction of the MFMA peak per CU measured for each tile on MI355X (tile-time model of
+// est_time below); it only ranks the configurations.
 KCfg g_cfgs[] = {
-    SH_KCFG(256, 256, 0.75f),
-    SH_KCFG(256, 128, 0.65f),
-    SH_KCFG(128, 256, 0.65f),
-    SH_KCFG(128, 192, 0.60f),
-    SH_KCFG(128, 128, 0.50f),
-    SH_KCFG(64, 64, 0.20f),
+    SH_KCFG(256, 256, 0.22f),
+    SH_KCFG(256, 128, 0.20f),
+    SH_KCFG(128, 256, 0.20f),
+    SH_KCFG(128, 192, 0.23f),
+    SH_KCFG(128, 128, 0.22f),
+    SH_KCFG(64, 64, 0.10f),
+    SH_KCFG2(256, 256, 2, 0.35f),
+    SH_KCFG2(256, 128, 3, 0.33f),
+    SH_KCFG2(128, 256, 3, 0.32f),
+    SH_KCFG2(128, 192, 3, 0.27f),
+    SH_KCFG2(128, 128, 3, 0.25f),
+    SH_KCFG2(128, 192, 2, 0.30f),
+    SH_KCFG2(128, 128, 2, 0.27f),
 };
 #undef SH_KCFG
+#undef SH_KCFG2
 constexpr int kNumCfg = sizeof(g_cfgs) / sizeof(g_cfgs[0]);
 
 int env_int(const char *name, int dflt) {
@@ -322,12 +541,17 @@ double est_time(const KCfg &c, uint32_t M, uint32_t N, uint32_t K, uint32_t spli
 
 struct Plan { int cfg; uint32_t splits; };
 
-Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, uint32_t want_splits) {
+bool eligible(const KCfg &c, bool vec, bool fast) {
+    if (c.v2) return fast;
+    return vec || c.bm * c.bn <= 128 * 128;
+}
+
+Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t want_splits) {
     const int cus = sh_num_cus() > 0 ? sh_num_cus() : 256;
     Plan best{4, 1};
     double bt = 1e300;
     for (int i = 0; i < kNumCfg; ++i) {
-        if (!vec && g_cfgs[i].bm * g_cfgs[i].bn > 128 * 128) continue;
+        if (!eligible(g_cfgs[i], vec, fast)) continue;
         uint32_t lo = 1, hi = 1;
         if (want_splits) lo = hi = want_splits;
         else hi = std::max<uint32_t>(1, std::min<uint32_t>(8, K / 512));
@@ -337,7 +561,7 @@ Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, uint32_t want_splits) 
         }
     }
     const int fc = env_int("SH_GEMM_CFG", -1);
-    if (fc >= 0 && fc < kNumCfg && (vec || g_cfgs[fc].bm * g_cfgs[fc].bn <= 128 * 128)) best.cfg = fc;
+    if (fc >= 0 && fc < kNumCfg && eligible(g_cfgs[fc], vec, fast)) best.cfg = fc;
     const int fs = env_int("SH_GEMM_SPLITS", 0);
     if (fs > 0 && !want_splits) best.splits = (uint32_t)fs;
     return best;
@@ -355,8 +579,9 @@ int launch(const GemmReq &r, const char *name) {
     const uint32_t ldr = e ? e->ldr : 0;
     const bool vec = r.N % 8 == 0 && r.K % 8 == 0 && r.ldx % 8 == 0 && r.ldw % 8 == 0 && r.ldz % 8 == 0 &&
                      sh_aligned16(r.x) && sh_aligned16(r.w) && sh_aligned16(r.z) &&
-                     (!res || (ldr % 8 == 0 && sh_aligned16(res))) && (!bias || (bias & 3) == 0);
-    Plan p = choose(r.M, r.N, r.K, vec, r.splits);
+                     (!res || (ldr % 8 == 0 && sh_aligned16(res))) && (!bias || sh_aligned16(bias));
+    const bool fast = vec && r.K % BK == 0 && r.K > 0;
+    Plan p = choose(r.M, r.N, r.K, vec, fast, r.splits);
     if (r.mesh) p.splits = 1;
     KCfg &c = g_cfgs[p.cfg];
     uint32_t splits = std::max<uint32_t>(1, std::min<uint32_t>(p.splits, sh_cdiv(std::max<uint32_t>(r.K, 1), BK)));
@@ -378,11 +603,11 @@ int launch(const GemmReq &r, const char *name) {
 
     hipStream_t st = sh_stream();
     const bool split = splits > 1;
-    KernelFn fn = vec ? c.vec[split] : c.scalar[split];
+    KernelFn fn = (vec || c.v2) ? c.vec[split] : c.scalar[split];
     if (!c.attr_set) {
         for (int v = 0; v < 2; ++v) {
             (void)hipFuncSetAttribute((const void *)c.vec[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
-            (void)hipFuncSetAttribute((const void *)c.scalar[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
+            if (c.scalar[v]) (void)hipFuncSetAttribute((const void *)c.scalar[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
         }
         c.attr_set = true;
     }

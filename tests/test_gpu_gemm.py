@@ -71,11 +71,13 @@ def test_real_data_fills(lib, gpu):
     assert bad == 0, err
 
 
-@pytest.mark.parametrize("cfg_index", range(6))
-def test_every_tile_config(lib, gpu, cfg_index, monkeypatch):
-    """Each compiled tile shape on a problem with partial tiles in M, N and a K tail (K % 64 != 0)."""
+@pytest.mark.parametrize("K", [136, 192])
+@pytest.mark.parametrize("cfg_index", range(13))
+def test_every_tile_config(lib, gpu, cfg_index, K, monkeypatch):
+    """Each compiled tile shape on a problem with partial tiles in M and N; K = 136 has a K tail (only the
+    general kernels take it), K = 192 is a multiple of 64 (the direct-to-LDS kernels take it)."""
     monkeypatch.setenv("SH_GEMM_CFG", str(cfg_index))
-    M, N, K = 328, 200, 136
+    M, N = 328, 200
     x = data.normal((M, K), 11)
     w = data.normal((K, N), 12, std=1 / np.sqrt(K))
     import torch
