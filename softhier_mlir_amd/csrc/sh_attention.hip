@@ -235,6 +235,191 @@ __global__ __launch_bounds__(256) void k_flash(AttnArgs a) {
     }
 }
 
+// ---- DMA variant (dh == 64 or 128, 16-byte aligned operands) ------------------------------------------
+// K and V key blocks are copied HBM -> LDS by global_load_lds_dwordx4 into a ring of NST stages (all four
+// blocks of an S = 256 head are requested before the first is used). K rows keep the A-operand layout of the
+// score MFMA; V stays in its natural [key][d] layout and the O^T MFMA reads its A operand (8 keys of one d per
+// lane) with two ds_read_b64_tr_b16: lane group g of a 16-key substep supplies keys 4g..4g+3 and 8+4g..8+4g+3,
+// the order in which the score accumulators hold P. Keys past S are fetched from row S-1 (valid memory) and
+// get zero weight.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void attn_dma16(const void *src, uint32_t lds_wave_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_wave_base), "v"(src) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+template <int N>
+__device__ __forceinline__ void attn_wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ uint32_t attn_lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+typedef short attn_s4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ attn_s4 attn_read_tr(uint32_t addr) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) attn_s4 *)(uintptr_t)addr);
+}
+// V rows are DC chunks wide; chunk c of row k sits at c ^ vfw(k) so a transpose read's 4 rows x 64 bytes
+// land on distinct banks (row pitch 128 B: alternate rows share a bank half; 256 B: every row starts at bank 0)
+template <int DH>
+__device__ __forceinline__ uint32_t vfw(uint32_t k) { return DH == 128 ? 4u * (k & 3u) : 4u * ((k >> 1) & 1u); }
+
+template <int DH, int NST>
+__global__ __launch_bounds__(256) void k_flash_dma(AttnArgs a) {
+    constexpr int DC = DH / 8, NS = DH / 16, DT = DH / 32;
+    constexpr int KCH = KB * DC;                     // 16-byte chunks per K (or V) block
+    constexpr int KR = KCH / 256;                    // DMA rounds per thread per block, per operand
+    constexpr int LOADS = 2 * KR;                    // DMA instructions per wave per block (K and V)
+    constexpr uint32_t STAGE = 2u * KCH * 16u;       // K block then V block
+    static_assert(KCH % 256 == 0 && NST >= 2, "attention tiling");
+    __shared__ uint4 smem[NST * 2 * KCH];
+
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = lane >> 5, r32 = lane & 31;
+    const int q4 = lane >> 4, iq = lane & 15;
+    const uint32_t b = blockIdx.z, h = blockIdx.y;
+    const uint32_t S = a.S;
+    const uint16_t *Q = a.q + b * a.bsq + (uint64_t)h * DH;
+    const uint16_t *Kp = a.k + b * a.bsk + (uint64_t)h * DH;
+    const uint16_t *Vp = a.v + b * a.bsv + (uint64_t)h * DH;
+    uint16_t *O = a.o + b * a.bso + (uint64_t)h * DH;
+    const uint32_t qw0 = blockIdx.x * QPB + wave * QPW, myq = qw0 + r32;
+    const uint32_t nkb = (S + KB - 1) / KB;
+
+    // per-lane DMA sources: slot p of a block -> (key, physical chunk) -> logical chunk (column part only;
+    // the row is added per block, clamped to S - 1)
+    const uint16_t *kcol[KR];
+    const uint16_t *vcol[KR];
+    uint32_t kkey[KR];
+#pragma unroll
+    for (int r = 0; r < KR; ++r) {
+        const uint32_t p = r * 256 + wave * 64 + lane, key = p / DC, pc = p % DC;
+        kkey[r] = key;
+        kcol[r] = Kp + 8 * (pc ^ kswz<DH>(key));
+        vcol[r] = Vp + 8 * (pc ^ vfw<DH>(key));
+    }
+    const uint32_t lds0 = attn_lds_addr(smem);
+    const uint32_t wave_off = (uint32_t)__builtin_amdgcn_readfirstlane(wave * 64 * 16);
+    auto issue = [&](uint32_t kb, int stage) {
+        const uint32_t st = lds0 + (uint32_t)stage * STAGE;
+        const uint32_t k0 = kb * KB;
+#pragma unroll
+        for (int r = 0; r < KR; ++r) {
+            const uint64_t row = min(k0 + kkey[r], S - 1);                      // rows past S read row S-1
+            attn_dma16(kcol[r] + row * a.ldk, st + r * 4096 + wave_off);
+            attn_dma16(vcol[r] + row * a.ldv, st + KCH * 16 + r * 4096 + wave_off);
+        }
+    };
+
+    sh_h8 qf[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) qf[s] = __builtin_bit_cast(sh_h8, ld8<true>(Q, a.ldq, myq, 16 * s + 8 * g, S, DH));
+    sh_f16v oacc[DT];
+#pragma unroll
+    for (int i = 0; i < DT; ++i) oacc[i] = sh_f16v{};
+    float m_run = -INFINITY, l_run = 0.f;
+
+#pragma unroll
+    for (int s = 0; s < NST - 1; ++s) issue(min((uint32_t)s, nkb - 1), s);
+
+    for (uint32_t kb = 0; kb < nkb; ++kb) {
+        attn_wait_vmcnt<(NST - 2) * LOADS>();
+        __syncthreads();
+        issue(min(kb + NST - 1, nkb - 1), (int)((kb + NST - 1) % NST));
+        const int st = (int)(kb % NST);
+        const uint4 *sk = smem + st * 2 * KCH;
+        const uint32_t vbase = lds0 + (uint32_t)st * STAGE + KCH * 16;
+
+        sh_f16v sacc[2];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            sacc[tt] = sh_f16v{};
+            const uint32_t key = 32 * tt + r32;
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const sh_h8 kf = __builtin_bit_cast(sh_h8, sk[key * DC + ((2 * s + g) ^ kswz<DH>(key))]);
+                sacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], sacc[tt], 0, 0, 0);
+            }
+        }
+        const bool masked = (kb + 1) * KB > S;
+        if (masked) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (kb * KB + 32 * tt + 8 * (r >> 2) + 4 * g + (r & 3) >= S) sacc[tt][r] = a.c >= 0.f ? -INFINITY : INFINITY;
+        }
+        float mb;
+        if (a.c >= 0.f) {
+            mb = -INFINITY;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mb = fmaxf(mb, sacc[tt][r]);
+            mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+        } else {
+            mb = INFINITY;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mb = fminf(mb, sacc[tt][r]);
+            mb = fminf(mb, __shfl_xor(mb, 32, 64));
+        }
+        const float m_new = fmaxf(m_run, a.c * mb);
+        const float alpha = sh_fast_exp2(m_run - m_new);
+        m_run = m_new;
+        float psum = 0.f;
+        sh_h8 pf[4];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float p = sh_fast_exp2(fmaf(sacc[tt][r], a.c, -m_new));
+                if (masked && kb * KB + 32 * tt + 8 * (r >> 2) + 4 * g + (r & 3) >= S) p = 0.f;
+                psum += p;
+                pf[2 * tt + (r >> 3)][r & 7] = (_Float16)p;
+            }
+        l_run = l_run * alpha + psum;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const uint32_t d = 32 * dt + 16 * (q4 & 1) + 4 * (iq & 3);
+#pragma unroll
+            for (int sp = 0; sp < 4; ++sp) {
+                const uint32_t k0 = 16 * sp + 4 * g + (iq >> 2), k1 = k0 + 8;
+                const attn_s4 lo = attn_read_tr(vbase + k0 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k0)) + 2 * (d & 7));
+                const attn_s4 hi = attn_read_tr(vbase + k1 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k1)) + 2 * (d & 7));
+                const sh_h8 vf = __builtin_bit_cast(sh_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[sp], oacc[dt], 0, 0, 0);
+            }
+        }
+    }
+    attn_wait_vmcnt<0>();      // clamped tail loads land before the LDS is reused below
+    __syncthreads();
+
+    const float l = l_run + __shfl_xor(l_run, 32, 64);
+    const float inv = 1.f / l;
+    uint16_t *so = (uint16_t *)smem + wave * (QPW * DH);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const int d0 = 32 * dt + 8 * rb + 4 * g;
+            const uint32_t lo = (uint32_t)sh_dev_f2h(oacc[dt][4 * rb] * inv) | ((uint32_t)sh_dev_f2h(oacc[dt][4 * rb + 1] * inv) << 16);
+            const uint32_t hi = (uint32_t)sh_dev_f2h(oacc[dt][4 * rb + 2] * inv) | ((uint32_t)sh_dev_f2h(oacc[dt][4 * rb + 3] * inv) << 16);
+            const int ch = (d0 >> 3) ^ (r32 & 7);
+            *(uint2 *)(so + r32 * DH + ch * 8 + (d0 & 7)) = make_uint2(lo, hi);
+        }
+    __syncthreads();
+    for (int c = lane; c < QPW * DC; c += 64) {
+        const int row = c / DC, ch = c % DC;
+        const uint32_t qq = qw0 + row;
+        if (qq >= S) continue;
+        *(uint4 *)(O + (uint64_t)qq * a.ldo + 8 * ch) = ((const uint4 *)so)[row * DC + (ch ^ (row & 7))];
+    }
+}
+
 // Any dh: one 256-thread block per (query, head, sequence); scores of the row in LDS (S <= 16384).
 __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
     extern __shared__ float sc[];
@@ -304,7 +489,11 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
     const bool vec = dh % 8 == 0 && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 8 == 0 &&
                      bsq % 8 == 0 && bsk % 8 == 0 && bsv % 8 == 0 && bso % 8 == 0 &&
                      sh_aligned16(q) && sh_aligned16(k) && sh_aligned16(v) && sh_aligned16(o);
-    if (dh <= 128) {
+    if ((dh == 64 || dh == 128) && vec) {
+        const dim3 grid(sh_cdiv(S, QPB), H, B), block(256);
+        if (dh == 64) hipLaunchKernelGGL((k_flash_dma<64, 4>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((k_flash_dma<128, 2>), grid, block, 0, st, a);
+    } else if (dh <= 128) {
         const dim3 grid(sh_cdiv(S, QPB), H, B), block(256);
         if (dh <= 64) {
             if (vec) hipLaunchKernelGGL((k_flash<64, true>), grid, block, 0, st, a);

@@ -83,7 +83,8 @@ def test_baseline_config4_batched(lib, gpu, B, S):
     assert bad == 0, err
 
 
-@pytest.mark.parametrize("S,D,H", [(100, 128, 2), (260, 384, 6), (36, 96, 3), (512, 1536, 12), (64, 576, 12), (20, 72, 2)])
+@pytest.mark.parametrize("S,D,H", [(100, 128, 2), (260, 384, 6), (36, 96, 3), (512, 1536, 12), (64, 576, 12), (20, 72, 2),
+                                   (12, 128, 2), (40, 256, 2), (1, 768, 12), (130, 1536, 12)])
 def test_shapes_ragged_and_head_widths(lib, gpu, S, D, H):
     """Ragged S (masked last key block), dh = 64 / 32 / 128 / 48 (padded) / 36 (element-wise path)."""
     q, k, v = data.normal((S, D), S), data.normal((S, D), S + 1), data.normal((S, D), S + 2)
