@@ -489,7 +489,8 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
     const bool vec = dh % 8 == 0 && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 8 == 0 &&
                      bsq % 8 == 0 && bsk % 8 == 0 && bsv % 8 == 0 && bso % 8 == 0 &&
                      sh_aligned16(q) && sh_aligned16(k) && sh_aligned16(v) && sh_aligned16(o);
-    if ((dh == 64 || dh == 128) && vec) {
+    static const int force_reg = [] { const char *e = getenv("SH_ATTN_REG"); return e && *e == '1'; }();
+    if ((dh == 64 || dh == 128) && vec && !force_reg) {
         const dim3 grid(sh_cdiv(S, QPB), H, B), block(256);
         if (dh == 64) hipLaunchKernelGGL((k_flash_dma<64, 4>), grid, block, 0, st, a);
         else hipLaunchKernelGGL((k_flash_dma<128, 2>), grid, block, 0, st, a);

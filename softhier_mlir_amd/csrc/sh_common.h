@@ -36,6 +36,12 @@ __device__ __forceinline__ float sh_dev_h2f(uint16_t h) {
 __device__ __forceinline__ uint16_t sh_dev_f2h(float f) {   // v_cvt_f16_f32: round to nearest even
     return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
+// Correctly rounded fp16 addition of packed pairs (v_pk_add_f16, round to nearest even). For fp16 operands
+// this equals rounding their fp32 sum to fp16: fp32 keeps 24 >= 2*11 + 2 significand bits, which makes the
+// double rounding exact (Figueroa, "When is double rounding innocuous?", SIGNUM 1995).
+__device__ __forceinline__ uint32_t sh_hadd2(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(sh_h2, a) + __builtin_bit_cast(sh_h2, b));
+}
 __device__ __forceinline__ float sh_fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float sh_fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 __device__ __forceinline__ float sh_fast_rsq(float x) { return __builtin_amdgcn_rsqf(x); }
@@ -45,10 +51,16 @@ __device__ __forceinline__ float sh_fast_rsq(float x) { return __builtin_amdgcn_
 // clamped so 2^t stays finite (x / (1 + 2^126) is 0 to fp16 precision for every x that reaches it).
 #define SH_GELU_K0 (-2.3022082f)
 #define SH_GELU_K1 (-0.10294324f)
+// Contraction is off and the final fp32 product is materialised (the empty asm) so that every caller (row
+// op, GEMM epilogue) evaluates the same fp32 operations and stores bit-identical fp16 results: without it the
+// compiler may fold the last product into a mixed-precision FMA that rounds straight to fp16.
 __device__ __forceinline__ float sh_gelu_f(float x) {
+#pragma clang fp contract(off)
     float t = x * (SH_GELU_K0 + SH_GELU_K1 * x * x);
     t = fminf(fmaxf(t, -126.f), 126.f);
-    return x * sh_fast_rcp(1.f + sh_fast_exp2(t));
+    float y = x * sh_fast_rcp(1.f + sh_fast_exp2(t));
+    __asm__("" : "+v"(y));
+    return y;
 }
 
 __device__ __forceinline__ float sh_wave_sum(float v) {

@@ -44,6 +44,9 @@ struct GemmArgs {
     uint32_t xcd_groups;         // > 1: XCD-aware block remap with this many XCDs (requires divisibility)
 };
 
+// Zero-filled stand-in read by the epilogue for operands a call does not have (never written).
+__device__ __align__(64) uint32_t g_epi_zero[16];
+
 __device__ __forceinline__ uint32_t swz(uint32_t r) { return (r ^ (r >> 3)) & 7u; }
 
 template <int BM, int BN>
@@ -89,41 +92,41 @@ __device__ __forceinline__ uint16_t epi_chain(const GemmArgs &a, uint16_t p, uin
     return sh_dev_f2h(v);
 }
 
-// The same chain on 8 consecutive columns (16-byte loads of z_old / bias / residual).
-__device__ __forceinline__ uint4 epi_chain8(const GemmArgs &a, uint4 q, uint32_t gm, uint32_t gn) {
-    float v[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = sh_dev_h2f((uint16_t)(comp(q, e >> 1) >> (16 * (e & 1))));
+// The same chain on 8 consecutive columns, with z_old / bias / residual already loaded (16-byte chunks; an
+// fp32 bias is b0:b1). fp16 + fp16 steps use packed fp16 adds, which round exactly like the fp32 form above.
+__device__ __forceinline__ uint4 epi_chain8(const GemmArgs &a, uint4 q, const uint4 &zo, const uint4 &b0, const uint4 &b1,
+                                            const uint4 &rq) {
+    uint32_t w[4] = {q.x, q.y, q.z, q.w};
     if (a.accumulate) {
-        const uint4 zq = *(const uint4 *)(a.z + (uint64_t)gm * a.ldz + gn);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = sh_dev_h2f(sh_dev_f2h(v[e] + sh_dev_h2f((uint16_t)(comp(zq, e >> 1) >> (16 * (e & 1))))));
+        for (int p = 0; p < 4; ++p) w[p] = sh_hadd2(comp(zo, p), w[p]);
     }
     if (a.bias) {
-        float b[8];
         if (a.bias_fp32) {
-            const float4 b0 = *(const float4 *)((const float *)a.bias + gn), b1 = *(const float4 *)((const float *)a.bias + gn + 4);
-            b[0] = b0.x; b[1] = b0.y; b[2] = b0.z; b[3] = b0.w; b[4] = b1.x; b[5] = b1.y; b[6] = b1.z; b[7] = b1.w;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const sh_h2 h = __builtin_bit_cast(sh_h2, w[p]);
+                const uint4 &bb = p < 2 ? b0 : b1;
+                const float lo = (float)h.x + __uint_as_float(comp(bb, (2 * p) & 3));
+                const float hi = (float)h.y + __uint_as_float(comp(bb, (2 * p + 1) & 3));
+                w[p] = __builtin_bit_cast(uint32_t, sh_h2{(_Float16)lo, (_Float16)hi});
+            }
         } else {
-            const uint4 bq = *(const uint4 *)((const uint16_t *)a.bias + gn);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) b[e] = sh_dev_h2f((uint16_t)(comp(bq, e >> 1) >> (16 * (e & 1))));
+            for (int p = 0; p < 4; ++p) w[p] = sh_hadd2(w[p], comp(b0, p));
         }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = sh_dev_h2f(sh_dev_f2h(v[e] + b[e]));
     }
     if (a.act == SH_ACT_GELU) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = sh_dev_h2f(sh_dev_f2h(sh_gelu_f(v[e])));
+        for (int p = 0; p < 4; ++p) {
+            const sh_h2 h = __builtin_bit_cast(sh_h2, w[p]);
+            w[p] = __builtin_bit_cast(uint32_t, sh_h2{(_Float16)sh_gelu_f((float)h.x), (_Float16)sh_gelu_f((float)h.y)});
+        }
     }
     if (a.res) {
-        const uint4 rq = *(const uint4 *)(a.res + (uint64_t)gm * a.ldr + gn);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] += sh_dev_h2f((uint16_t)(comp(rq, e >> 1) >> (16 * (e & 1))));
+        for (int p = 0; p < 4; ++p) w[p] = sh_hadd2(w[p], comp(rq, p));
     }
-    uint32_t w[4];
-#pragma unroll
-    for (int p = 0; p < 4; ++p) w[p] = (uint32_t)sh_dev_f2h(v[2 * p]) | ((uint32_t)sh_dev_f2h(v[2 * p + 1]) << 16);
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
@@ -166,15 +169,59 @@ __device__ __forceinline__ void epilogue(const GemmArgs &a, sh_f16v (&acc)[FM][F
     __syncthreads();
     const bool plain = !a.accumulate && !a.bias && a.act == SH_ACT_NONE && !a.res;
     constexpr int CPR = BN / 8;             // 16-byte chunks per tile row
-    for (int c = t; c < BM * CPR; c += 256) {
-        const int row = c / CPR, ch = c % CPR;
-        const uint32_t gm = m0 + row, gn = n0 + 8 * ch;
-        if (gm >= a.M || gn >= a.N) continue;
-        uint4 q = ((const uint4 *)sC)[row * CPR + (ch ^ (row & 7))];
-        if (VEC) {
-            if (!plain) q = epi_chain8(a, q, gm, gn);
-            *(uint4 *)(a.z + (uint64_t)gm * a.ldz + gn) = q;
-        } else {
+    if (VEC && plain) {
+        for (int c = t; c < BM * CPR; c += 256) {
+            const int row = c / CPR, ch = c % CPR;
+            const uint32_t gm = m0 + row, gn = n0 + 8 * ch;
+            if (gm < a.M && gn < a.N) *(uint4 *)(a.z + (uint64_t)gm * a.ldz + gn) = ((const uint4 *)sC)[row * CPR + (ch ^ (row & 7))];
+        }
+    } else if (VEC) {
+        // Chunk c = t + 256 i of the tile, in batches of NB chunks: (1) every global operand of the batch is
+        // loaded, branch-free, before any is used; (2) the fp16 products are read from LDS; (3) the chain runs;
+        // (4) the stores go out. A batch waits for one memory latency, and no load waits behind a store. An
+        // operand that is off is read from a 64-byte zero block (one cached line) and ignored.
+        constexpr int ITER = BM * CPR / 256, CAP = BM * BN >= 256 * 256 ? 4 : 6;       // CAP: registers in flight
+        constexpr int NB = ITER % CAP == 0 ? CAP : ITER % 4 == 0 ? 4 : ITER % 2 == 0 ? 2 : 1;
+        static_assert(ITER * 256 == BM * CPR && ITER % NB == 0, "epilogue chunk split");
+        const uint16_t *zero = (const uint16_t *)g_epi_zero;
+        const uint16_t *zs = a.accumulate ? a.z : zero, *rs = a.res ? a.res : zero;
+        const uint64_t ldzs = a.accumulate ? a.ldz : 0, ldrs = a.res ? a.ldr : 0;
+        const uint32_t zcs = a.accumulate ? 1 : 0, rcs = a.res ? 1 : 0;
+        const char *bs = a.bias ? (const char *)a.bias : (const char *)zero;
+        const uint32_t besz = a.bias ? (a.bias_fp32 ? 4 : 2) : 0, b1off = (a.bias && a.bias_fp32) ? 16 : 0;
+#pragma unroll 1
+        for (int i0 = 0; i0 < ITER; i0 += NB) {
+            uint4 q[NB], zo[NB], b0[NB], b1[NB], rq[NB];
+            uint32_t gms[NB], gns[NB];
+            bool ok[NB];
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const int c = t + 256 * (i0 + j), row = c / CPR, ch = c % CPR;
+                ok[j] = m0 + row < a.M && n0 + 8 * ch < a.N;
+                gms[j] = ok[j] ? m0 + row : m0;
+                gns[j] = ok[j] ? n0 + 8 * ch : n0;
+                zo[j] = *(const uint4 *)(zs + gms[j] * ldzs + gns[j] * zcs);
+                b0[j] = *(const uint4 *)(bs + gns[j] * besz);
+                b1[j] = *(const uint4 *)(bs + gns[j] * besz + b1off);
+                rq[j] = *(const uint4 *)(rs + gms[j] * ldrs + gns[j] * rcs);
+            }
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const int c = t + 256 * (i0 + j), row = c / CPR, ch = c % CPR;
+                q[j] = ((const uint4 *)sC)[row * CPR + (ch ^ (row & 7))];
+            }
+#pragma unroll
+            for (int j = 0; j < NB; ++j) q[j] = epi_chain8(a, q[j], zo[j], b0[j], b1[j], rq[j]);
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+                if (ok[j]) *(uint4 *)(a.z + (uint64_t)gms[j] * a.ldz + gns[j]) = q[j];
+        }
+    } else {
+        for (int c = t; c < BM * CPR; c += 256) {
+            const int row = c / CPR, ch = c % CPR;
+            const uint32_t gm = m0 + row, gn = n0 + 8 * ch;
+            if (gm >= a.M || gn >= a.N) continue;
+            const uint4 q = ((const uint4 *)sC)[row * CPR + (ch ^ (row & 7))];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 if (gn + e >= a.N) break;

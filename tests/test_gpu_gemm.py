@@ -131,6 +131,30 @@ def test_fused_epilogue_bias_gelu_residual(lib, gpu):
     assert bad == 0, err
 
 
+@pytest.mark.parametrize("act,accumulate", [(shops.SH_ACT_GELU, 0), (shops.SH_ACT_NONE, 1)])
+def test_fused_epilogue_is_the_library_sequence_bitwise(lib, gpu, act, accumulate):
+    """sh_gemm_ex(bias fp16 [+GELU] + residual) stores exactly what the reference's unfused sequence stores:
+    sh_gemm (Z = or Z +=) -> sh_add_bias -> [sh_gelu] -> sh_add (siglip.py:150-168 op order), bit for bit."""
+    import torch
+    M, N, K = 320, 448, 256
+    x, w = data.normal((M, K), 41), data.normal((K, N), 42, std=1 / np.sqrt(K))
+    b16, r, z0 = data.normal((1, N), 43, std=0.5), data.normal((M, N), 44), data.normal((M, N), 45)
+    X, W, B16, R = to_dev(x), to_dev(w), to_dev(b16), to_dev(r)
+    Z1, Z2 = to_dev(z0), to_dev(z0)
+    c = shops.cfg(64, 64, 64, accumulate=accumulate)          # tiles that divide M, N, K (sh_gemm.inc.c:60-63)
+    e = shops.epi(bias=A(B16), act=act, residual=A(R), ldr=N)
+    assert lib.sh_gemm_ex(A(X), A(W), A(Z1), M, N, K, K, N, N, c, e) == 0, shops.last_error()
+    assert lib.sh_gemm(A(X), A(W), A(Z2), M, N, K, K, N, N, c, shops.SH_ALL) == 0
+    lib.sh_add_bias(A(Z2), A(Z2), A(B16), M, N, N, shops.SH_ALL)
+    if act == shops.SH_ACT_GELU:
+        lib.sh_gelu(A(Z2), A(Z2), M, N, N, shops.SH_ALL)
+    lib.sh_add(A(Z2), A(Z2), A(R), M, N, N, shops.SH_ALL)
+    torch.cuda.synchronize()
+    z1, z2 = to_np(Z1).view(np.uint16), to_np(Z2).view(np.uint16)
+    bad = np.argwhere(z1 != z2)
+    assert len(bad) == 0, f"{len(bad)} differ, e.g. " + ", ".join(f"{tuple(ix)}: {z1[tuple(ix)]:04x} vs {z2[tuple(ix)]:04x}" for ix in bad[:6])
+
+
 def test_splitk_matches_and_is_deterministic(lib, gpu):
     """BASELINE config 2 FFN-down: M=256, K=3072, N=768, split-K = 4."""
     M, N, K = 256, 768, 3072
