@@ -18,6 +18,7 @@
 // Heads with dh <= 128 use this kernel (dh padded to 64 or 128 with zeros); wider heads use a simple
 // per-query kernel.
 #include "sh_common.h"
+#include <hip/hip_ext.h>
 #include <chrono>
 
 namespace {
@@ -485,32 +486,33 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
         if (!sh_hip_ok(hipEventCreate(&g_prof.e0), "hipEventCreate") || !sh_hip_ok(hipEventCreate(&g_prof.e1), "hipEventCreate")) return SH_EHIP;
     }
     g_prof.entry_ns = 0;
-    (void)hipEventRecord(g_prof.e0, st);
+    // The kernel's start / end timestamps come with its dispatch (no separate event packets on the stream).
+    auto go = [&](auto kern, dim3 grid, size_t shm) {
+        hipExtLaunchKernelGGL(kern, grid, dim3(256), (uint32_t)shm, st, g_prof.e0, g_prof.e1, 0u, a);
+    };
     const bool vec = dh % 8 == 0 && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 8 == 0 &&
                      bsq % 8 == 0 && bsk % 8 == 0 && bsv % 8 == 0 && bso % 8 == 0 &&
                      sh_aligned16(q) && sh_aligned16(k) && sh_aligned16(v) && sh_aligned16(o);
     static const int force_reg = [] { const char *e = getenv("SH_ATTN_REG"); return e && *e == '1'; }();
+    const dim3 grid(sh_cdiv(S, QPB), H, B);
     if ((dh == 64 || dh == 128) && vec && !force_reg) {
-        const dim3 grid(sh_cdiv(S, QPB), H, B), block(256);
-        if (dh == 64) hipLaunchKernelGGL((k_flash_dma<64, 4>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((k_flash_dma<128, 2>), grid, block, 0, st, a);
+        if (dh == 64) go(k_flash_dma<64, 4>, grid, 0);
+        else go(k_flash_dma<128, 2>, grid, 0);
     } else if (dh <= 128) {
-        const dim3 grid(sh_cdiv(S, QPB), H, B), block(256);
         if (dh <= 64) {
-            if (vec) hipLaunchKernelGGL((k_flash<64, true>), grid, block, 0, st, a);
-            else hipLaunchKernelGGL((k_flash<64, false>), grid, block, 0, st, a);
+            if (vec) go(k_flash<64, true>, grid, 0);
+            else go(k_flash<64, false>, grid, 0);
         } else {
-            if (vec) hipLaunchKernelGGL((k_flash<128, true>), grid, block, 0, st, a);
-            else hipLaunchKernelGGL((k_flash<128, false>), grid, block, 0, st, a);
+            if (vec) go(k_flash<128, true>, grid, 0);
+            else go(k_flash<128, false>, grid, 0);
         }
     } else {
         if (S > 16384) { sh_set_error(-1, "[sh_attention] dh=%u > 128 supports S <= 16384", dh); return -1; }
         static bool attr = false;
         if (!attr) { (void)hipFuncSetAttribute((const void *)k_attn_rows, hipFuncAttributeMaxDynamicSharedMemorySize, 16384 * 4); attr = true; }
-        hipLaunchKernelGGL(k_attn_rows, dim3(S, H, B), dim3(256), S * sizeof(float), st, a);
+        go(k_attn_rows, dim3(S, H, B), S * sizeof(float));
     }
     if (!sh_launch_ok("sh_attention")) return SH_EHIP;
-    (void)hipEventRecord(g_prof.e1, st);
     g_prof.valid = true;
     return 0;
 }

@@ -25,6 +25,8 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <map>
+#include <tuple>
 
 namespace {
 
@@ -614,6 +616,71 @@ Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t wa
     return best;
 }
 
+void set_attrs(KCfg &c) {
+    if (c.attr_set) return;
+    for (int v = 0; v < 2; ++v) {
+        (void)hipFuncSetAttribute((const void *)c.vec[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
+        if (c.scalar[v]) (void)hipFuncSetAttribute((const void *)c.scalar[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
+    }
+    c.attr_set = true;
+}
+
+void set_grid(GemmArgs &a, const KCfg &c) {
+    a.tiles_m = sh_cdiv(a.M, c.bm); a.tiles_n = sh_cdiv(a.N, c.bn);
+    const uint32_t nblk = a.tiles_m * a.tiles_n * a.splits;
+    const int X = sh_num_xcds();
+    a.xcd_groups = (X > 1 && nblk % (uint32_t)X == 0) ? (uint32_t)X : 1;
+}
+
+// One-time timing of the tile configurations for a large unsplit problem. Every unsplit configuration
+// accumulates K in the same order with the same MFMA, so they store bit-identical results and the choice only
+// changes speed. Trial runs write a scratch output (no residual, no accumulate; bias and activation as in the
+// call); the winner is cached per shape. Skipped under stream capture, for small problems, or SH_GEMM_TUNE=0.
+typedef std::tuple<uint32_t, uint32_t, uint32_t, uint64_t, uint64_t, uint32_t, uint32_t> TuneKey;
+std::map<TuneKey, int> g_tuned;
+
+int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st) {
+    static const int enabled = env_int("SH_GEMM_TUNE", 1);
+    if (!enabled || env_int("SH_GEMM_CFG", -1) >= 0) return heur;
+    const int cus = sh_num_cus() > 0 ? sh_num_cus() : 256;
+    if (est_time(g_cfgs[heur], call.M, call.N, call.K, 1, cus) < 12e-6) return heur;
+    const TuneKey key{call.M, call.N, call.K, call.ldx, call.ldw, call.bias ? 1u + call.bias_fp32 : 0u, call.act};
+    auto it = g_tuned.find(key);
+    if (it != g_tuned.end()) return it->second;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return heur;
+    uint16_t *scratch = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (hipMalloc(&scratch, (size_t)call.M * call.N * 2) != hipSuccess) { (void)hipGetLastError(); return heur; }
+    int best = heur;
+    if (hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess) {
+        GemmArgs a = call;
+        a.z = scratch; a.ldz = call.N; a.res = nullptr; a.ldr = 0; a.accumulate = 0; a.splits = 1; a.part = nullptr;
+        float best_ms = 1e30f;
+        for (int i = 0; i < kNumCfg; ++i) {
+            KCfg &c = g_cfgs[i];
+            if (!c.v2) continue;
+            set_attrs(c);
+            set_grid(a, c);
+            const dim3 grid(a.tiles_m * a.tiles_n);
+            hipLaunchKernelGGL(c.vec[0], grid, dim3(256), c.lds, st, a);
+            (void)hipEventRecord(e0, st);
+            for (int rep = 0; rep < 3; ++rep) hipLaunchKernelGGL(c.vec[0], grid, dim3(256), c.lds, st, a);
+            (void)hipEventRecord(e1, st);
+            float ms = 0.f;
+            if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) { best = heur; break; }
+            if (ms < best_ms) { best_ms = ms; best = i; }
+        }
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipStreamSynchronize(st);
+    (void)hipFree(scratch);
+    (void)hipGetLastError();
+    g_tuned[key] = best;
+    return best;
+}
+
 struct GemmReq {
     uint64_t x, w, z; uint32_t M, N, K; uint32_t ldx, ldw, ldz;
     uint32_t accumulate; const sh_gemm_epi *epi; uint32_t splits; bool mesh;
@@ -630,6 +697,13 @@ int launch(const GemmReq &r, const char *name) {
     const bool fast = vec && r.K % BK == 0 && r.K > 0;
     Plan p = choose(r.M, r.N, r.K, vec, fast, r.splits);
     if (r.mesh) p.splits = 1;
+    if (fast && p.splits == 1 && g_cfgs[p.cfg].v2) {
+        GemmArgs t{};
+        t.x = (const uint16_t *)r.x; t.w = (const uint16_t *)r.w; t.bias = (const void *)bias;
+        t.ldx = r.ldx; t.ldw = r.ldw; t.M = r.M; t.N = r.N; t.K = r.K; t.kps = sh_cdiv(r.K, BK) * BK; t.splits = 1;
+        t.bias_fp32 = (e && e->bias_fmt == SH_BIAS_FP32) ? 1 : 0; t.act = e ? e->act : 0;
+        p.cfg = tuned_cfg(t, p.cfg, sh_stream());
+    }
     KCfg &c = g_cfgs[p.cfg];
     uint32_t splits = std::max<uint32_t>(1, std::min<uint32_t>(p.splits, sh_cdiv(std::max<uint32_t>(r.K, 1), BK)));
     const uint32_t kps = sh_cdiv(sh_cdiv(std::max<uint32_t>(r.K, 1), splits), BK) * BK;
@@ -651,13 +725,7 @@ int launch(const GemmReq &r, const char *name) {
     hipStream_t st = sh_stream();
     const bool split = splits > 1;
     KernelFn fn = (vec || c.v2) ? c.vec[split] : c.scalar[split];
-    if (!c.attr_set) {
-        for (int v = 0; v < 2; ++v) {
-            (void)hipFuncSetAttribute((const void *)c.vec[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
-            if (c.scalar[v]) (void)hipFuncSetAttribute((const void *)c.scalar[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
-        }
-        c.attr_set = true;
-    }
+    set_attrs(c);
     if (split) {
         const size_t ws = (size_t)splits * r.M * r.N * sizeof(float);
         a.part = (float *)sh_workspace(ws);
