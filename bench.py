@@ -36,7 +36,19 @@ def parse():
     ap.add_argument("--seq", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true", help="skip the numpy CPU baseline")
     ap.add_argument("--no-rowops", action="store_true", help="skip the row-op bandwidth measurement")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run 3 plain device copies of 512 MiB (a known-size kernel for scaling HBM counters)")
     return ap.parse_args()
+
+
+def counted_traffic(op: str):
+    """HBM bytes per launch of `op` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (scaled by a
+    known-size copy; profiles/*hbm_counters.md), or None when no summary covers the op."""
+    for f in sorted((ROOT / "profiles").glob("*hbm_counters.md")):
+        for line in f.read_text().splitlines():
+            if line.startswith(f"traffic_bytes_per_launch {op}:"):
+                return int(line.split(":")[1])
+    return None
 
 
 def rowops_bandwidth(lib, torch, B: int, S: int, D: int, F: int, H: int, reps: int = 3) -> dict:
@@ -151,6 +163,14 @@ def main() -> int:
     lp = encoder.LayerParams.from_host(p)
     step = enc.layer_fused if args.sequence == "fused" else enc.layer_reference
 
+    if args.copy_calibration:
+        src = torch.empty(256 << 20, dtype=torch.float16, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     for _ in range(args.warmup):
         step(x, out, lp, B, S)
     torch.cuda.synchronize()
@@ -221,12 +241,14 @@ def main() -> int:
         if c["flop"]:
             ach = c["flop"] / (us * 1e-6) / 1e12
             roofline = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
-                        "frac": round(ach / PEAK_TFLOPS, 4), "traffic": None,
-                        "algorithmic_flop_per_launch": c["flop"], "avg_launch_us": round(us, 2)}
+                        "frac": round(ach / PEAK_TFLOPS, 4), "traffic": counted_traffic(dom),
+                        "algorithmic_flop_per_launch": c["flop"], "algorithmic_bytes_per_launch": c["bytes"],
+                        "avg_launch_us": round(us, 2)}
         else:
             ach = c["bytes"] / (us * 1e-6) / 1e9
             roofline = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                        "frac": round(ach / PEAK_GBS, 4), "traffic": None, "avg_launch_us": round(us, 2)}
+                        "frac": round(ach / PEAK_GBS, 4), "traffic": counted_traffic(dom),
+                        "algorithmic_bytes_per_launch": c["bytes"], "avg_launch_us": round(us, 2)}
 
     rowops = None if args.no_rowops else rowops_bandwidth(lib, torch, B, S, D, F, H)
     cpu = None if args.no_cpu else cpu_baseline(B, S, D, F, H, p, xh)
