@@ -487,8 +487,12 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
     }
     g_prof.entry_ns = 0;
     // The kernel's start / end timestamps come with its dispatch (no separate event packets on the stream).
+    // Under stream capture (a HIP graph) the launch carries no events and the profile is left unset.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const bool capturing = hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
     auto go = [&](auto kern, dim3 grid, size_t shm) {
-        hipExtLaunchKernelGGL(kern, grid, dim3(256), (uint32_t)shm, st, g_prof.e0, g_prof.e1, 0u, a);
+        if (capturing) hipLaunchKernelGGL(kern, grid, dim3(256), (uint32_t)shm, st, a);
+        else hipExtLaunchKernelGGL(kern, grid, dim3(256), (uint32_t)shm, st, g_prof.e0, g_prof.e1, 0u, a);
     };
     const bool vec = dh % 8 == 0 && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 8 == 0 &&
                      bsq % 8 == 0 && bsk % 8 == 0 && bsv % 8 == 0 && bso % 8 == 0 &&
@@ -513,7 +517,7 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
         go(k_attn_rows, dim3(S, H, B), S * sizeof(float));
     }
     if (!sh_launch_ok("sh_attention")) return SH_EHIP;
-    g_prof.valid = true;
+    g_prof.valid = !capturing;
     return 0;
 }
 

@@ -58,6 +58,7 @@ class Encoder:
         self.lib = shops.load()
         self.lib.sh_init()
         self._bufs: dict = {}
+        self._plan = None                    # (key, calls) of the last fused layer's argument set
         self.gemm_cfg = shops.cfg()          # tile hints 256^3 (library default), as the reference's default policy
         self.tap = None                      # optional tap(name) -> context manager around each op (timing)
 
@@ -68,6 +69,7 @@ class Encoder:
         if self._bufs.get("rows") != rows:
             z = lambda c: torch.empty((rows, c), dtype=torch.float16, device=self.device)  # noqa: E731
             D, F = self.D, self.F
+            self._plan = None
             self._bufs = {"rows": rows, "ln1": z(D), "qkv": z(3 * D), "q": z(D), "k": z(D), "v": z(D), "o": z(D),
                           "ao": z(D), "h": z(D), "ln2": z(D), "f1": z(F), "g": z(F), "f2": z(D)}
         return self._bufs
@@ -101,33 +103,60 @@ class Encoder:
         return out
 
     # -- fused sequence (additive entry points) ------------------------------------------------------------
-    def layer_fused(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int) -> torch.Tensor:
+    def _fused_plan(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int) -> list:
+        """The layer's library calls with every argument converted once: (op name, function, args, what)."""
+        key = (x.data_ptr(), out.data_ptr(), B, S) + tuple(t.data_ptr() for t in p.t.values())
+        if self._plan is not None and self._plan[0] == key:
+            return self._plan[1]
         L, A = self.lib, shops.addr
         D, F, H, rows = self.D, self.F, self.H, B * S
         b = self.buffers(rows)
         cfg = self.gemm_cfg
         D3 = 3 * D
-        with self._op("ln1"):
-            L.sh_layernorm(A(b["ln1"]), A(x), A(p["g1"]), A(p["be1"]), rows, D, D, self.eps, shops.SH_ALL)
-        with self._op("qkv"):
-            e = shops.epi(bias=A(p["bqkv"]))
-            _check(L.sh_gemm_ex(A(b["ln1"]), A(p["wqkv"]), A(b["qkv"]), rows, D3, D, D, D3, D3, cfg, e), "sh_gemm_ex qkv")
         qkv = b["qkv"]
-        with self._op("attention"):
-            _check(L.sh_attention_batched(A(qkv), A(qkv, D), A(qkv, 2 * D), A(b["o"]), B, S, D, H, D3, D3, D3, D,
-                                          S * D3, S * D3, S * D3, S * D, 1.0 / math.sqrt(D // H), 0), "sh_attention_batched")
-        with self._op("out_proj"):
-            e = shops.epi(bias=A(p["bo"]), residual=A(x), ldr=D)
-            _check(L.sh_gemm_ex(A(b["o"]), A(p["wo"]), A(b["h"]), rows, D, D, D, D, D, cfg, e), "sh_gemm_ex wo")
-        with self._op("ln2"):
-            L.sh_layernorm(A(b["ln2"]), A(b["h"]), A(p["g2"]), A(p["be2"]), rows, D, D, self.eps, shops.SH_ALL)
-        with self._op("ffn_up"):
-            e = shops.epi(bias=A(p["b1"]), act=shops.SH_ACT_GELU)
-            _check(L.sh_gemm_ex(A(b["ln2"]), A(p["w1"]), A(b["g"]), rows, F, D, D, F, F, cfg, e), "sh_gemm_ex w1")
-        with self._op("ffn_down"):
-            e = shops.epi(bias=A(p["b2"]), residual=A(b["h"]), ldr=D)
-            _check(L.sh_gemm_ex(A(b["g"]), A(p["w2"]), A(out), rows, D, F, F, D, D, cfg, e), "sh_gemm_ex w2")
+        calls = [
+            ("ln1", L.sh_layernorm, (A(b["ln1"]), A(x), A(p["g1"]), A(p["be1"]), rows, D, D, self.eps, shops.SH_ALL), None),
+            ("qkv", L.sh_gemm_ex, (A(b["ln1"]), A(p["wqkv"]), A(qkv), rows, D3, D, D, D3, D3, cfg,
+                                   shops.epi(bias=A(p["bqkv"]))), "sh_gemm_ex qkv"),
+            ("attention", L.sh_attention_batched, (A(qkv), A(qkv, D), A(qkv, 2 * D), A(b["o"]), B, S, D, H, D3, D3, D3, D,
+                                                   S * D3, S * D3, S * D3, S * D, 1.0 / math.sqrt(D // H), 0), "sh_attention_batched"),
+            ("out_proj", L.sh_gemm_ex, (A(b["o"]), A(p["wo"]), A(b["h"]), rows, D, D, D, D, D, cfg,
+                                        shops.epi(bias=A(p["bo"]), residual=A(x), ldr=D)), "sh_gemm_ex wo"),
+            ("ln2", L.sh_layernorm, (A(b["ln2"]), A(b["h"]), A(p["g2"]), A(p["be2"]), rows, D, D, self.eps, shops.SH_ALL), None),
+            ("ffn_up", L.sh_gemm_ex, (A(b["ln2"]), A(p["w1"]), A(b["g"]), rows, F, D, D, F, F, cfg,
+                                      shops.epi(bias=A(p["b1"]), act=shops.SH_ACT_GELU)), "sh_gemm_ex w1"),
+            ("ffn_down", L.sh_gemm_ex, (A(b["g"]), A(p["w2"]), A(out), rows, D, F, F, D, D, cfg,
+                                        shops.epi(bias=A(p["b2"]), residual=A(b["h"]), ldr=D)), "sh_gemm_ex w2"),
+        ]
+        self._plan = (key, calls)
+        return calls
+
+    def layer_fused(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int) -> torch.Tensor:
+        for name, fn, args, what in self._fused_plan(x, out, p, B, S):
+            with self._op(name):
+                rc = fn(*args)
+            if what is not None:
+                _check(rc, what)
         return out
+
+    def capture(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int) -> "torch.cuda.CUDAGraph":
+        """Record one fused layer into a HIP graph (replay with `.replay()` on any stream). The layer runs once
+        eagerly first, so buffers exist and every GEMM shape has its tile configuration settled; during capture
+        the library enqueues on the capture stream, then returns to the stream it had."""
+        self.layer_fused(x, out, p, B, S)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        prev = self.lib.sh_get_stream()
+        try:
+            with torch.cuda.stream(s):
+                self.lib.sh_set_stream(s.cuda_stream)
+                with torch.cuda.graph(g, stream=s):
+                    self.layer_fused(x, out, p, B, S)
+        finally:
+            self.lib.sh_set_stream(prev)
+        torch.cuda.synchronize()
+        return g
 
     @staticmethod
     def op_costs(B: int, S: int, D: int = 768, F: int = 3072, H: int = 12) -> dict:

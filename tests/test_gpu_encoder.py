@@ -46,3 +46,28 @@ def test_twelve_layer_stack(lib, gpu):
     want = refs.encoder_stack(x, ps, H, B=B)
     bad, err, _ = refs.close(to_np(out), want)
     assert bad == 0, err
+
+
+def test_captured_layer_graph_replays_match_eager(lib, gpu):
+    """The fused layer recorded into a HIP graph: every replay (with eager library work and synchronisations
+    between replays, and a new input copied into the captured buffer) stores exactly what the eager call
+    sequence stores for the same input."""
+    import torch
+    B, S, D, F, H = 4, 256, 768, 3072, 12
+    p = encoder.LayerParams.from_host(data.encoder_params(D, F, seed=100))
+    enc = encoder.Encoder(D, F, H)
+    x = to_dev(data.normal((B * S, D), 7))
+    out = torch.empty_like(x)
+    g = enc.capture(x, out, p, B, S)
+    eager = torch.empty_like(x)
+    for seed in (7, 8, 9):
+        x.copy_(to_dev(data.normal((B * S, D), seed)))
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        enc.layer_fused(x, eager, p, B, S)          # eager work between replays (same buffers for the scratch)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), eager.view(torch.int16))
+    want = refs.encoder_layer(data.normal((B * S, D), 9), {k: v.cpu().numpy() for k, v in p.t.items()}, H, B=B)
+    bad, err, _ = refs.close(to_np(out), want)
+    assert bad == 0, err
