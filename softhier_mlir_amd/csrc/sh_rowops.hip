@@ -36,25 +36,49 @@ __device__ __forceinline__ uint32_t slot_col(int lane, int u, int i) {
     return VEC ? 8u * (uint32_t)(lane + 64 * u) + (uint32_t)i : (uint32_t)lane + 64u * (uint32_t)(8 * u + i);
 }
 
-template <int NCH, bool VEC>
-__device__ __forceinline__ void load_row(const uint16_t *__restrict__ p, uint32_t cols, int lane, float (&v)[NCH][8]) {
+// 16-byte chunk u of a row for this lane: every chunk is loaded (one past the row end reads chunk 0 and is
+// zeroed in unpack_row), so all the loads of a row are in flight together.
+// Makes q's value available at this point (an empty asm that reads and writes it), so its load is not moved later.
+__device__ __forceinline__ void pin4(uint4 &q) { __asm__ volatile("" : "+v"(q.x), "+v"(q.y), "+v"(q.z), "+v"(q.w)); }
+
+template <int NCH>
+__device__ __forceinline__ void load_raw(const uint16_t *__restrict__ p, uint32_t cols, int lane, uint4 (&raw)[NCH]) {
 #pragma unroll
     for (int u = 0; u < NCH; ++u) {
-        if (VEC) {
-            const uint32_t c0 = slot_col<true>(lane, u, 0);
-            if (c0 < cols) unpack8(*(const uint4 *)(p + c0), v[u]);
-            else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[u][i] = 0.f;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t c = slot_col<false>(lane, u, i);
-                v[u][i] = c < cols ? sh_dev_h2f(p[c]) : 0.f;
-            }
-        }
+        const uint32_t c0 = slot_col<true>(lane, u, 0);
+        raw[u] = *(const uint4 *)(p + (c0 < cols ? c0 : 0u));
     }
+}
+
+template <int NCH>
+__device__ __forceinline__ void unpack_row(const uint4 (&raw)[NCH], uint32_t cols, int lane, float (&v)[NCH][8]) {
+#pragma unroll
+    for (int u = 0; u < NCH; ++u) {
+        float f[8];
+        unpack8(raw[u], f);
+        const bool ok = slot_col<true>(lane, u, 0) < cols;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[u][i] = ok ? f[i] : 0.f;
+    }
+}
+
+template <int NCH, bool VEC>
+__device__ __forceinline__ void load_row(const uint16_t *__restrict__ p, uint32_t cols, int lane, float (&v)[NCH][8]) {
+    if (VEC) {
+        uint4 raw[NCH];
+        load_raw<NCH>(p, cols, lane, raw);
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) pin4(raw[u]);   // all chunks issued before the first wait
+        unpack_row<NCH>(raw, cols, lane, v);
+        return;
+    }
+#pragma unroll
+    for (int u = 0; u < NCH; ++u)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t c = slot_col<false>(lane, u, i);
+            v[u][i] = c < cols ? sh_dev_h2f(p[c]) : 0.f;
+        }
 }
 
 template <int NCH, bool VEC>
@@ -81,8 +105,26 @@ __global__ __launch_bounds__(256) void k_layernorm(uint16_t *y, const uint16_t *
     const int lane = threadIdx.x & 63;
     const uint32_t row = blockIdx.x * kRowWaves + (threadIdx.x >> 6);
     if (row >= rows) return;
-    float v[NCH][8];
-    load_row<NCH, VEC>(x + row * ldx, cols, lane, v);
+    float v[NCH][8], g[NCH][8], b[NCH][8];
+    if (VEC) {                                        // x, gamma and beta loads in flight together
+        uint4 rx[NCH], rg[NCH], rb[NCH];
+        load_raw<NCH>(x + row * ldx, cols, lane, rx);
+        load_raw<NCH>(gamma, cols, lane, rg);
+        load_raw<NCH>(beta, cols, lane, rb);
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) {               // pin all three here: the compiler would otherwise sink
+            pin4(rx[u]);                              // the gamma / beta loads past the reductions
+            pin4(rg[u]);
+            pin4(rb[u]);
+        }
+        unpack_row<NCH>(rx, cols, lane, v);
+        unpack_row<NCH>(rg, cols, lane, g);
+        unpack_row<NCH>(rb, cols, lane, b);
+    } else {
+        load_row<NCH, VEC>(x + row * ldx, cols, lane, v);
+        load_row<NCH, VEC>(gamma, cols, lane, g);
+        load_row<NCH, VEC>(beta, cols, lane, b);
+    }
     float s = 0.f;
 #pragma unroll
     for (int u = 0; u < NCH; ++u)
@@ -99,9 +141,6 @@ __global__ __launch_bounds__(256) void k_layernorm(uint16_t *y, const uint16_t *
             q += d * d;
         }
     const float rs = sh_fast_rsq(sh_wave_sum(q) * inv_n + eps);
-    float g[NCH][8], b[NCH][8];
-    load_row<NCH, VEC>(gamma, cols, lane, g);
-    load_row<NCH, VEC>(beta, cols, lane, b);
 #pragma unroll
     for (int u = 0; u < NCH; ++u)
 #pragma unroll
@@ -199,27 +238,46 @@ __global__ __launch_bounds__(256) void k_elementwise(uint16_t *y, const uint16_t
     constexpr int U = 4;   // items per thread, issued together
     const uint32_t base = blockIdx.x * (256u * U) + threadIdx.x;
     (void)rows;
+    if (VEC) {
+        // all loads of the thread's items first (an item past the end reloads item 0 and is not stored), then
+        // compute and store: no load waits behind a store even when y aliases a
+        uint4 ra[U], rb[U];
+        uint64_t off[U];
+        bool ok[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t it = base + u * 256u;
+            ok[u] = it < items;
+            const uint32_t itc = ok[u] ? it : 0u;
+            const uint32_t r = sh_div(itc, div), cc = itc - r * per_row;
+            off[u] = r * ld + 8ull * cc;
+            ra[u] = *(const uint4 *)(a + off[u]);
+            if (OP == OP_ADD) rb[u] = *(const uint4 *)(b + off[u]);
+            else if (OP == OP_BIAS) rb[u] = *(const uint4 *)(b + 8ull * cc);
+            else rb[u] = make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (!ok[u]) continue;
+            float fa[8], fb[8];
+            unpack8(ra[u], fa);
+            unpack8(rb[u], fb);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) fa[i] = ew<OP>(fa[i], fb[i], s);
+            *(uint4 *)(y + off[u]) = pack8(fa);
+        }
+        return;
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const uint32_t it = base + u * 256u;
         if (it >= items) break;
         const uint32_t r = sh_div(it, div), cc = it - r * per_row;
-        if (VEC) {
-            const uint64_t off = r * ld + 8ull * cc;
-            float fa[8], fb[8];
-            unpack8(*(const uint4 *)(a + off), fa);
-            if (OP == OP_ADD) unpack8(*(const uint4 *)(b + off), fb);
-            else if (OP == OP_BIAS) unpack8(*(const uint4 *)(b + 8ull * cc), fb);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) fa[i] = ew<OP>(fa[i], (OP == OP_ADD || OP == OP_BIAS) ? fb[i] : 0.f, s);
-            *(uint4 *)(y + off) = pack8(fa);
-        } else {
-            const uint64_t off = r * ld + cc;
-            float fb = 0.f;
-            if (OP == OP_ADD) fb = sh_dev_h2f(b[off]);
-            else if (OP == OP_BIAS) fb = sh_dev_h2f(b[cc]);
-            y[off] = sh_dev_f2h(ew<OP>(sh_dev_h2f(a[off]), fb, s));
-        }
+        const uint64_t off = r * ld + cc;
+        float fb = 0.f;
+        if (OP == OP_ADD) fb = sh_dev_h2f(b[off]);
+        else if (OP == OP_BIAS) fb = sh_dev_h2f(b[cc]);
+        y[off] = sh_dev_f2h(ew<OP>(sh_dev_h2f(a[off]), fb, s));
     }
 }
 
