@@ -421,6 +421,178 @@ __global__ __launch_bounds__(256) void k_flash_dma(AttnArgs a) {
     }
 }
 
+// Two-pass variant of k_flash_dma for dh 64 / 128 (the default for aligned heads). On CDNA the softmax
+// VALU work, not the MFMA work, bounds attention, so the row maximum is found first in a cheap pass over the
+// keys (S^T = K . Q^T on MFMA, then max3 only); the second pass recomputes the scores and, with the final
+// maximum known, needs no running rescale of O or l: p = 2^(c s - m), P (fp16) feeds O^T += V^T . P^T, and
+// the row sums l come from one more MFMA with an all-ones A operand (the sums of the fp16 numerators the
+// PV product used). Masking of keys past S happens only in the last, partial key block.
+template <int DH, int NST>
+__global__ __launch_bounds__(256) void k_flash2(AttnArgs a) {
+    constexpr int DC = DH / 8, NS = DH / 16, DT = DH / 32;
+    constexpr int KCH = KB * DC;                     // 16-byte chunks per K (or V) block
+    constexpr int KR = KCH / 256;                    // DMA rounds per thread per block, per operand
+    constexpr uint32_t STAGE = 2u * KCH * 16u;       // K block then V block
+    static_assert(KCH % 256 == 0 && NST >= 2, "attention tiling");
+    __shared__ uint4 smem[NST * 2 * KCH];
+
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = lane >> 5, r32 = lane & 31;
+    const int q4 = lane >> 4, iq = lane & 15;
+    const uint32_t b = blockIdx.z, h = blockIdx.y;
+    const uint32_t S = a.S;
+    const uint16_t *Q = a.q + b * a.bsq + (uint64_t)h * DH;
+    const uint16_t *Kp = a.k + b * a.bsk + (uint64_t)h * DH;
+    const uint16_t *Vp = a.v + b * a.bsv + (uint64_t)h * DH;
+    uint16_t *O = a.o + b * a.bso + (uint64_t)h * DH;
+    const uint32_t qw0 = blockIdx.x * QPB + wave * QPW, myq = qw0 + r32;
+    const uint32_t nkb = (S + KB - 1) / KB;
+    const bool ragged = S % KB != 0;                 // the last key block is partial
+
+    const uint16_t *kcol[KR];
+    const uint16_t *vcol[KR];
+    uint32_t kkey[KR];
+#pragma unroll
+    for (int r = 0; r < KR; ++r) {
+        const uint32_t p = r * 256 + wave * 64 + lane, key = p / DC, pc = p % DC;
+        kkey[r] = key;
+        kcol[r] = Kp + 8 * (pc ^ kswz<DH>(key));
+        vcol[r] = Vp + 8 * (pc ^ vfw<DH>(key));
+    }
+    const uint32_t lds0 = attn_lds_addr(smem);
+    const uint32_t wave_off = (uint32_t)__builtin_amdgcn_readfirstlane(wave * 64 * 16);
+    auto issue = [&](uint32_t kb, int stage, bool with_v) {
+        const uint32_t st = lds0 + (uint32_t)stage * STAGE;
+        const uint32_t k0 = kb * KB;
+#pragma unroll
+        for (int r = 0; r < KR; ++r) {
+            const uint64_t row = min(k0 + kkey[r], S - 1);                      // rows past S read row S-1
+            attn_dma16(kcol[r] + row * a.ldk, st + r * 4096 + wave_off);
+            if (with_v) attn_dma16(vcol[r] + row * a.ldv, st + KCH * 16 + r * 4096 + wave_off);
+        }
+    };
+
+    sh_h8 qf[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) qf[s] = __builtin_bit_cast(sh_h8, ld8<true>(Q, a.ldq, myq, 16 * s + 8 * g, S, DH));
+
+    // S^T tile pair of key block in stage st: sacc[tt][r] = s(key 32 tt + 8 (r/4) + 4 g + r%4, query r32)
+    auto scores = [&](int st, sh_f16v (&sacc)[2]) {
+        const uint4 *sk = smem + st * 2 * KCH;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            sacc[tt] = sh_f16v{};
+            const uint32_t key = 32 * tt + r32;
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const sh_h8 kf = __builtin_bit_cast(sh_h8, sk[key * DC + ((2 * s + g) ^ kswz<DH>(key))]);
+                sacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], sacc[tt], 0, 0, 0);
+            }
+        }
+    };
+    auto key_ok = [&](uint32_t kb, int tt, int r) { return kb * KB + 32 * tt + 8 * (r >> 2) + 4 * g + (r & 3) < S; };
+
+    // ---- pass 1: extreme of s over all keys (max for c >= 0, min for c < 0), K blocks only ----
+    const bool pos = a.c >= 0.f;
+#pragma unroll
+    for (int s = 0; s < NST - 1; ++s) issue(min((uint32_t)s, nkb - 1), s, false);
+    float ext = pos ? -INFINITY : INFINITY;
+    for (uint32_t kb = 0; kb < nkb; ++kb) {
+        attn_wait_vmcnt<(NST - 2) * KR>();
+        __syncthreads();
+        issue(min(kb + NST - 1, nkb - 1), (int)((kb + NST - 1) % NST), false);
+        sh_f16v sacc[2];
+        scores((int)(kb % NST), sacc);
+        if (ragged && kb == nkb - 1) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (!key_ok(kb, tt, r)) sacc[tt][r] = pos ? -INFINITY : INFINITY;
+        }
+        if (pos) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) ext = fmaxf(ext, sacc[tt][r]);
+        } else {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) ext = fminf(ext, sacc[tt][r]);
+        }
+    }
+    ext = pos ? fmaxf(ext, __shfl_xor(ext, 32, 64)) : fminf(ext, __shfl_xor(ext, 32, 64));
+    const float m = a.c * ext;                       // max over keys of c s
+    attn_wait_vmcnt<0>();                            // the ring is idle before pass 2 refills it
+    __syncthreads();
+
+    // ---- pass 2: p = 2^(c s - m); O^T += V^T P^T; l += 1^T P^T ----
+    sh_f16v oacc[DT];
+#pragma unroll
+    for (int i = 0; i < DT; ++i) oacc[i] = sh_f16v{};
+    sh_f16v lacc = sh_f16v{};
+    sh_h8 ones;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ones[e] = (_Float16)1.0f;
+#pragma unroll
+    for (int s = 0; s < NST - 1; ++s) issue(min((uint32_t)s, nkb - 1), s, true);
+    for (uint32_t kb = 0; kb < nkb; ++kb) {
+        attn_wait_vmcnt<(NST - 2) * 2 * KR>();
+        __syncthreads();
+        issue(min(kb + NST - 1, nkb - 1), (int)((kb + NST - 1) % NST), true);
+        const int st = (int)(kb % NST);
+        sh_f16v sacc[2];
+        scores(st, sacc);
+        sh_h8 pf[4];
+        const bool tail = ragged && kb == nkb - 1;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float p = sh_fast_exp2(fmaf(sacc[tt][r], a.c, -m));
+                if (tail && !key_ok(kb, tt, r)) p = 0.f;
+                pf[2 * tt + (r >> 3)][r & 7] = (_Float16)p;
+            }
+        const uint32_t vbase = lds0 + (uint32_t)st * STAGE + KCH * 16;
+#pragma unroll
+        for (int sp = 0; sp < 4; ++sp) lacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, pf[sp], lacc, 0, 0, 0);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const uint32_t d = 32 * dt + 16 * (q4 & 1) + 4 * (iq & 3);
+#pragma unroll
+            for (int sp = 0; sp < 4; ++sp) {
+                const uint32_t k0 = 16 * sp + 4 * g + (iq >> 2), k1 = k0 + 8;
+                const attn_s4 lo = attn_read_tr(vbase + k0 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k0)) + 2 * (d & 7));
+                const attn_s4 hi = attn_read_tr(vbase + k1 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k1)) + 2 * (d & 7));
+                const sh_h8 vf = __builtin_bit_cast(sh_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[sp], oacc[dt], 0, 0, 0);
+            }
+        }
+    }
+    attn_wait_vmcnt<0>();      // clamped tail loads land before the LDS is reused below
+    __syncthreads();
+
+    const float inv = 1.f / lacc[0];                 // every row of the ones product holds this query's l
+    uint16_t *so = (uint16_t *)smem + wave * (QPW * DH);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const int d0 = 32 * dt + 8 * rb + 4 * g;
+            const uint32_t lo = (uint32_t)sh_dev_f2h(oacc[dt][4 * rb] * inv) | ((uint32_t)sh_dev_f2h(oacc[dt][4 * rb + 1] * inv) << 16);
+            const uint32_t hi = (uint32_t)sh_dev_f2h(oacc[dt][4 * rb + 2] * inv) | ((uint32_t)sh_dev_f2h(oacc[dt][4 * rb + 3] * inv) << 16);
+            const int ch = (d0 >> 3) ^ (r32 & 7);
+            *(uint2 *)(so + r32 * DH + ch * 8 + (d0 & 7)) = make_uint2(lo, hi);
+        }
+    __syncthreads();
+    for (int c = lane; c < QPW * DC; c += 64) {
+        const int row = c / DC, ch = c % DC;
+        const uint32_t qq = qw0 + row;
+        if (qq >= S) continue;
+        *(uint4 *)(O + (uint64_t)qq * a.ldo + 8 * ch) = ((const uint4 *)so)[row * DC + (ch ^ (row & 7))];
+    }
+}
+
 // Any dh: one 256-thread block per (query, head, sequence); scores of the row in LDS (S <= 16384).
 __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
     extern __shared__ float sc[];
@@ -497,9 +669,12 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
     const bool vec = dh % 8 == 0 && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 8 == 0 &&
                      bsq % 8 == 0 && bsk % 8 == 0 && bsv % 8 == 0 && bso % 8 == 0 &&
                      sh_aligned16(q) && sh_aligned16(k) && sh_aligned16(v) && sh_aligned16(o);
-    static const int force_reg = [] { const char *e = getenv("SH_ATTN_REG"); return e && *e == '1'; }();
+    static const int impl = [] { const char *e = getenv("SH_ATTN_IMPL"); return (e && *e) ? atoi(e) : 0; }();
     const dim3 grid(sh_cdiv(S, QPB), H, B);
-    if ((dh == 64 || dh == 128) && vec && !force_reg) {
+    if ((dh == 64 || dh == 128) && vec && impl == 0) {
+        if (dh == 64) go(k_flash2<64, 4>, grid, 0);
+        else go(k_flash2<128, 2>, grid, 0);
+    } else if ((dh == 64 || dh == 128) && vec && impl == 1) {
         if (dh == 64) go(k_flash_dma<64, 4>, grid, 0);
         else go(k_flash_dma<128, 2>, grid, 0);
     } else if (dh <= 128) {

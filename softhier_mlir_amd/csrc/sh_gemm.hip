@@ -96,7 +96,7 @@ __device__ __forceinline__ uint16_t epi_chain(const GemmArgs &a, uint16_t p, uin
         const float b = a.bias_fp32 ? ((const float *)a.bias)[gn] : sh_dev_h2f(((const uint16_t *)a.bias)[gn]);
         v = sh_dev_h2f(sh_dev_f2h(v + b));
     }
-    if (a.act == SH_ACT_GELU) v = sh_dev_h2f(sh_dev_f2h(sh_gelu_f(v)));
+    if (a.act == SH_ACT_GELU) { const uint16_t h = sh_dev_f2h(v); v = sh_dev_h2f((uint16_t)sh_gelu_u32(h | ((uint32_t)h << 16))); }
     if (a.res) v += sh_dev_h2f(a.res[(uint64_t)gm * a.ldr + gn]);
     return sh_dev_f2h(v);
 }
@@ -127,10 +127,7 @@ __device__ __forceinline__ uint4 epi_chain8(const GemmArgs &a, uint4 q, const ui
     }
     if (a.act == SH_ACT_GELU) {
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const sh_h2 h = __builtin_bit_cast(sh_h2, w[p]);
-            w[p] = __builtin_bit_cast(uint32_t, sh_h2{(_Float16)sh_gelu_f((float)h.x), (_Float16)sh_gelu_f((float)h.y)});
-        }
+        for (int p = 0; p < 4; ++p) w[p] = sh_gelu_u32(w[p]);
     }
     if (a.res) {
 #pragma unroll
@@ -523,6 +520,234 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs a) {
 }
 
 // Sum of the split partials in split order, then the epilogue of k_gemm. Item = 8 columns (VEC) or 1.
+// ---- v3: 8-wave ping-pong ----------------------------------------------------------------------------------
+// Two groups of four wavefronts share a CU (two waves per SIMD) and alternate, barrier by barrier, between a
+// memory phase (issue global->LDS DMA, read one whole k-slice of fragments from LDS into registers) and a
+// compute phase (the slice's MFMAs back to back, all operands already in registers). Group 1 starts one
+// barrier late, so while one group computes the other feeds: the MFMA pipe of every SIMD always has a wave
+// with ready operands. Group g owns output rows [g BM/2, (g+1) BM/2) of the tile; within a group the waves
+// form a 2 x 2 grid of (BM/4) x (BN/2) sub-tiles. Two LDS stages. Barrier indices (i-th __syncthreads of the
+// block): group 0 reads slice k between barriers 2k and 2k+1 and computes it before 2k+2; group 1 reads it
+// between 2k+1 and 2k+2 and computes it before 2k+3. Group 0 loads the X rows of slice k+1 while it reads
+// slice k and waits for them before barrier 2k+2; group 1 loads the W rows of slice k+1 during its compute
+// phase of slice k-1 (barriers 2k..2k+1) and waits before barrier 2k+2. Every stage is refilled only after
+// both groups passed the barrier that ends their reads of it, and is complete at the barrier that starts
+// the first read.
+template <int BM, int BN>
+struct Cfg3 {
+    static constexpr int TM = BM / 4, TN = BN / 2, FM = TM / 32, FN = TN / 32;
+    static constexpr int XCH = BM * 8;               // 16-byte chunks per X slice (BM rows x 64 k)
+    static constexpr int WCPR = BN / 8;              // chunks per W row
+    static constexpr int WCH = BK * WCPR;            // chunks per W slice
+    static constexpr int XR = XCH / 256, WR = WCH / 256;   // DMA rounds per thread of the loading group
+    static constexpr size_t STAGE = (size_t)(XCH + WCH) * 16;
+    static constexpr size_t LDS = 2 * STAGE > (size_t)BM * BN * 2 ? 2 * STAGE : (size_t)BM * BN * 2;
+    static_assert(BM % 128 == 0 && BN % 64 == 0 && XCH % 256 == 0 && WCH % 256 == 0 && FM >= 1 && FN >= 1, "tile");
+    static_assert(LDS <= 160 * 1024, "resources");
+};
+
+// Accumulators -> Z for the 8-wave layout (wave origin row0 / col0 in the tile), otherwise as epilogue().
+template <int BM, int BN, int NT, bool SPLIT, int FM, int FN>
+__device__ __forceinline__ void epilogue8(const GemmArgs &a, sh_f16v (&acc)[FM][FN], uint32_t m0, uint32_t n0, uint32_t split,
+                                          uint16_t *sC, uint32_t row0, uint32_t col0) {
+    const int t = threadIdx.x, lane = t & 63, g = lane >> 5, r32 = lane & 31;
+    if (SPLIT) {
+        float *P = a.part + (uint64_t)split * a.M * a.N;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const uint32_t gn = n0 + col0 + j * 32 + r32;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t gm = m0 + row0 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (gm < a.M && gn < a.N) P[(uint64_t)gm * a.N + gn] = acc[i][j][r];
+                }
+            }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const uint32_t col = col0 + j * 32 + r32;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t row = row0 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                sC[row * BN + (((col >> 3) ^ (row & 7)) << 3) + (col & 7)] = sh_dev_f2h(acc[i][j][r]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    __syncthreads();
+    const bool plain = !a.accumulate && !a.bias && a.act == SH_ACT_NONE && !a.res;
+    constexpr int CPR = BN / 8;
+    if (plain) {
+        for (int c = t; c < BM * CPR; c += NT) {
+            const int row = c / CPR, ch = c % CPR;
+            const uint32_t gm = m0 + row, gn = n0 + 8 * ch;
+            if (gm < a.M && gn < a.N) *(uint4 *)(a.z + (uint64_t)gm * a.ldz + gn) = ((const uint4 *)sC)[row * CPR + (ch ^ (row & 7))];
+        }
+        return;
+    }
+    constexpr int ITER = BM * CPR / NT, NB = ITER % 4 == 0 ? 4 : ITER % 2 == 0 ? 2 : 1;
+    static_assert(ITER * NT == BM * CPR, "epilogue chunk split");
+    const uint16_t *zero = (const uint16_t *)g_epi_zero;
+    const uint16_t *zs = a.accumulate ? a.z : zero, *rs = a.res ? a.res : zero;
+    const uint64_t ldzs = a.accumulate ? a.ldz : 0, ldrs = a.res ? a.ldr : 0;
+    const uint32_t zcs = a.accumulate ? 1 : 0, rcs = a.res ? 1 : 0;
+    const char *bs = a.bias ? (const char *)a.bias : (const char *)zero;
+    const uint32_t besz = a.bias ? (a.bias_fp32 ? 4 : 2) : 0, b1off = (a.bias && a.bias_fp32) ? 16 : 0;
+#pragma unroll 1
+    for (int i0 = 0; i0 < ITER; i0 += NB) {
+        uint4 q[NB], zo[NB], b0[NB], b1[NB], rq[NB];
+        uint32_t gms[NB], gns[NB];
+        bool ok[NB];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int c = t + NT * (i0 + j), row = c / CPR, ch = c % CPR;
+            ok[j] = m0 + row < a.M && n0 + 8 * ch < a.N;
+            gms[j] = ok[j] ? m0 + row : m0;
+            gns[j] = ok[j] ? n0 + 8 * ch : n0;
+            zo[j] = *(const uint4 *)(zs + gms[j] * ldzs + gns[j] * zcs);
+            b0[j] = *(const uint4 *)(bs + gns[j] * besz);
+            b1[j] = *(const uint4 *)(bs + gns[j] * besz + b1off);
+            rq[j] = *(const uint4 *)(rs + gms[j] * ldrs + gns[j] * rcs);
+        }
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int c = t + NT * (i0 + j), row = c / CPR, ch = c % CPR;
+            q[j] = ((const uint4 *)sC)[row * CPR + (ch ^ (row & 7))];
+        }
+#pragma unroll
+        for (int j = 0; j < NB; ++j) q[j] = epi_chain8(a, q[j], zo[j], b0[j], b1[j], rq[j]);
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+            if (ok[j]) *(uint4 *)(a.z + (uint64_t)gms[j] * a.ldz + gns[j]) = q[j];
+    }
+}
+
+// One block barrier that the compiler cannot move other instructions across (MFMAs included).
+__device__ __forceinline__ void hard_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int BM, int BN, bool SPLIT>
+__global__ __launch_bounds__(512) void k_gemm3(GemmArgs a) {
+    using C = Cfg3<BM, BN>;
+    extern __shared__ uint4 smem[];
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6), grp = wave >> 2, w4 = wave & 3;   // wave-uniform
+    const int wm = w4 >> 1, wn = w4 & 1, g = lane >> 5, r32 = lane & 31;
+    const int lt = t & 255;                            // thread index within the group
+
+    const uint32_t nblk = a.tiles_m * a.tiles_n * a.splits;
+    uint32_t L = blockIdx.x;
+    if (a.xcd_groups > 1) L = (blockIdx.x % a.xcd_groups) * (nblk / a.xcd_groups) + blockIdx.x / a.xcd_groups;
+    const uint32_t tn = L % a.tiles_n, rest = L / a.tiles_n;
+    const uint32_t tm = rest % a.tiles_m, split = rest / a.tiles_m;
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t kbeg = split * a.kps;
+    const uint32_t kend = min(a.K, kbeg + a.kps);
+    const int KT = kend > kbeg ? (int)((kend - kbeg) / BK) : 0;
+
+    // DMA sources of this thread's rounds: group 0 owns the X slice, group 1 the W slice
+    constexpr int NR = C::XR > C::WR ? C::XR : C::WR;
+    const uint16_t *src[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const uint32_t p = r * 256 + lt;
+        if (grp == 0) {
+            const uint32_t m = p >> 3, c = (p & 7) ^ swz(m);
+            src[r] = a.x + (uint64_t)min(m0 + m, a.M - 1) * a.ldx + kbeg + 8 * c;
+        } else {
+            const uint32_t k = p / C::WCPR, c = (p % C::WCPR) ^ fw<BN>(k);
+            uint32_t gn = n0 + 8 * c;
+            if (gn >= a.N) gn = a.N - 8;
+            src[r] = a.w + (uint64_t)(kbeg + k) * a.ldw + gn;
+        }
+    }
+    const uint32_t lds0 = lds_addr(smem);
+    const uint32_t wave_off = (uint32_t)__builtin_amdgcn_readfirstlane(w4 * 64 * 16);
+    const int my_rounds = grp == 0 ? C::XR : C::WR;
+    auto issue = [&](int slice, int stage) {        // this thread's share of slice `slice` into `stage`
+        const uint32_t st = lds0 + (uint32_t)stage * (uint32_t)C::STAGE + (grp == 0 ? 0u : (uint32_t)C::XCH * 16u);
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            if (r >= my_rounds) break;
+            const uint64_t adv = grp == 0 ? (uint64_t)slice * BK : (uint64_t)slice * BK * a.ldw;
+            lds_dma16(src[r] + adv, st + r * 4096 + wave_off);
+        }
+    };
+
+    sh_f16v acc[C::FM][C::FN];
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j) acc[i][j] = sh_f16v{};
+    const uint32_t row0 = grp * (BM / 2) + wm * C::TM, col0 = wn * C::TN;
+    const int q = lane >> 4, iq = lane & 15;
+
+    sh_h8 af[4][C::FM], bf[4][C::FN];
+    auto read_slice = [&](int stage) {
+        const uint4 *X = (const uint4 *)((const char *)smem + (uint32_t)stage * (uint32_t)C::STAGE);
+        const uint32_t wbase = lds0 + (uint32_t)stage * (uint32_t)C::STAGE + C::XCH * 16;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+#pragma unroll
+            for (int i = 0; i < C::FM; ++i) {
+                const uint32_t m = row0 + i * 32 + r32;
+                af[s][i] = __builtin_bit_cast(sh_h8, X[m * 8 + ((2 * s + g) ^ swz(m))]);
+            }
+#pragma unroll
+            for (int j = 0; j < C::FN; ++j) {
+                const uint32_t n = (uint32_t)(col0 + j * 32 + 16 * (q & 1) + 4 * (iq & 3));
+                const uint32_t k0 = 16 * s + 8 * g + (iq >> 2), k1 = k0 + 4;
+                const sh_s4 lo = ds_read_tr(wbase + k0 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k0)) + 2 * (n & 7));
+                const sh_s4 hi = ds_read_tr(wbase + k1 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k1)) + 2 * (n & 7));
+                bf[s][j] = __builtin_bit_cast(sh_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            }
+        }
+    };
+    auto compute_slice = [&]() {
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+                for (int j = 0; j < C::FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[s][i], bf[s][j], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_s_setprio(0);
+    };
+
+    // prologue: slice 0 complete at barrier 0; group 1 also has its share of slice 1 in flight
+    if (KT > 0) {
+        issue(0, 0);
+        if (grp == 1 && KT > 1) { issue(1, 1); wait_vmcnt<C::WR>(); }
+        else wait_vmcnt<0>();
+    }
+    hard_barrier();                                   // barrier 0
+    if (grp == 1) hard_barrier();                     // barrier 1: group 1 runs one phase behind
+    for (int k = 0; k < KT; ++k) {
+        const int st = k & 1;
+        // memory phase
+        if (grp == 0 && k + 1 < KT) issue(k + 1, st ^ 1);
+        read_slice(st);
+        if (grp == 1) wait_vmcnt<0>();                // group 1's share of slice k+1 (issued a phase ago)
+        __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0): the fragments are in registers
+        hard_barrier();
+        // compute phase
+        if (grp == 1 && k + 2 < KT) issue(k + 2, st);
+        compute_slice();
+        if (grp == 0) wait_vmcnt<0>();                // group 0's share of slice k+1
+        hard_barrier();
+    }
+    if (grp == 0) hard_barrier();                     // both groups end on the same barrier count
+    epilogue8<BM, BN, 512, SPLIT, C::FM, C::FN>(a, acc, m0, n0, split, (uint16_t *)smem, row0, col0);
+}
+
 template <bool VEC>
 __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs a, ShDiv div, uint32_t per_row, uint32_t items) {
     const uint32_t it = blockIdx.x * 256u + threadIdx.x;
@@ -560,12 +785,14 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs a, ShDiv div, ui
 // ---- host side ------------------------------------------------------------------------------------------
 typedef void (*KernelFn)(GemmArgs);
 // v2 entries need vec operands and K % 64 == 0; v1 entries take anything (scalar variants for small tiles).
-struct KCfg { int bm, bn, stages; bool v2; KernelFn vec[2], scalar[2]; size_t lds; float eff; bool attr_set; };
+struct KCfg { int bm, bn, stages; bool v2; KernelFn vec[2], scalar[2]; size_t lds; float eff; bool attr_set; int threads = 256; };
 
 #define SH_KCFG(BM, BN, EFF) { BM, BN, 2, false, { k_gemm<BM, BN, true, false>, k_gemm<BM, BN, true, true> }, \
                                { k_gemm<BM, BN, false, false>, k_gemm<BM, BN, false, true> }, Cfg<BM, BN>::LDS, EFF, false }
 #define SH_KCFG2(BM, BN, ST, EFF) { BM, BN, ST, true, { k_gemm2<BM, BN, ST, false>, k_gemm2<BM, BN, ST, true> }, \
-                                    { nullptr, nullptr }, Cfg2<BM, BN, ST>::LDS, EFF, false }
+                                    { nullptr, nullptr }, Cfg2<BM, BN, ST>::LDS, EFF, false, 256 }
+#define SH_KCFG3(BM, BN, EFF) { BM, BN, 2, true, { k_gemm3<BM, BN, false>, k_gemm3<BM, BN, true> }, \
+                                { nullptr, nullptr }, Cfg3<BM, BN>::LDS, EFF, false, 512 }
 // eff = sustained fraction of the MFMA peak per CU measured for each tile on MI355X (tile-time model of
 // est_time below); it only ranks the configurations.
 KCfg g_cfgs[] = {
@@ -582,9 +809,13 @@ KCfg g_cfgs[] = {
     SH_KCFG2(128, 128, 3, 0.25f),
     SH_KCFG2(128, 192, 2, 0.30f),
     SH_KCFG2(128, 128, 2, 0.27f),
+    SH_KCFG3(256, 128, 0.28f),
+    SH_KCFG3(128, 256, 0.28f),
+    SH_KCFG3(128, 128, 0.26f),
 };
 #undef SH_KCFG
 #undef SH_KCFG2
+#undef SH_KCFG3
 constexpr int kNumCfg = sizeof(g_cfgs) / sizeof(g_cfgs[0]);
 
 int env_int(const char *name, int dflt) {
@@ -678,9 +909,9 @@ int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st) {
             set_attrs(c);
             set_grid(a, c);
             const dim3 grid(a.tiles_m * a.tiles_n);
-            hipLaunchKernelGGL(c.vec[0], grid, dim3(256), c.lds, st, a);
+            hipLaunchKernelGGL(c.vec[0], grid, dim3(c.threads), c.lds, st, a);
             (void)hipEventRecord(e0, st);
-            for (int rep = 0; rep < 3; ++rep) hipLaunchKernelGGL(c.vec[0], grid, dim3(256), c.lds, st, a);
+            for (int rep = 0; rep < 3; ++rep) hipLaunchKernelGGL(c.vec[0], grid, dim3(c.threads), c.lds, st, a);
             (void)hipEventRecord(e1, st);
             float ms = 0.f;
             if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) { best = heur; break; }
@@ -746,7 +977,7 @@ int launch(const GemmReq &r, const char *name) {
         a.part = (float *)sh_workspace(ws);
         if (!a.part) return SH_EHIP;
     }
-    hipLaunchKernelGGL(fn, dim3(nblk), dim3(256), c.lds, st, a);
+    hipLaunchKernelGGL(fn, dim3(nblk), dim3(c.threads), c.lds, st, a);
     if (!sh_launch_ok(name)) return SH_EHIP;
     if (split) {
         const bool rvec = vec;

@@ -227,9 +227,8 @@ __global__ __launch_bounds__(256) void k_softmax_wide(uint16_t *y, const uint16_
 // Elementwise ops over [rows, cols] with one leading dim; item = a 16-byte chunk (VEC) or one half.
 template <int OP>
 __device__ __forceinline__ float ew(float a, float b, float s) {
-    if (OP == OP_GELU) return sh_gelu_f(a);
     if (OP == OP_SCALE) return a * s;
-    return a + b;   // OP_ADD, OP_BIAS
+    return a + b;   // OP_ADD, OP_BIAS (rounded once to fp16 by the caller)
 }
 
 template <int OP, bool VEC>
@@ -259,6 +258,11 @@ __global__ __launch_bounds__(256) void k_elementwise(uint16_t *y, const uint16_t
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (!ok[u]) continue;
+            if (OP == OP_GELU) {                      // on fp16 pairs, as the GEMM epilogue does
+                const uint4 q = ra[u];
+                *(uint4 *)(y + off[u]) = make_uint4(sh_gelu_u32(q.x), sh_gelu_u32(q.y), sh_gelu_u32(q.z), sh_gelu_u32(q.w));
+                continue;
+            }
             float fa[8], fb[8];
             unpack8(ra[u], fa);
             unpack8(rb[u], fb);
@@ -277,7 +281,12 @@ __global__ __launch_bounds__(256) void k_elementwise(uint16_t *y, const uint16_t
         float fb = 0.f;
         if (OP == OP_ADD) fb = sh_dev_h2f(b[off]);
         else if (OP == OP_BIAS) fb = sh_dev_h2f(b[cc]);
-        y[off] = sh_dev_f2h(ew<OP>(sh_dev_h2f(a[off]), fb, s));
+        if (OP == OP_GELU) {
+            const uint32_t h = a[off];
+            y[off] = (uint16_t)sh_gelu_u32(h | (h << 16));
+        } else {
+            y[off] = sh_dev_f2h(ew<OP>(sh_dev_h2f(a[off]), fb, s));
+        }
     }
 }
 
