@@ -8,6 +8,8 @@
 // Rows wider than the register-resident limit (8192 columns) use a block-per-row loop kernel. Tensors
 // whose base, leading dim or width is not a multiple of 8 halves take element-wise variants.
 #include "sh_common.h"
+#include <algorithm>
+#include <cstdlib>
 
 namespace {
 

@@ -171,3 +171,16 @@ def test_large_rows_batched_hbm_shapes(lib, gpu):
     I = to_dev(ints)
     lib.sh_add(A(Y), A(I), A(I), rows, cols, cols, ALL)
     assert np.array_equal(to_np(Y), (2 * ints.astype(np.float32)).astype(np.float16))
+
+
+@pytest.mark.parametrize("rows,cols,inplace", [(8192, 768, False), (10007, 520, True), (9000, 1024, False)])
+def test_layernorm_many_rows_against_oracle(lib, gpu, rows, cols, inplace):
+    """Row counts large enough for the pipelined LayerNorm (a fixed grid of waves walking the rows with two
+    rows of loads in flight), including a ragged last pass and the in-place form, against the oracle."""
+    x = data.normal((rows, cols), 41)
+    g, be = data.normal((1, cols), 42, 1.0, 0.02), data.normal((1, cols), 43, 0.0, 0.02)
+    X = to_dev(x)
+    Y = X if inplace else _empty(rows, cols)
+    lib.sh_layernorm(A(Y), A(X), A(to_dev(g)), A(to_dev(be)), rows, cols, cols, 1e-6, ALL)
+    bad, err, _ = refs.close(to_np(Y), refs.layernorm(x, g, be, 1e-6))
+    assert bad == 0, err
