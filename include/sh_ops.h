@@ -84,6 +84,16 @@ int sh_gemm_mesh(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uin
 /* sh_ops.h:88 (sh_gemm.inc.c:24-30): l1_base + (pipeline ? 2 : 1) * (tm*tk + tk*tn) * 2 + tm*tn*2. */
 uint32_t sh_gemm_l1_bytes(uint32_t M, uint32_t N, uint32_t K, const sh_gemm_cfg *cfg);
 
+/* Small-M GEMM (sh_ops.h:74-85): Z = X.W (+= with cfg->accumulate) with the reference's plan checks. cfg fields
+ * are "0 = auto" here: tm = rows per block (must divide M), tn = column granule (4), tk = K panel. Returns 0, -1
+ * (tm does not divide M / NULL), -2 (no plan fits the reference's scratch limit 0x90000 from l1_base), -3 (fmt). */
+enum { SH_XM_AUTO = 0, SH_XM_PANEL = 1, SH_XM_WHOLE = 2 };                                   /* sh_ops.h:79 */
+int sh_gemm_xmcast(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
+                   uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg);        /* sh_ops.h:80-81 */
+int sh_gemm_xmcast_ex(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
+                      uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg, uint32_t mode);  /* sh_ops.h:82-83 */
+uint32_t sh_gemm_xmcast_l1_bytes(uint32_t M, uint32_t N, uint32_t K, const sh_gemm_cfg *cfg, uint32_t mode);  /* sh_ops.h:84, ~0u: no plan */
+
 /* ---- row-wise / elementwise ops (sh_ops.h:90-100, runtime/sh_rowops.inc.c:383-465) -------------------
  * fp16 in/out, fp32 arithmetic, one pass over HBM. Parameter rows (gamma, beta, bias) are fp16 rows. */
 void sh_layernorm(uint64_t y, uint64_t x, uint64_t gamma, uint64_t beta, uint32_t rows, uint32_t cols, uint32_t ld, float eps, uint32_t cluster);  /* sh_ops.h:94 */

@@ -849,7 +849,7 @@ Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t wa
         if (!eligible(g_cfgs[i], vec, fast)) continue;
         uint32_t lo = 1, hi = 1;
         if (want_splits) lo = hi = want_splits;
-        else hi = std::max<uint32_t>(1, std::min<uint32_t>(8, K / 512));
+        else hi = std::max<uint32_t>(1, std::min<uint32_t>(16, K / 128));
         for (uint32_t s = lo; s <= hi; ++s) {
             const double tt = est_time(g_cfgs[i], M, N, K, s, cus);
             if (tt < bt * 0.97) { bt = tt; best = {i, s}; }
@@ -1079,3 +1079,81 @@ int sh_gemm_mesh(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uin
 }
 
 }  // extern "C"
+
+// ---- small-M GEMM (reference sh_gemm.inc.c:192-344) ----------------------------------------------------------
+// The reference streams each cluster's W column slice while X is multicast once over its mesh. On the GPU X (M <= a
+// few hundred rows) is re-read from L2 by every column tile and W crosses HBM once, so the work is the tiled GEMM
+// with a split count chosen for the few output tiles of a small M. The plan (column slice per cluster, K panel,
+// whole / panel schedule) and its TCDM bytes are computed exactly as the reference computes them, on its 16-cluster
+// mesh, so sh_gemm_xmcast_l1_bytes and the -1 / -2 / -3 answers match.
+namespace {
+constexpr uint32_t kXmClusters = 16;          // ARCH_NUM_CLUSTER_X * ARCH_NUM_CLUSTER_Y of the reference mesh
+constexpr uint32_t kXmL1Limit = 0x90000u;     // SH_XM_L1_LIMIT (sh_gemm.inc.c:210)
+constexpr uint32_t kXmWholeMax = 0x50000u;    // SH_XM_WHOLE_MAX (sh_gemm.inc.c:214)
+
+uint32_t xm_need(uint32_t rows, uint32_t K, uint32_t Nc, uint32_t tk, uint32_t whole) {   // sh_gemm.inc.c:219-221
+    return (whole ? rows * K * 2 : 2 * rows * tk * 2) + 2 * tk * Nc * 2 + rows * Nc * 2;
+}
+
+// 0 and *end = the scratch end offset, or a negative reason (sh_gemm.inc.c:223-251)
+int xm_plan(uint32_t M, uint32_t N, uint32_t K, const sh_gemm_cfg &c, uint32_t mode, uint32_t *end) {
+    const uint32_t g = c.tn ? c.tn : 4;
+    const uint32_t rows = c.tm ? c.tm : M;
+    if (rows == 0 || M % rows) return -1;
+    const uint32_t Nc = ((N + kXmClusters - 1) / kXmClusters + g - 1) / g * g;
+    if (c.l1_base >= kXmL1Limit) return -2;
+    const uint32_t lim = kXmL1Limit - c.l1_base;
+    const bool try_whole = mode == SH_XM_WHOLE || (mode == SH_XM_AUTO && rows * K * 2 <= kXmWholeMax);
+    for (int w = try_whole ? 1 : 0; w >= 0; --w) {
+        if (mode == SH_XM_WHOLE && !w) break;
+        uint32_t tk = 0;
+        if (c.tk) {
+            if (K % c.tk == 0 && xm_need(rows, K, Nc, c.tk, (uint32_t)w) <= lim) tk = c.tk;
+        } else {
+            for (uint32_t d = K < 256 ? K : 256; d; --d)
+                if (K % d == 0 && xm_need(rows, K, Nc, d, (uint32_t)w) <= lim) { tk = d; break; }
+        }
+        if (!tk) continue;
+        *end = c.l1_base + xm_need(rows, K, Nc, tk, (uint32_t)w);
+        return 0;
+    }
+    return -2;
+}
+
+void xm_cfg(sh_gemm_cfg *c, const sh_gemm_cfg *in) {   // fields 0 mean "auto" here (sh_gemm.inc.c:261)
+    if (in) *c = *in;
+    else { c->tm = c->tn = c->tk = 0; c->pipeline = 1; c->accumulate = 0; c->fmt = 0; c->l1_base = 0; }
+}
+}  // namespace
+
+extern "C" {
+
+uint32_t sh_gemm_xmcast_l1_bytes(uint32_t M, uint32_t N, uint32_t K, const sh_gemm_cfg *cfg, uint32_t mode) {
+    sh_gemm_cfg c;
+    xm_cfg(&c, cfg);
+    uint32_t end = 0;
+    return xm_plan(M, N, K, c, mode, &end) ? 0xFFFFFFFFu : end;
+}
+
+int sh_gemm_xmcast_ex(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
+                      uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg, uint32_t mode) {
+    sh_gemm_cfg c;
+    xm_cfg(&c, cfg);
+    uint32_t end = 0;
+    const int rc = (c.fmt & 3) ? -3 : xm_plan(M, N, K, c, mode, &end);
+    if (rc) {
+        sh_set_error(rc, "[sh_gemm_xmcast] %ux%ux%u tile %u,%u,%u mode %u: no plan (%d)", M, N, K, c.tm, c.tn, c.tk, mode, rc);
+        return rc;
+    }
+    if (!x || !w || !z) { sh_set_error(-1, "[sh_gemm_xmcast] NULL tensor address"); return -1; }
+    GemmReq r{x, w, z, M, N, K, ldx, ldw, ldz, c.accumulate, nullptr, 0, false};
+    return launch(r, "sh_gemm_xmcast");
+}
+
+int sh_gemm_xmcast(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
+                   uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg) {
+    return sh_gemm_xmcast_ex(x, w, z, M, N, K, ldx, ldw, ldz, cfg, SH_XM_AUTO);
+}
+
+}  // extern "C"
+

@@ -22,6 +22,7 @@ SH_ALL = 0xFFFFFFFF
 SH_FP16, SH_FP8, SH_INT16, SH_INT8 = 0, 1, 2, 3
 SH_EHIP = -3
 SH_ACT_NONE, SH_ACT_GELU = 0, 1
+SH_XM_AUTO, SH_XM_PANEL, SH_XM_WHOLE = 0, 1, 2
 SH_BIAS_FP16, SH_BIAS_FP32 = 0, 1
 SH_MESH_P = 4
 
@@ -51,6 +52,9 @@ _SIGS: dict[str, tuple] = {
     "sh_gemm": (i32, [u64, u64, u64, u32, u32, u32, u32, u32, u32, C.POINTER(sh_gemm_cfg), u32]),
     "sh_gemm_mesh": (i32, [u64, u64, u64, u32, u32, u32, u32, u32, u32, C.POINTER(sh_gemm_cfg)]),
     "sh_gemm_l1_bytes": (u32, [u32, u32, u32, C.POINTER(sh_gemm_cfg)]),
+    "sh_gemm_xmcast": (i32, [u64, u64, u64, u32, u32, u32, u32, u32, u32, C.POINTER(sh_gemm_cfg)]),
+    "sh_gemm_xmcast_ex": (i32, [u64, u64, u64, u32, u32, u32, u32, u32, u32, C.POINTER(sh_gemm_cfg), u32]),
+    "sh_gemm_xmcast_l1_bytes": (u32, [u32, u32, u32, C.POINTER(sh_gemm_cfg), u32]),
     "sh_gemm_splitk": (i32, [u64, u64, u64, u32, u32, u32, u32, u32, u32, C.POINTER(sh_gemm_cfg), u32, u32]),
     "sh_gemm_ex": (i32, [u64, u64, u64, u32, u32, u32, u32, u32, u32, C.POINTER(sh_gemm_cfg), C.POINTER(sh_gemm_epi)]),
     # row ops

@@ -92,6 +92,37 @@ def test_gemm_argument_errors_without_gpu(lib):
     assert lib.sh_gemm_ex(one, one, one, 16, 32, 16, 16, 32, 32, None, e) == -1                 # ldr < N
 
 
+def test_xmcast_plan_follows_the_reference_schedules(lib):
+    """sh_gemm_xmcast_l1_bytes / plan (sh_gemm.inc.c:219-258) against what docs/XPANEL_MCAST.md reports: the column
+    slice of N=1600 on 16 clusters is 100 (1600/16 rounded up to the granule 4), K panels are the largest divisor
+    of K <= 256 that fits, and AUTO picks the whole-X schedule up to 320 KB of X (50x1600x720, 200x1600x720) and
+    panels above it (200x720x960: X = 384 KB; 400x1600x720)."""
+    X, P, W = shops.SH_XM_AUTO, shops.SH_XM_PANEL, shops.SH_XM_WHOLE
+    # whole X, M=50, N=1600, K=720: X 72000 B + two W panels (tk=240, Nc=100) + Y (50 x 100)
+    assert lib.sh_gemm_xmcast_l1_bytes(50, 1600, 720, None, W) == 50 * 720 * 2 + 2 * 240 * 100 * 2 + 50 * 100 * 2
+    for m, n, k, whole in ((50, 1600, 720, True), (200, 1600, 720, True), (200, 720, 960, False), (400, 1600, 720, False)):
+        auto = lib.sh_gemm_xmcast_l1_bytes(m, n, k, None, X)
+        assert auto == lib.sh_gemm_xmcast_l1_bytes(m, n, k, None, W if whole else P) != 0xFFFFFFFF
+    # panel schedule of 200x720x960: Nc = ceil(720/16)=45 -> 48; tk = 240 (largest divisor of 960 <= 256)
+    assert lib.sh_gemm_xmcast_l1_bytes(200, 720, 960, None, P) == 2 * 200 * 240 * 2 + 2 * 240 * 48 * 2 + 200 * 48 * 2
+    # explicit tk must divide K; rows per block must divide M; l1_base at the limit leaves no plan
+    assert lib.sh_gemm_xmcast_l1_bytes(50, 1600, 720, shops.cfg(0, 0, 7), P) == 0xFFFFFFFF
+    assert lib.sh_gemm_xmcast_l1_bytes(50, 1600, 720, shops.cfg(16, 0, 0), P) == 0xFFFFFFFF
+    assert lib.sh_gemm_xmcast_l1_bytes(50, 1600, 720, shops.cfg(l1_base=0x90000), P) == 0xFFFFFFFF
+    # whole X of 50 x 8192 x 2 = 800 KB cannot fit: WHOLE has no plan, AUTO falls back to panels
+    assert lib.sh_gemm_xmcast_l1_bytes(50, 256, 8192, None, W) == 0xFFFFFFFF
+    assert lib.sh_gemm_xmcast_l1_bytes(50, 256, 8192, None, X) == lib.sh_gemm_xmcast_l1_bytes(50, 256, 8192, None, P)
+
+
+def test_xmcast_argument_errors_without_gpu(lib):
+    one = 1 << 20
+    assert lib.sh_gemm_xmcast_ex(one, one, one, 50, 64, 64, 64, 64, 64, shops.cfg(16, 0, 0), shops.SH_XM_AUTO) == -1
+    assert lib.sh_gemm_xmcast_ex(one, one, one, 50, 64, 64, 64, 64, 64, shops.cfg(l1_base=0x90000), 0) == -2
+    assert lib.sh_gemm_xmcast(one, one, one, 50, 64, 64, 64, 64, 64, shops.cfg(fmt=shops.SH_FP8)) == -3
+    assert shops.last_error()[0] == -3
+    assert lib.sh_gemm_xmcast(0, one, one, 50, 64, 64, 64, 64, 64, None) == -1
+
+
 def test_attention_argument_errors_without_gpu(lib):
     one = 1 << 20
     assert lib.sh_attention(one, one, one, one, 256, 768, 7, 768, 768, 768, 768, 0.125, shops.SH_ALL) == -1  # D % H

@@ -288,3 +288,29 @@ def test_large_encoder_shape_property(lib, gpu):
     Z = torch.empty((M, K), dtype=torch.float16, device="cuda")
     assert lib.sh_gemm(A(X), A(I), A(Z), M, K, K, K, K, K, None, shops.SH_ALL) == 0
     assert np.array_equal(codes(Z), x.view(np.uint16))
+
+
+@pytest.mark.parametrize("M,N,K,mode,tm,acc", [(50, 1600, 720, 0, 0, 0), (200, 720, 960, 1, 0, 0), (241, 960, 960, 0, 0, 0),
+                                               (50, 720, 2048, 2, 25, 1), (200, 4096, 720, 0, 0, 0)])
+def test_xmcast_small_m_shapes(lib, gpu, M, N, K, mode, tm, acc):
+    """sh_gemm_xmcast_ex on the small-M GEMM shapes of docs/XPANEL_MCAST.md section 3 (SmolVLA expert and prefix),
+    every schedule mode, rows-per-block and accumulate; integer-valued data as the reference's run (exact), and
+    normal data against the fp32 product."""
+    import torch
+    for fill in ("int", "normal"):
+        if fill == "int":
+            x, w = lcg.fill_fp16(M, K, 81, -2, 2), lcg.fill_fp16(K, N, 82, -2, 2)
+        else:
+            x, w = data.normal((M, K), 83), data.normal((K, N), 84, std=1 / np.sqrt(K))
+        z0 = lcg.fill_fp16(M, N, 85, -3, 3)
+        X, W, Z = to_dev(x), to_dev(w), to_dev(z0)
+        rc = lib.sh_gemm_xmcast_ex(A(X), A(W), A(Z), M, N, K, K, N, N, shops.cfg(tm, 0, 0, accumulate=acc), mode)
+        assert rc == 0, shops.last_error()
+        # accumulate stores r16(z0 + r16(X W)) (the product is rounded where sh_gemm would store it)
+        want = refs.r16(refs.gemm(x, w)) + z0.astype(np.float32) if acc else refs.gemm(x, w)
+        got = to_np(Z)
+        if fill == "int":
+            assert np.array_equal(got.astype(np.float32), refs.r16(want))
+        else:
+            bad, err, _ = refs.close(got, want)
+            assert bad == 0, err
