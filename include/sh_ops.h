@@ -119,6 +119,23 @@ uint32_t sh_attention_q_block(uint32_t S, uint32_t dh, uint32_t H, uint32_t P); 
 /* sh_ops.h:127: ns stamps of the last attention call: 7 entry, 0 kernel start, 1..5 = 0, 6 kernel end. */
 uint32_t sh_attention_profile(uint32_t S, uint32_t dh, uint32_t phase);
 
+/* ---- Llama-style decoder ops (sh_ops.h:277-307, runtime/sh_llm.inc.c) -----------------------------------
+ * Token masks: tok[j] (uint16, one per position) is the cumulative attention-block id of position j, SH_LLM_PAD
+ * for padding; query i attends key j iff tok[j] <= tok[i] (unsigned). A padding query row (or one with no allowed
+ * key) is uniform. Row ops need cols % 4 == 0 (and cols <= 8192 here); violations set sh_last_error and return. */
+#define SH_LLM_PAD 0xFFFFu                                                                         /* sh_ops.h:283 */
+void sh_rmsnorm(uint64_t y, uint64_t x, uint64_t gamma, uint32_t rows, uint32_t cols, uint32_t ld, float eps, uint32_t cluster);  /* sh_ops.h:284 */
+void sh_rope(uint64_t y, uint64_t x, uint64_t cos_sin, uint32_t rows, uint32_t cols, uint32_t ld, uint32_t ld_table, uint32_t dh,
+             uint32_t cluster);                                                                    /* sh_ops.h:288, rotate-half */
+void sh_silu_mul(uint64_t y, uint64_t a, uint64_t b, uint32_t rows, uint32_t cols, uint32_t ld, uint32_t cluster);  /* sh_ops.h:289 */
+void sh_softmax_masked(uint64_t y, uint64_t x, uint32_t rows, uint32_t cols, uint32_t ld, float scale, uint64_t tok_q,
+                       uint64_t tok_k, uint32_t cluster);                                          /* sh_ops.h:292, scale > 0 */
+int sh_attention_head_masked(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t S, uint32_t dh, uint32_t ldq,
+                             uint32_t ldk, uint32_t ldv, uint32_t ldo, float scale, uint64_t tok, uint32_t cluster);  /* sh_ops.h:294-295 */
+int sh_attention_gqa(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t S, uint32_t D, uint32_t H, uint32_t Hkv,
+                     uint32_t ldq, uint32_t ldk, uint32_t ldv, uint32_t ldo, float scale, uint64_t tok, uint32_t cluster);  /* sh_ops.h:299-300 */
+void sh_pixel_shuffle(uint64_t dst, uint64_t src, uint32_t grid, uint32_t D, uint32_t s, uint32_t cluster);  /* sh_ops.h:303, bit-exact */
+
 /* ---- test helpers (sh_ops.h:220-240, runtime/sh_test.inc.c, runtime/sh_rt.inc.c:31-59) ----------------
  * Fills run as GPU kernels (LCG jump-ahead per element, identical values to the sequential loop); dumps
  * gather on the GPU and print on the host in the reference's "<tag> r c hex" format. */

@@ -7,6 +7,8 @@ Sources (runwangdl/softhier-mlir):
              subtraction, tanh-GELU, add, add_bias (per column), scale, transpose; siglip_ref.py:20-22, 42
   attention  tests/gvsoc/run.py:921-934   s = r16(q k^T) * scale; p = r16(softmax(s)); o = r16(p v)
   encoder    softhier_mlir/testing/siglip_ref.py:9-45 with the op order of frontend/siglip.py:133-168
+  llm ops    tests/gvsoc/run.py:175-235   RMSNorm, RoPE (rotate-half), silu(a) b, token-masked softmax, GQA
+             attention (semantics of runtime/sh_ops.h:277-304)
 """
 from __future__ import annotations
 
@@ -156,6 +158,87 @@ def encoder_stack(x, params: list[dict], heads: int, B: int = 1, eps: float = 1e
 
 
 # ---- tolerance ------------------------------------------------------------------------------------------
+# ---- Llama-style decoder ops (run.py:175-235; sh_ops.h:277-304) ----------------------------------------
+LLM_PAD = 0xFFFF
+
+
+def rmsnorm(x, g, eps: float) -> np.ndarray:
+    """x / sqrt(mean(x^2) + eps) * g per row (run.py:232, HF LlamaRMSNorm; fp32 statistics)."""
+    x = f32(x)
+    return x / np.sqrt((x * x).mean(1, keepdims=True) + eps) * f32(g)
+
+
+def rope(x, table, dh: int) -> np.ndarray:
+    """HF rotate-half RoPE on every dh-wide head of each row (run.py:233-234): table row = cos[dh/2] | sin[dh/2]
+    for that row's position; y1 = x1 cos - x2 sin, y2 = x2 cos + x1 sin."""
+    x, t = f32(x), f32(table)
+    S, D = x.shape
+    xh = x.reshape(S, D // dh, dh)
+    x1, x2 = xh[..., :dh // 2], xh[..., dh // 2:]
+    c, s = t[:, None, :dh // 2], t[:, None, dh // 2:dh]
+    return np.concatenate([x1 * c - x2 * s, x2 * c + x1 * s], -1).reshape(S, D)
+
+
+def silu_mul(a, b) -> np.ndarray:
+    """silu(a) * b = a / (1 + e^-a) * b (run.py:235)."""
+    a = f32(a)
+    return a / (1 + np.exp(-a)) * f32(b)
+
+
+def llm_tokens(S: int, kind: str) -> np.ndarray:
+    """Token classes of the reference's llmops driver (run.py:175-183 == llmops/main.c tok_prefix): causal
+    tok[j] = j; prefix: image tokens 0, the first 5 language tokens 0, the rest PAD, the state token 1."""
+    if kind == "causal":
+        return np.arange(S, dtype=np.uint32)
+    img = S - 64
+    tok = np.full(S, LLM_PAD, dtype=np.uint32)
+    tok[:img] = 0
+    tok[img:img + 5] = 0
+    tok[img + 48] = 1
+    return tok
+
+
+def softmax_masked(x, scale: float, tok_q, tok_k) -> np.ndarray:
+    """softmax(scale x) over the keys j with tok_k[j] <= tok_q[i] (unsigned); a PAD query row (or one with no
+    allowed key) is uniform (run.py:186-196)."""
+    x = f32(x)
+    tq, tk = np.asarray(tok_q, np.int64), np.asarray(tok_k, np.int64)
+    allowed = (tk[None, :] <= tq[:, None]) & (tq[:, None] != LLM_PAD)
+    z = np.where(allowed, scale * x, -np.inf)
+    m = np.where(allowed.any(1, keepdims=True), z.max(1, keepdims=True, initial=-np.inf), 0.0)
+    e = np.where(allowed, np.exp(z - m), 0.0)
+    s = e.sum(1, keepdims=True)
+    return np.where(s > 0, e / np.where(s > 0, s, 1.0), 1.0 / x.shape[1]).astype(F32)
+
+
+def attention_gqa(q, k, v, H: int, Hkv: int, tok=None, scale: float = 0.125) -> np.ndarray:
+    """H query heads over Hkv key/value heads (head h reads kv head h // (H / Hkv)), optional token mask
+    (run.py:199-216): s = r16(q k^T), p = masked softmax(scale s) (plain softmax without a mask), o = r16(r16(p) v)."""
+    q, k, v = f32(q), f32(k), f32(v)
+    S, D = q.shape
+    dh, grp = D // H, H // Hkv
+    o = np.zeros((S, D), F32)
+    for hd in range(H):
+        sl, kv = slice(hd * dh, (hd + 1) * dh), slice((hd // grp) * dh, (hd // grp + 1) * dh)
+        s = r16(q[:, sl] @ k[:, kv].T)
+        if tok is None:
+            p = np.exp(scale * s - (scale * s).max(1, keepdims=True))
+            p = p / p.sum(1, keepdims=True)
+        else:
+            p = softmax_masked(s, scale, tok, tok)
+        o[:, sl] = r16(r16(p) @ v[:, kv])
+    return o
+
+
+def pixel_shuffle(src: np.ndarray, grid: int, s: int) -> np.ndarray:
+    """[grid^2, D] raster patch tokens -> [(grid/s)^2, D s^2]: output token (gr, gb) = the s x s patch block at
+    rows gr s.., cols gb s.., row-major (sh_ops.h:305-307, SmolVLMConnector.pixel_shuffle). Bit-exact."""
+    D = src.shape[1]
+    g = grid // s
+    blocks = src.reshape(g, s, g, s, D).transpose(0, 2, 1, 3, 4)        # [gr, gb, i, j, D]
+    return blocks.reshape(g * g, s * s * D)
+
+
 def close(got, want, atol: float = 2e-2, rtol: float = 1e-2) -> tuple[int, float, float]:
     """(elements outside |got - want| <= atol + rtol |want|, max abs error, max |want|)."""
     got, want = f32(got), f32(want)

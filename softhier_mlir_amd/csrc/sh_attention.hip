@@ -34,7 +34,10 @@ struct AttnArgs {
     uint64_t bsq, bsk, bsv, bso;    // batch strides (elements)
     uint32_t S, dh;
     float c;                        // scale * log2(e)
+    const uint16_t *tok;            // token classes of the S positions (sh_ops.h:277-282), or null: no mask
+    uint32_t grp;                   // query heads per key/value head (GQA); 1 for plain multi-head attention
 };
+constexpr uint32_t kLlmPad = 0xFFFFu;   // SH_LLM_PAD: a padding position
 
 template <int DH>
 __device__ __forceinline__ uint32_t kswz(uint32_t r) {
@@ -71,8 +74,8 @@ __global__ __launch_bounds__(256) void k_flash(AttnArgs a) {
     const uint32_t b = blockIdx.z, h = blockIdx.y;
     const uint32_t S = a.S, dh = a.dh;
     const uint16_t *Q = a.q + b * a.bsq + (uint64_t)h * dh;
-    const uint16_t *Kp = a.k + b * a.bsk + (uint64_t)h * dh;
-    const uint16_t *Vp = a.v + b * a.bsv + (uint64_t)h * dh;
+    const uint16_t *Kp = a.k + b * a.bsk + (uint64_t)(h / a.grp) * dh;
+    const uint16_t *Vp = a.v + b * a.bsv + (uint64_t)(h / a.grp) * dh;
     uint16_t *O = a.o + b * a.bso + (uint64_t)h * dh;
     const uint32_t qw0 = blockIdx.x * QPB + wave * QPW;    // first query of this wavefront
     const uint32_t myq = qw0 + r32;
@@ -281,8 +284,8 @@ __global__ __launch_bounds__(256) void k_flash_dma(AttnArgs a) {
     const uint32_t b = blockIdx.z, h = blockIdx.y;
     const uint32_t S = a.S;
     const uint16_t *Q = a.q + b * a.bsq + (uint64_t)h * DH;
-    const uint16_t *Kp = a.k + b * a.bsk + (uint64_t)h * DH;
-    const uint16_t *Vp = a.v + b * a.bsv + (uint64_t)h * DH;
+    const uint16_t *Kp = a.k + b * a.bsk + (uint64_t)(h / a.grp) * DH;
+    const uint16_t *Vp = a.v + b * a.bsv + (uint64_t)(h / a.grp) * DH;
     uint16_t *O = a.o + b * a.bso + (uint64_t)h * DH;
     const uint32_t qw0 = blockIdx.x * QPB + wave * QPW, myq = qw0 + r32;
     const uint32_t nkb = (S + KB - 1) / KB;
@@ -427,7 +430,7 @@ __global__ __launch_bounds__(256) void k_flash_dma(AttnArgs a) {
 // maximum known, needs no running rescale of O or l: p = 2^(c s - m), P (fp16) feeds O^T += V^T . P^T, and
 // the row sums l come from one more MFMA with an all-ones A operand (the sums of the fp16 numerators the
 // PV product used). Masking of keys past S happens only in the last, partial key block.
-template <int DH, int NST>
+template <int DH, int NST, bool MASK>
 __global__ __launch_bounds__(256) void k_flash2(AttnArgs a) {
     constexpr int DC = DH / 8, NS = DH / 16, DT = DH / 32;
     constexpr int KCH = KB * DC;                     // 16-byte chunks per K (or V) block
@@ -441,12 +444,16 @@ __global__ __launch_bounds__(256) void k_flash2(AttnArgs a) {
     const uint32_t b = blockIdx.z, h = blockIdx.y;
     const uint32_t S = a.S;
     const uint16_t *Q = a.q + b * a.bsq + (uint64_t)h * DH;
-    const uint16_t *Kp = a.k + b * a.bsk + (uint64_t)h * DH;
-    const uint16_t *Vp = a.v + b * a.bsv + (uint64_t)h * DH;
+    const uint16_t *Kp = a.k + b * a.bsk + (uint64_t)(h / a.grp) * DH;
+    const uint16_t *Vp = a.v + b * a.bsv + (uint64_t)(h / a.grp) * DH;
     uint16_t *O = a.o + b * a.bso + (uint64_t)h * DH;
     const uint32_t qw0 = blockIdx.x * QPB + wave * QPW, myq = qw0 + r32;
     const uint32_t nkb = (S + KB - 1) / KB;
     const bool ragged = S % KB != 0;                 // the last key block is partial
+    // token mask (MASK): key j is allowed for this lane's query iff tok[j] <= tok[query]; a padding query (or
+    // one with no allowed key, found in pass 1) averages V uniformly over the S keys
+    const uint32_t tq = MASK ? (myq < S ? (uint32_t)a.tok[myq] : kLlmPad) : 0u;
+    bool uni = MASK && tq == kLlmPad;
 
     const uint16_t *kcol[KR];
     const uint16_t *vcol[KR];
@@ -489,7 +496,12 @@ __global__ __launch_bounds__(256) void k_flash2(AttnArgs a) {
             }
         }
     };
-    auto key_ok = [&](uint32_t kb, int tt, int r) { return kb * KB + 32 * tt + 8 * (r >> 2) + 4 * g + (r & 3) < S; };
+    auto key_of = [&](uint32_t kb, int tt, int r) { return kb * KB + 32 * tt + 8 * (r >> 2) + 4 * g + (r & 3); };
+    auto key_ok = [&](uint32_t kb, int tt, int r) {
+        const uint32_t key = key_of(kb, tt, r);
+        if (!MASK) return key < S;
+        return key < S && (uint32_t)a.tok[min(key, S - 1)] <= tq;
+    };
 
     // ---- pass 1: extreme of s over all keys (max for c >= 0, min for c < 0), K blocks only ----
     const bool pos = a.c >= 0.f;
@@ -502,7 +514,7 @@ __global__ __launch_bounds__(256) void k_flash2(AttnArgs a) {
         issue(min(kb + NST - 1, nkb - 1), (int)((kb + NST - 1) % NST), false);
         sh_f16v sacc[2];
         scores((int)(kb % NST), sacc);
-        if (ragged && kb == nkb - 1) {
+        if (MASK || (ragged && kb == nkb - 1)) {
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -522,7 +534,8 @@ __global__ __launch_bounds__(256) void k_flash2(AttnArgs a) {
         }
     }
     ext = pos ? fmaxf(ext, __shfl_xor(ext, 32, 64)) : fminf(ext, __shfl_xor(ext, 32, 64));
-    const float m = a.c * ext;                       // max over keys of c s
+    if (MASK) uni = uni || ext == -INFINITY;
+    const float m = (MASK && uni) ? 0.f : a.c * ext;   // max over keys of c s
     attn_wait_vmcnt<0>();                            // the ring is idle before pass 2 refills it
     __syncthreads();
 
@@ -550,7 +563,12 @@ __global__ __launch_bounds__(256) void k_flash2(AttnArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 float p = sh_fast_exp2(fmaf(sacc[tt][r], a.c, -m));
-                if (tail && !key_ok(kb, tt, r)) p = 0.f;
+                if (MASK) {
+                    if (uni) p = key_of(kb, tt, r) < S ? 1.f : 0.f;
+                    else if (!key_ok(kb, tt, r)) p = 0.f;
+                } else if (tail && !key_ok(kb, tt, r)) {
+                    p = 0.f;
+                }
                 pf[2 * tt + (r >> 3)][r & 7] = (_Float16)p;
             }
         const uint32_t vbase = lds0 + (uint32_t)st * STAGE + KCH * 16;
@@ -599,14 +617,19 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
     __shared__ float red[4];
     const uint32_t qi = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const uint16_t *Q = a.q + b * a.bsq + (uint64_t)h * a.dh + (uint64_t)qi * a.ldq;
-    const uint16_t *Kp = a.k + b * a.bsk + (uint64_t)h * a.dh;
-    const uint16_t *Vp = a.v + b * a.bsv + (uint64_t)h * a.dh;
+    const uint16_t *Kp = a.k + b * a.bsk + (uint64_t)(h / a.grp) * a.dh;
+    const uint16_t *Vp = a.v + b * a.bsv + (uint64_t)(h / a.grp) * a.dh;
     uint16_t *O = a.o + b * a.bso + (uint64_t)h * a.dh + (uint64_t)qi * a.ldo;
+    // token mask: key j is allowed for query qi iff tok[j] <= tok[qi]; a padding query, or one with no allowed
+    // key, averages V uniformly
+    const uint32_t tq = a.tok ? a.tok[qi] : 0u;
+    bool uni = a.tok && tq == kLlmPad;
     float mx = -INFINITY;
     for (uint32_t j = threadIdx.x; j < a.S; j += 256) {
         float s = 0.f;
         for (uint32_t d = 0; d < a.dh; ++d) s += sh_dev_h2f(Q[d]) * sh_dev_h2f(Kp[(uint64_t)j * a.ldk + d]);
         s *= a.c;
+        if (a.tok && a.tok[j] > tq) s = -INFINITY;
         sc[j] = s;
         mx = fmaxf(mx, s);
     }
@@ -615,8 +638,13 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     __syncthreads();
+    uni = uni || mx == -INFINITY;
     float sum = 0.f;
-    for (uint32_t j = threadIdx.x; j < a.S; j += 256) { const float p = sh_fast_exp2(sc[j] - mx); sc[j] = p; sum += p; }
+    for (uint32_t j = threadIdx.x; j < a.S; j += 256) {
+        const float p = uni ? 1.f : (sc[j] == -INFINITY ? 0.f : sh_fast_exp2(sc[j] - mx));
+        sc[j] = p;
+        sum += p;
+    }
     sum = sh_wave_sum(sum);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sum;
     __syncthreads();
@@ -647,12 +675,13 @@ int check_ref(uint32_t S, uint32_t dh, uint32_t sq) {          // sh_attention.i
 }
 
 int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, uint32_t dh, uint32_t H,
-        uint32_t ldq, uint32_t ldk, uint32_t ldv, uint32_t ldo, uint64_t bsq, uint64_t bsk, uint64_t bsv, uint64_t bso, float scale) {
+        uint32_t ldq, uint32_t ldk, uint32_t ldv, uint32_t ldo, uint64_t bsq, uint64_t bsk, uint64_t bsv, uint64_t bso, float scale,
+        uint64_t tok = 0, uint32_t grp = 1) {
     if (!q || !k || !v || !o) { sh_set_error(-1, "[sh_attention] NULL tensor address"); return -1; }
     if (B == 0 || S == 0 || H == 0 || dh == 0) return 0;
     if (H > 65535 || B > 65535) { sh_set_error(-1, "[sh_attention] H=%u or B=%u above 65535", H, B); return -1; }
     AttnArgs a{(const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)v, (uint16_t *)o,
-               ldq, ldk, ldv, ldo, bsq, bsk, bsv, bso, S, dh, scale * 1.4426950408889634f};
+               ldq, ldk, ldv, ldo, bsq, bsk, bsv, bso, S, dh, scale * 1.4426950408889634f, (const uint16_t *)tok, grp};
     hipStream_t st = sh_stream();
     if (!g_prof.e0) {
         if (!sh_hip_ok(hipEventCreate(&g_prof.e0), "hipEventCreate") || !sh_hip_ok(hipEventCreate(&g_prof.e1), "hipEventCreate")) return SH_EHIP;
@@ -671,9 +700,17 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
                      sh_aligned16(q) && sh_aligned16(k) && sh_aligned16(v) && sh_aligned16(o);
     static const int impl = [] { const char *e = getenv("SH_ATTN_IMPL"); return (e && *e) ? atoi(e) : 0; }();
     const dim3 grid(sh_cdiv(S, QPB), H, B);
-    if ((dh == 64 || dh == 128) && vec && impl == 0) {
-        if (dh == 64) go(k_flash2<64, 4>, grid, 0);
-        else go(k_flash2<128, 2>, grid, 0);
+    if (tok && (dh == 64 || dh == 128) && vec) {
+        if (dh == 64) go(k_flash2<64, 4, true>, grid, 0);
+        else go(k_flash2<128, 2, true>, grid, 0);
+    } else if (tok) {
+        if (S > 16384) { sh_set_error(-1, "[sh_attention] masked heads with dh=%u support S <= 16384", dh); return -1; }
+        static bool attr_m = false;
+        if (!attr_m) { (void)hipFuncSetAttribute((const void *)k_attn_rows, hipFuncAttributeMaxDynamicSharedMemorySize, 16384 * 4); attr_m = true; }
+        go(k_attn_rows, dim3(S, H, B), S * sizeof(float));
+    } else if ((dh == 64 || dh == 128) && vec && impl == 0) {
+        if (dh == 64) go(k_flash2<64, 4, false>, grid, 0);
+        else go(k_flash2<128, 2, false>, grid, 0);
     } else if ((dh == 64 || dh == 128) && vec && impl == 1) {
         if (dh == 64) go(k_flash_dma<64, 4>, grid, 0);
         else go(k_flash_dma<128, 2>, grid, 0);
@@ -706,6 +743,20 @@ uint32_t q_block_rule(uint32_t S, uint32_t dh, uint32_t H, uint32_t P) {   // sh
         if (!best || rows < best_rows) { best = sq; best_rows = rows; }
     }
     return best;
+}
+
+// The reference's masked head keeps the whole head resident (sh_llm.inc.c:250-272): S <= 256, S % 4, dh % 4,
+// scale > 0, and its TCDM (head layout + the token array + one 4-class mask cache per core, 3 cores) must fit.
+int check_masked(const char *op, uint32_t S, uint32_t dh, float scale) {
+    const uint32_t end = l1_bytes_q(S, dh, S);
+    const uint32_t ltok = (end + 63) & ~63u, lcls = ltok + ((S * 2 + 63) & ~63u);
+    const uint32_t clsb = (64u + 4u * 2u * S * 2u + 63) & ~63u, lend = lcls + 3u * clsb;
+    if (S > 256 || (S & 3) || (dh & 3) || dh == 0 || !(scale > 0.f) || lend > SH_REF_TCDM_BYTES) {
+        sh_set_error(-1, "[%s] S=%u dh=%u: need S <= 256, S %% 4 == 0, dh %% 4 == 0, scale > 0, L1 %u <= %u",
+                     op, S, dh, lend, SH_REF_TCDM_BYTES);
+        return -1;
+    }
+    return 0;
 }
 
 }  // namespace
@@ -744,6 +795,23 @@ int sh_attention_batched(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_
     if (H == 0 || dh * H != D) { sh_set_error(-1, "[sh_attention_batched] D=%u not divisible by H=%u", D, H); return -1; }
     if (sq && S % sq) { sh_set_error(-1, "[sh_attention_batched] sq=%u does not divide S=%u", sq, S); return -1; }
     return run(q, k, v, o, B, S, dh, H, ldq, ldk, ldv, ldo, bsq, bsk, bsv, bso, scale);
+}
+
+int sh_attention_head_masked(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t S, uint32_t dh,
+                             uint32_t ldq, uint32_t ldk, uint32_t ldv, uint32_t ldo, float scale, uint64_t tok, uint32_t) {
+    if (check_masked("sh_attention_head_masked", S, dh, scale)) return -1;
+    return run(q, k, v, o, 1, S, dh, 1, ldq, ldk, ldv, ldo, 0, 0, 0, 0, scale, tok, 1);
+}
+
+int sh_attention_gqa(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t S, uint32_t D, uint32_t H, uint32_t Hkv,
+                     uint32_t ldq, uint32_t ldk, uint32_t ldv, uint32_t ldo, float scale, uint64_t tok, uint32_t) {
+    const uint32_t dh = H ? D / H : 0;
+    if (H == 0 || Hkv == 0 || dh * H != D || H % Hkv) {                 // sh_llm.inc.c:327-331
+        sh_set_error(-1, "[sh_attention_gqa] bad D=%u H=%u Hkv=%u", D, H, Hkv);
+        return -1;
+    }
+    if (check_masked("sh_attention_gqa", S, dh, scale)) return -1;      // every head fails the same way (:333-337)
+    return run(q, k, v, o, 1, S, dh, H, ldq, ldk, ldv, ldo, 0, 0, 0, 0, scale, tok, H / Hkv);
 }
 
 uint32_t sh_attention_profile(uint32_t, uint32_t, uint32_t phase) {

@@ -14,7 +14,7 @@
 namespace {
 
 constexpr int kRowWaves = 4;          // rows per 256-thread block
-enum { OP_GELU = 0, OP_ADD = 1, OP_BIAS = 2, OP_SCALE = 3 };
+enum { OP_GELU = 0, OP_ADD = 1, OP_BIAS = 2, OP_SCALE = 3, OP_SILU_MUL = 4 };
 
 __device__ __forceinline__ void unpack8(const uint4 q, float *f) {
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
@@ -230,6 +230,10 @@ __global__ __launch_bounds__(256) void k_softmax_wide(uint16_t *y, const uint16_
 template <int OP>
 __device__ __forceinline__ float ew(float a, float b, float s) {
     if (OP == OP_SCALE) return a * s;
+    if (OP == OP_SILU_MUL) {   // a b / (1 + 2^t), t = -a log2(e) clamped to [-14, 15] (sh_llm.inc.c:152-167)
+        const float t = fminf(fmaxf(-a * 1.4426950408889634f, -14.f), 15.f);
+        return a * b * sh_fast_rcp(1.f + sh_fast_exp2(t));
+    }
     return a + b;   // OP_ADD, OP_BIAS (rounded once to fp16 by the caller)
 }
 
@@ -253,7 +257,7 @@ __global__ __launch_bounds__(256) void k_elementwise(uint16_t *y, const uint16_t
             const uint32_t r = sh_div(itc, div), cc = itc - r * per_row;
             off[u] = r * ld + 8ull * cc;
             ra[u] = *(const uint4 *)(a + off[u]);
-            if (OP == OP_ADD) rb[u] = *(const uint4 *)(b + off[u]);
+            if (OP == OP_ADD || OP == OP_SILU_MUL) rb[u] = *(const uint4 *)(b + off[u]);
             else if (OP == OP_BIAS) rb[u] = *(const uint4 *)(b + 8ull * cc);
             else rb[u] = make_uint4(0, 0, 0, 0);
         }
@@ -281,7 +285,7 @@ __global__ __launch_bounds__(256) void k_elementwise(uint16_t *y, const uint16_t
         const uint32_t r = sh_div(it, div), cc = it - r * per_row;
         const uint64_t off = r * ld + cc;
         float fb = 0.f;
-        if (OP == OP_ADD) fb = sh_dev_h2f(b[off]);
+        if (OP == OP_ADD || OP == OP_SILU_MUL) fb = sh_dev_h2f(b[off]);
         else if (OP == OP_BIAS) fb = sh_dev_h2f(b[cc]);
         if (OP == OP_GELU) {
             const uint32_t h = a[off];
@@ -396,12 +400,141 @@ void launch_elementwise(int op, uint64_t y, uint64_t a, uint64_t b, uint32_t row
         case OP_GELU: SH_EW(OP_GELU); break;
         case OP_ADD: SH_EW(OP_ADD); break;
         case OP_BIAS: SH_EW(OP_BIAS); break;
+        case OP_SILU_MUL: SH_EW(OP_SILU_MUL); break;
         default: SH_EW(OP_SCALE); break;
     }
 #undef SH_EW
     sh_launch_ok(name);
 }
 
+
+// ---- Llama-style decoder row ops (reference runtime/sh_llm.inc.c) ------------------------------------------
+constexpr uint32_t kLlmPad = 0xFFFFu;      // SH_LLM_PAD
+__device__ __forceinline__ uint32_t comp4r(const uint4 &q, int i) { return i == 0 ? q.x : i == 1 ? q.y : i == 2 ? q.z : q.w; }
+
+// y = x rsqrt(mean(x^2) + eps) gamma per row, fp32 statistics (sh_llm.inc.c:91-120). Same layout as k_layernorm.
+template <int NCH, bool VEC>
+__global__ __launch_bounds__(256) void k_rmsnorm(uint16_t *y, const uint16_t *x, const uint16_t *gamma, uint32_t rows,
+                                                 uint32_t cols, uint64_t ld, float eps) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t row = blockIdx.x * kRowWaves + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    float v[NCH][8], g[NCH][8];
+    if (VEC) {
+        uint4 rx[NCH], rg[NCH];
+        load_raw<NCH>(x + row * ld, cols, lane, rx);
+        load_raw<NCH>(gamma, cols, lane, rg);
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) { pin4(rx[u]); pin4(rg[u]); }
+        unpack_row<NCH>(rx, cols, lane, v);
+        unpack_row<NCH>(rg, cols, lane, g);
+    } else {
+        load_row<NCH, VEC>(x + row * ld, cols, lane, v);
+        load_row<NCH, VEC>(gamma, cols, lane, g);
+    }
+    float q = 0.f;
+#pragma unroll
+    for (int u = 0; u < NCH; ++u)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q += v[u][i] * v[u][i];
+    const float rs = sh_fast_rsq(sh_wave_sum(q) / (float)cols + eps);
+#pragma unroll
+    for (int u = 0; u < NCH; ++u)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[u][i] = v[u][i] * rs * g[u][i];
+    store_row<NCH, VEC>(y + row * ld, cols, lane, v);
+}
+
+// softmax(scale x) per row over the keys j with tok_k[j] <= tok_q[row] (unsigned); a padding query row, or one
+// with no allowed key, is uniform 1/cols (sh_llm.inc.c:175-248; run.py:186-196). c = scale log2(e) > 0.
+template <int NCH, bool VEC>
+__global__ __launch_bounds__(256) void k_softmax_masked(uint16_t *y, const uint16_t *x, uint32_t rows, uint32_t cols, uint64_t ld,
+                                                        float c, const uint16_t *tok_q, const uint16_t *tok_k) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t row = blockIdx.x * kRowWaves + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const uint32_t ti = tok_q[row];
+    float v[NCH][8];
+    bool keep[NCH][8];
+    load_row<NCH, VEC>(x + row * ld, cols, lane, v);
+#pragma unroll
+    for (int u = 0; u < NCH; ++u) {
+        if (VEC) {
+            const uint32_t c0 = slot_col<true>(lane, u, 0);
+            const uint4 t = *(const uint4 *)(tok_k + (c0 < cols ? c0 : 0u));
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                keep[u][i] = c0 + i < cols && ((comp4r(t, i >> 1) >> (16 * (i & 1))) & 0xFFFFu) <= ti;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t col = slot_col<false>(lane, u, i);
+                keep[u][i] = col < cols && (uint32_t)tok_k[col] <= ti;
+            }
+        }
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < NCH; ++u)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v[u][i] *= c;
+            if (keep[u][i]) m = fmaxf(m, v[u][i]);
+        }
+    m = sh_wave_max(m);
+    const bool uni = ti == kLlmPad || m == -INFINITY;
+    float s = 0.f;
+#pragma unroll
+    for (int u = 0; u < NCH; ++u)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float e = uni ? 1.f : (keep[u][i] ? sh_fast_exp2(v[u][i] - m) : 0.f);
+            v[u][i] = e;
+            if (slot_col<VEC>(lane, u, i) < cols) s += e;
+        }
+    const float inv = 1.f / sh_wave_sum(s);
+#pragma unroll
+    for (int u = 0; u < NCH; ++u)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[u][i] *= inv;
+    store_row<NCH, VEC>(y + row * ld, cols, lane, v);
+}
+
+// Rotate-half RoPE (sh_llm.inc.c:127-150): item = (row, p), p < cols / 2 -> head p / half, pair j = p % half:
+// y1 = x1 cos - x2 sin, y2 = x2 cos + x1 sin with x1 = x[h dh + j], x2 = x[h dh + half + j], the row's table
+// entry cos = t[j], sin = t[half + j]. In place allowed (each item reads and writes its own pair).
+__global__ __launch_bounds__(256) void k_rope(uint16_t *y, const uint16_t *x, const uint16_t *tab, uint64_t ld, uint64_t ldt,
+                                              uint32_t half, ShDiv per_row, ShDiv by_half, uint32_t items) {
+    const uint32_t it = blockIdx.x * 256u + threadIdx.x;
+    if (it >= items) return;
+    const uint32_t row = sh_div(it, per_row), p = it - row * per_row.d;
+    const uint32_t h = sh_div(p, by_half), j = p - h * half;
+    const uint64_t o1 = (uint64_t)row * ld + 2ull * h * half + j, o2 = o1 + half;
+    const float x1 = sh_dev_h2f(x[o1]), x2 = sh_dev_h2f(x[o2]);
+    const float cs = sh_dev_h2f(tab[(uint64_t)row * ldt + j]), sn = sh_dev_h2f(tab[(uint64_t)row * ldt + half + j]);
+    y[o1] = sh_dev_f2h(x1 * cs - x2 * sn);
+    y[o2] = sh_dev_f2h(x2 * cs + x1 * sn);
+}
+
+// SmolVLM connector pixel shuffle (sh_llm.inc.c:344-362): dst token t = (gr, gb) of the (grid/s)^2 output tokens
+// is s chunks of s D elements: chunk i = src rows (gr s + i) grid + gb s .. + s (contiguous). 16-byte items.
+__global__ __launch_bounds__(256) void k_pixel_shuffle(uint4 *dst, const uint4 *src, uint32_t grid, uint32_t s, uint32_t dv,
+                                                       uint32_t g, uint32_t items) {
+    const uint32_t it = blockIdx.x * 256u + threadIdx.x;   // dst item (16 bytes); dv = D / 8 items per patch
+    if (it >= items) return;
+    const uint32_t chunk = s * dv, per_tok = s * chunk, t = it / per_tok, r = it - t * per_tok, i = r / chunk, e = r - i * chunk;
+    const uint32_t gr = t / g, gb = t - gr * g;
+    dst[it] = src[(uint64_t)((gr * s + i) * grid + gb * s) * dv + e];
+}
+
+__global__ __launch_bounds__(256) void k_pixel_shuffle1(uint16_t *dst, const uint16_t *src, uint32_t grid, uint32_t s, uint32_t D,
+                                                        uint32_t g, uint32_t items) {
+    const uint32_t it = blockIdx.x * 256u + threadIdx.x;   // dst element
+    if (it >= items) return;
+    const uint32_t chunk = s * D, per_tok = s * chunk, t = it / per_tok, r = it - t * per_tok, i = r / chunk, e = r - i * chunk;
+    const uint32_t gr = t / g, gb = t - gr * g;
+    dst[it] = src[(uint64_t)((gr * s + i) * grid + gb * s) * D + e];
+}
 }  // namespace
 
 extern "C" {
@@ -473,6 +606,87 @@ void sh_transpose(uint64_t dst, uint64_t src, uint32_t rows, uint32_t cols, uint
         hipLaunchKernelGGL(k_transpose1, grid, dim3(256), 0, st, D, S, rows, cols, (uint64_t)ld_src, (uint64_t)ld_dst);
     }
     sh_launch_ok("sh_transpose");
+}
+
+
+// ---- Llama-style decoder ops (sh_ops.h:277-307; reference runtime/sh_llm.inc.c) ------------------------------
+void sh_rmsnorm(uint64_t y, uint64_t x, uint64_t gamma, uint32_t rows, uint32_t cols, uint32_t ld, float eps, uint32_t) {
+    if (cols & 3) { sh_set_error(-1, "[sh_rmsnorm] cols %u %% 4 != 0", cols); return; }            // sh_llm.inc.c:122
+    if (cols > 8192) { sh_set_error(-1, "[sh_rmsnorm] cols %u > 8192", cols); return; }
+    if (!gamma && rows && cols) { sh_set_error(-1, "[sh_rmsnorm] NULL gamma"); return; }
+    if (!check_args("sh_rmsnorm", y, x, rows, cols, ld)) return;
+    hipStream_t st = sh_stream();
+    const dim3 grid(sh_cdiv(rows, kRowWaves)), block(256);
+    const bool vec = vec_ok(cols, {y, x, gamma}, {ld});
+    uint16_t *Y = (uint16_t *)y; const uint16_t *X = (const uint16_t *)x, *G = (const uint16_t *)gamma;
+#define SH_RMS(N) do { if (vec) hipLaunchKernelGGL((k_rmsnorm<N, true>), grid, block, 0, st, Y, X, G, rows, cols, (uint64_t)ld, eps); \
+                       else hipLaunchKernelGGL((k_rmsnorm<N, false>), grid, block, 0, st, Y, X, G, rows, cols, (uint64_t)ld, eps); } while (0)
+    if (cols <= 512) SH_RMS(1); else if (cols <= 1024) SH_RMS(2); else if (cols <= 2048) SH_RMS(4); else if (cols <= 4096) SH_RMS(8); else SH_RMS(16);
+#undef SH_RMS
+    sh_launch_ok("sh_rmsnorm");
+}
+
+void sh_rope(uint64_t y, uint64_t x, uint64_t cos_sin, uint32_t rows, uint32_t cols, uint32_t ld, uint32_t ld_table, uint32_t dh, uint32_t) {
+    if (dh == 0 || (dh & 7) || cols % dh) {                                                       // sh_llm.inc.c:147
+        sh_set_error(-1, "[sh_rope] need dh %% 8 == 0 and cols %% dh == 0 (dh=%u cols=%u)", dh, cols);
+        return;
+    }
+    if (!cos_sin && rows && cols) { sh_set_error(-1, "[sh_rope] NULL table"); return; }
+    if (ld_table < dh && rows > 1) { sh_set_error(-1, "[sh_rope] ld_table %u < dh %u", ld_table, dh); return; }
+    if (!check_args("sh_rope", y, x, rows, cols, ld)) return;
+    const uint64_t items64 = (uint64_t)rows * (cols / 2);
+    if (items64 > 0xFFFFFF00ull) { sh_set_error(-1, "[sh_rope] %u x %u is too large", rows, cols); return; }
+    const uint32_t items = (uint32_t)items64;
+    hipLaunchKernelGGL(k_rope, dim3(sh_cdiv(items, 256u)), dim3(256), 0, sh_stream(), (uint16_t *)y, (const uint16_t *)x,
+                       (const uint16_t *)cos_sin, (uint64_t)ld, (uint64_t)ld_table, dh / 2, sh_make_div(cols / 2), sh_make_div(dh / 2), items);
+    sh_launch_ok("sh_rope");
+}
+
+void sh_silu_mul(uint64_t y, uint64_t a, uint64_t b, uint32_t rows, uint32_t cols, uint32_t ld, uint32_t) {
+    if (cols & 3) { sh_set_error(-1, "[sh_silu_mul] cols %u %% 4 != 0", cols); return; }           // sh_llm.inc.c:170
+    if (!b && rows && cols) { sh_set_error(-1, "[sh_silu_mul] NULL tensor address"); return; }
+    if (!check_args("sh_silu_mul", y, a, rows, cols, ld)) return;
+    launch_elementwise(OP_SILU_MUL, y, a, b, rows, cols, ld, 0.f, "sh_silu_mul");
+}
+
+void sh_softmax_masked(uint64_t y, uint64_t x, uint32_t rows, uint32_t cols, uint32_t ld, float scale, uint64_t tok_q,
+                       uint64_t tok_k, uint32_t) {
+    if ((cols & 3) || !(scale > 0.f)) {                                                            // sh_llm.inc.c:244
+        sh_set_error(-1, "[sh_softmax_masked] need cols %% 4 == 0 and scale > 0");
+        return;
+    }
+    if (cols > 8192) { sh_set_error(-1, "[sh_softmax_masked] cols %u > 8192", cols); return; }
+    if ((!tok_q || !tok_k) && rows && cols) { sh_set_error(-1, "[sh_softmax_masked] NULL token array"); return; }
+    if (!check_args("sh_softmax_masked", y, x, rows, cols, ld)) return;
+    hipStream_t st = sh_stream();
+    const float c = scale * 1.4426950408889634f;
+    const dim3 grid(sh_cdiv(rows, kRowWaves)), block(256);
+    const bool vec = vec_ok(cols, {y, x, tok_k}, {ld});
+    uint16_t *Y = (uint16_t *)y; const uint16_t *X = (const uint16_t *)x, *TQ = (const uint16_t *)tok_q, *TK = (const uint16_t *)tok_k;
+#define SH_SMM(N) do { if (vec) hipLaunchKernelGGL((k_softmax_masked<N, true>), grid, block, 0, st, Y, X, rows, cols, (uint64_t)ld, c, TQ, TK); \
+                       else hipLaunchKernelGGL((k_softmax_masked<N, false>), grid, block, 0, st, Y, X, rows, cols, (uint64_t)ld, c, TQ, TK); } while (0)
+    if (cols <= 512) SH_SMM(1); else if (cols <= 1024) SH_SMM(2); else if (cols <= 2048) SH_SMM(4); else if (cols <= 4096) SH_SMM(8); else SH_SMM(16);
+#undef SH_SMM
+    sh_launch_ok("sh_softmax_masked");
+}
+
+void sh_pixel_shuffle(uint64_t dst, uint64_t src, uint32_t grid, uint32_t D, uint32_t s, uint32_t) {
+    if (s == 0 || grid % s) { sh_set_error(-1, "[sh_pixel_shuffle] grid %u not divisible by s %u", grid, s); return; }
+    if (grid == 0 || D == 0) return;
+    if (!dst || !src) { sh_set_error(-1, "[sh_pixel_shuffle] NULL tensor address"); return; }
+    const uint64_t total = (uint64_t)grid * grid * D;
+    if (total > 0xFFFFFF00ull) { sh_set_error(-1, "[sh_pixel_shuffle] %u^2 x %u is too large", grid, D); return; }
+    sh_ensure_init();
+    const uint32_t g = grid / s;
+    hipStream_t st = sh_stream();
+    if (D % 8 == 0 && sh_aligned16(dst) && sh_aligned16(src)) {
+        const uint32_t items = (uint32_t)(total / 8);
+        hipLaunchKernelGGL(k_pixel_shuffle, dim3(sh_cdiv(items, 256u)), dim3(256), 0, st, (uint4 *)dst, (const uint4 *)src, grid, s, D / 8, g, items);
+    } else {
+        hipLaunchKernelGGL(k_pixel_shuffle1, dim3(sh_cdiv((uint32_t)total, 256u)), dim3(256), 0, st, (uint16_t *)dst, (const uint16_t *)src,
+                           grid, s, D, g, (uint32_t)total);
+    }
+    sh_launch_ok("sh_pixel_shuffle");
 }
 
 }  // extern "C"

@@ -23,6 +23,7 @@ SH_FP16, SH_FP8, SH_INT16, SH_INT8 = 0, 1, 2, 3
 SH_EHIP = -3
 SH_ACT_NONE, SH_ACT_GELU = 0, 1
 SH_XM_AUTO, SH_XM_PANEL, SH_XM_WHOLE = 0, 1, 2
+SH_LLM_PAD = 0xFFFF
 SH_BIAS_FP16, SH_BIAS_FP32 = 0, 1
 SH_MESH_P = 4
 
@@ -55,6 +56,13 @@ _SIGS: dict[str, tuple] = {
     "sh_gemm_xmcast": (i32, [u64, u64, u64, u32, u32, u32, u32, u32, u32, C.POINTER(sh_gemm_cfg)]),
     "sh_gemm_xmcast_ex": (i32, [u64, u64, u64, u32, u32, u32, u32, u32, u32, C.POINTER(sh_gemm_cfg), u32]),
     "sh_gemm_xmcast_l1_bytes": (u32, [u32, u32, u32, C.POINTER(sh_gemm_cfg), u32]),
+    "sh_rmsnorm": (None, [u64, u64, u64, u32, u32, u32, f32, u32]),
+    "sh_rope": (None, [u64, u64, u64, u32, u32, u32, u32, u32, u32]),
+    "sh_silu_mul": (None, [u64, u64, u64, u32, u32, u32, u32]),
+    "sh_softmax_masked": (None, [u64, u64, u32, u32, u32, f32, u64, u64, u32]),
+    "sh_attention_head_masked": (i32, [u64, u64, u64, u64, u32, u32, u32, u32, u32, u32, f32, u64, u32]),
+    "sh_attention_gqa": (i32, [u64, u64, u64, u64, u32, u32, u32, u32, u32, u32, u32, u32, f32, u64, u32]),
+    "sh_pixel_shuffle": (None, [u64, u64, u32, u32, u32, u32]),
     "sh_gemm_splitk": (i32, [u64, u64, u64, u32, u32, u32, u32, u32, u32, C.POINTER(sh_gemm_cfg), u32, u32]),
     "sh_gemm_ex": (i32, [u64, u64, u64, u32, u32, u32, u32, u32, u32, C.POINTER(sh_gemm_cfg), C.POINTER(sh_gemm_epi)]),
     # row ops

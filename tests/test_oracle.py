@@ -259,3 +259,89 @@ def test_encoder_lcg_layer_shapes_and_composition():
 def test_close_helper():
     bad, err, _ = refs.close(np.array([1.0, 2.0]), np.array([1.015, 2.05]))
     assert bad == 1 and abs(err - 0.05) < 1e-6
+
+
+# ---- Llama-style decoder ops (run.py:175-235) ---------------------------------------------------------------
+def test_rmsnorm_closed_forms():
+    c = np.full((2, 8), 2.0, np.float16)
+    g = lcg.fill_fp16(1, 8, 3, 1, 8, 0.25)
+    y = refs.rmsnorm(c, g, 0.0)                               # constant row c: x / |c| = 1, times gamma
+    assert np.allclose(y, np.repeat(g.astype(np.float32), 2, 0), atol=1e-6)
+    x = lcg.fill_fp16(5, 64, 4, -16, 16, 0.125)
+    y = refs.rmsnorm(x, np.ones((1, 64)), 1e-5)
+    assert np.allclose(np.sqrt((y * y).mean(1)), 1, atol=1e-4)             # unit RMS
+    brute = [[float(x[i, j]) / math.sqrt(sum(float(v) ** 2 for v in x[i]) / 64 + 1e-5) for j in range(64)] for i in range(5)]
+    assert np.allclose(y, brute, atol=1e-5)
+
+
+def test_rope_closed_forms():
+    x = lcg.fill_fp16(3, 32, 5, -16, 16, 0.125)              # two heads of dh = 16
+    ident = np.concatenate([np.ones((3, 8)), np.zeros((3, 8))], 1)
+    assert np.array_equal(refs.rope(x, ident, 16), x.astype(np.float32))
+    quarter = np.concatenate([np.zeros((3, 8)), np.ones((3, 8))], 1)       # cos 0, sin 1: (x1, x2) -> (-x2, x1)
+    y = refs.rope(x, quarter, 16)
+    assert np.array_equal(y[:, :8], -x[:, 8:16].astype(np.float32)) and np.array_equal(y[:, 8:16], x[:, :8].astype(np.float32))
+    th = np.linspace(0, 3, 8)
+    tab = np.repeat(np.concatenate([np.cos(th), np.sin(th)])[None], 3, 0)
+    y = refs.rope(x, tab, 16)
+    xf = x.astype(np.float64)
+    for h in range(2):                                                      # rotations keep each pair's norm
+        a, b = xf[:, 16 * h:16 * h + 8], xf[:, 16 * h + 8:16 * h + 16]
+        ya, yb = y[:, 16 * h:16 * h + 8], y[:, 16 * h + 8:16 * h + 16]
+        assert np.allclose(a * a + b * b, ya * ya + yb * yb, atol=1e-4)
+
+
+def test_silu_mul_closed_forms():
+    a = np.array([[0.0, 1.0, -1.0, 20.0, -20.0, 2.5]], np.float16)
+    y = refs.silu_mul(a, np.ones_like(a))
+    assert y[0, 0] == 0 and abs(y[0, 1] - 0.7310586) < 1e-6 and abs(y[0, 2] + 0.2689414) < 1e-6
+    assert abs(y[0, 3] - 20) < 1e-6 and abs(y[0, 4]) < 1e-7
+    b = lcg.fill_fp16(1, 6, 7, -4, 4, 0.5)
+    assert np.allclose(refs.silu_mul(a, b), y * b.astype(np.float32), atol=1e-6)
+
+
+def test_softmax_masked_closed_forms_and_brute_force():
+    S = 12
+    x = lcg.fill_fp16(S, S, 16, -32, 32, 0.25)
+    tc = refs.llm_tokens(S, "causal")
+    p = refs.softmax_masked(x, 0.5, tc, tc)
+    assert np.array_equal(p[0], np.eye(S)[0]) and np.allclose(p.sum(1), 1, atol=1e-6)
+    assert (np.triu(p, 1) == 0).all()                                       # nothing above the diagonal
+    zeros = np.zeros(S, np.uint32)
+    assert np.allclose(refs.softmax_masked(x, 0.5, zeros, zeros), refs.softmax(x, 0.5), atol=1e-6)
+    tok = np.array([0, 0, 0xFFFF, 1, 0, 2, 0xFFFF, 1, 0, 0, 2, 1], np.uint32)
+    p = refs.softmax_masked(x, 0.5, tok, tok)
+    assert np.allclose(p[2], 1 / S) and np.allclose(p[6], 1 / S)           # padding query rows are uniform
+    for i in range(S):                                                      # pure-Python brute force of the rest
+        if tok[i] == 0xFFFF:
+            continue
+        allowed = [j for j in range(S) if tok[j] <= tok[i]]
+        m = max(0.5 * float(x[i, j]) for j in allowed)
+        e = {j: math.exp(0.5 * float(x[i, j]) - m) for j in allowed}
+        for j in range(S):
+            assert abs(p[i, j] - (e[j] / sum(e.values()) if j in e else 0.0)) < 1e-6
+
+
+def test_attention_gqa_reduces_to_multi_head():
+    S, H, dh = 16, 4, 8
+    q = lcg.fill_fp16(S, H * dh, 21, -8, 8, 0.125)
+    k = lcg.fill_fp16(S, 2 * dh, 22, -8, 8, 0.125)
+    v = lcg.fill_fp16(S, 2 * dh, 23, -16, 16, 0.125)
+    kk, vv = np.repeat(k.reshape(S, 2, dh), 2, 1).reshape(S, H * dh), np.repeat(v.reshape(S, 2, dh), 2, 1).reshape(S, H * dh)
+    assert np.allclose(refs.attention_gqa(q, k, v, H, 2), refs.attention(q, kk, vv, H, 0.125), atol=1e-3)
+    zeros = np.zeros(S, np.uint32)
+    assert np.allclose(refs.attention_gqa(q, k, v, H, 2, zeros), refs.attention_gqa(q, k, v, H, 2), atol=1e-3)
+    tc = refs.llm_tokens(S, "causal")
+    o = refs.attention_gqa(q, k, v, H, 2, tc)
+    assert np.allclose(o[0, :dh], v[0, :dh].astype(np.float32), atol=1e-3)   # query 0 sees key 0 only
+
+
+def test_pixel_shuffle_brute_force():
+    grid, s, D = 6, 3, 4
+    src = np.arange(grid * grid * D, dtype=np.uint16).reshape(grid * grid, D)
+    dst = refs.pixel_shuffle(src, grid, s)
+    g = grid // s
+    for gr in range(g):
+        for gb in range(g):
+            want = np.concatenate([src[(gr * s + i) * grid + gb * s + jj] for i in range(s) for jj in range(s)])
+            assert np.array_equal(dst[gr * g + gb], want)
