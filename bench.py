@@ -1,13 +1,16 @@
 """Benchmark of the softhier-ops hot path on one MI355X: the SigLIP-B encoder layer (
 B=32, S=256, D=768, 12 heads, FFN 3072, fp16, weights N(0, 0.02), biases zero, x ~ N(0, 1), seeded).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--sequence fused|reference] [--no-cpu] [--no-rowops]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--sequence fused|reference] [--graph] [--no-cpu] [--no-rowops]
 
-A step is one forward pass of the layer over the batch through libshops.so (inputs resident in HBM). Prints ONE
-JSON line with the whole-job TFLOP/s, the roofline of the dominant kernel (HIP events around its launches in
-the timed region, on the library stream = the legacy null stream torch also uses), the per-op breakdown, the
-row-op HBM bandwidths at the batched shapes (cold: rotating buffer sets of >= 512 MiB) and the numpy CPU
-baseline (the oracle's restatement, timed on this host).
+A step is one forward pass of the layer over the batch through libshops.so (inputs resident in HBM), its calls
+launched one by one; `--graph` records the fused layer's seven calls once into a HIP graph and times replays of
+it instead (the same kernels every step; on MI355X this measured no faster: the gaps between kernels are not
+host launch time). Prints ONE JSON line with the whole-job TFLOP/s, the roofline of the dominant kernel (HIP events around its
+launches, on the library stream = the legacy null stream torch also uses), the per-op breakdown, the row-op HBM
+bandwidths at the batched shapes (cold: rotating buffer sets of >= 512 MiB; each next to a plain device copy of
+the same bytes, the practical ceiling at that size) and the numpy CPU baseline (the oracle's restatement, timed
+on this host).
 """
 from __future__ import annotations
 
@@ -94,23 +97,41 @@ def rowops_bandwidth(lib, torch, B: int, S: int, D: int, F: int, H: int, reps: i
             else:
                 lib.sh_transpose(A(y), A(x), r, c, c, r, shops.SH_ALL)
 
-        for s in sets:
-            run(*s)
-        torch.cuda.synchronize()
-        times = []
-        for _ in range(reps):
-            for s in sets:
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record()
-                run(*s)
-                e1.record()
-                times.append((e0, e1))
-        torch.cuda.synchronize()
-        ms = sorted(a.elapsed_time(b) for a, b in times)
-        med = ms[len(ms) // 2]
-        gbs = nbytes / (med * 1e-3) / 1e9
-        out[name] = {"shape": [r, c], "bytes": nbytes, "us": round(med * 1e3, 2), "GB/s": round(gbs, 1),
-                     "frac": round(gbs / PEAK_GBS, 3)}
+        def copy(x, y, b):
+            y.view(-1).copy_(x.view(-1))
+
+        def timed(fn):
+            """(median us of single launches with events around each, us per launch of all sets back to back)"""
+            for st in sets:
+                fn(*st)
+            torch.cuda.synchronize()
+            times = []
+            for _ in range(reps):
+                for st in sets:
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    fn(*st)
+                    e1.record()
+                    times.append((e0, e1))
+            torch.cuda.synchronize()
+            ms = sorted(a.elapsed_time(b) for a, b in times)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for st in sets:
+                fn(*st)
+            e1.record()
+            torch.cuda.synchronize()
+            return ms[len(ms) // 2] * 1e3, e0.elapsed_time(e1) * 1e3 / len(sets)
+
+        us, us_b = timed(run)
+        cus, cus_b = timed(copy)          # a device copy of the output's bytes: 2 x output bytes of traffic
+        gbs = nbytes / (us * 1e-6) / 1e9
+        cbytes = 2 * 2 * r * c
+        out[name] = {"shape": [r, c], "bytes": nbytes, "us": round(us, 2), "GB/s": round(gbs, 1),
+                     "frac": round(gbs / PEAK_GBS, 3), "us_batched": round(us_b, 2),
+                     "GB/s_batched": round(nbytes / (us_b * 1e-6) / 1e9, 1),
+                     "copy_GB/s": round(cbytes / (cus * 1e-6) / 1e9, 1),
+                     "frac_of_copy": round(gbs / (cbytes / (cus * 1e-6) / 1e9), 3)}
         del sets
         torch.cuda.empty_cache()
     return out
@@ -225,8 +246,17 @@ def main() -> int:
     # timed region: K steps, each one replay of the captured layer graph (or the eager op sequence)
     graph = None
     enc.tap = None
+    eager_ms = None
     if args.sequence == "fused" and args.graph:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step(x, out, lp, B, S)
+        torch.cuda.synchronize()
+        eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
         graph = enc.capture(x, out, lp, B, S)
+        for _ in range(args.warmup):
+            graph.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -276,6 +306,7 @@ def main() -> int:
                                + (", HIP graph replay" if graph is not None else ", eager launches"), "global_batch": B,
                    "seq_len": S, "d_model": D, "ffn": F, "heads": H, "layers": 1, "parallelism": "single GPU"},
         "mfma_frac_of_peak": round(value / PEAK_TFLOPS, 4),
+        "eager_ms_per_step": round(eager_ms, 4) if eager_ms is not None else None,
         "roofline": roofline, "breakdown": breakdown, "rowops": rowops, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

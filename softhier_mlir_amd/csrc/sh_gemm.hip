@@ -453,10 +453,12 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs a) {
 
     // Prologue: slices 0 .. STAGES-2. Every iteration then issues exactly LOADS DMAs (slices past the end are
     // clamped to the last slice and land in a stage nobody reads again), so the wait is a constant count.
+    if (KT > 0) {
 #pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s)
+        for (int s = 0; s < STAGES - 1; ++s)
 #pragma unroll
-        for (int d = 0; d < C::LOADS; ++d) issue_one(d, min(s, KT - 1), s);
+            for (int d = 0; d < C::LOADS; ++d) issue_one(d, min(s, KT - 1), s);
+    }
 
     constexpr int NM = C::FM * C::FN;                 // MFMAs per k-substep
     constexpr int MT = 4 * NM;                        // per slice
@@ -748,6 +750,142 @@ __global__ __launch_bounds__(512) void k_gemm3(GemmArgs a) {
     epilogue8<BM, BN, 512, SPLIT, C::FM, C::FN>(a, acc, m0, n0, split, (uint16_t *)smem, row0, col0);
 }
 
+// ---- v4: 256-row tiles, 32-k slices through a deep DMA ring ------------------------------------------------
+// Four wavefronts (2 x 2), each owning 128 x BN/2 outputs (16 or 12 or 8 accumulators of 32 x 32): the largest
+// tile one workgroup of a CU can hold, which keeps the per-CU operand feed at (256 + BN) x 32 x 2 bytes per 32-k
+// slice (about 70-90 GB/s per CU at the MFMA rate). Slices of 32 k flow through a STAGES-deep LDS ring, so
+// the loads of slice kt + STAGES - 1 are issued right after the barrier that opens slice kt and have
+// STAGES - 1 slices of MFMA time to land. The two k-substeps of a slice alternate fragment buffers, and the
+// MFMAs of substep 1 of slice kt run after the barrier of slice kt + 1, while the first fragment reads of
+// slice kt + 1 are in flight, so no barrier leaves the MFMA pipe without work.
+// LDS X rows are 64 bytes (4 chunks of 16 B), chunk c of row m stored at c ^ ((m >> 2) & 3): the 16 rows read
+// by 16 lanes of one ds_read_b128 then cover 16 distinct 16-byte bank groups. W rows (k-major, BN halves) are
+// laid out and read with ds_read_b64_tr_b16 as in k_gemm2. Every lane keeps the k order of k_gemm2 (substep s,
+// lane group g -> k chunk 2 s + g), so both kernels sum the products of one output element in the same order.
+template <int BN, int STAGES>
+struct Cfg4 {
+    static constexpr int BM = 256, SK = 32, TM = 128, TN = BN / 2, FM = 4, FN = TN / 32;
+    static constexpr int XCH = BM * 4;                 // 16-byte chunks per X slice
+    static constexpr int WCPR = BN / 8;                // chunks per W row (k-major W)
+    static constexpr int WCH = SK * WCPR;              // chunks per W slice (= BN x 4 for W^T as well)
+    static constexpr int XR = XCH / 256, WR = WCH / 256;
+    static constexpr int LOADS = XR + WR;              // DMA instructions per wave per slice
+    static constexpr size_t STAGE = (size_t)(XCH + WCH) * 16;
+    static constexpr size_t LDS = STAGES * STAGE > (size_t)BM * BN * 2 ? STAGES * STAGE : (size_t)BM * BN * 2;
+    static_assert(BN % 64 == 0 && BN <= 256 && WCH % 256 == 0 && FN >= 1, "tile");
+    static_assert(STAGES >= 3 && LOADS * (STAGES - 2) < 64 && LDS <= 160 * 1024, "resources");
+};
+
+__device__ __forceinline__ uint32_t sx4(uint32_t m) { return (m >> 2) & 3u; }
+
+template <int BN, int STAGES, bool SPLIT>
+__global__ __launch_bounds__(256) void k_gemm4(GemmArgs a) {
+    using C = Cfg4<BN, STAGES>;
+    constexpr int BM = C::BM, SK = C::SK, FM = C::FM, FN = C::FN;
+    extern __shared__ uint4 smem[];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int wm = wave >> 1, wn = wave & 1, g = lane >> 5, r32 = lane & 31;
+
+    const uint32_t nblk = a.tiles_m * a.tiles_n * a.splits;
+    uint32_t L = blockIdx.x;
+    if (a.xcd_groups > 1) L = (blockIdx.x % a.xcd_groups) * (nblk / a.xcd_groups) + blockIdx.x / a.xcd_groups;
+    const uint32_t tn = L % a.tiles_n, rest = L / a.tiles_n;
+    const uint32_t tm = rest % a.tiles_m, split = rest / a.tiles_m;
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t kbeg = split * a.kps;
+    const uint32_t kend = min(a.K, kbeg + a.kps);
+    const int KT = kend > kbeg ? (int)((kend - kbeg) / SK) : 0;
+
+    // per-lane DMA sources of every round (rows past M / columns past N are read from clamped valid addresses
+    // and only feed outputs that are never stored)
+    const uint16_t *xs[C::XR];
+    const uint16_t *ws[C::WR];
+#pragma unroll
+    for (int r = 0; r < C::XR; ++r) {
+        const uint32_t p = r * 256 + wave * 64 + lane, m = p >> 2, c = (p & 3) ^ sx4(m);
+        xs[r] = a.x + (uint64_t)min(m0 + m, a.M - 1) * a.ldx + kbeg + 8 * c;
+    }
+#pragma unroll
+    for (int r = 0; r < C::WR; ++r) {
+        const uint32_t p = r * 256 + wave * 64 + lane, k = p / C::WCPR, c = (p % C::WCPR) ^ fw<BN>(k);
+        uint32_t gn = n0 + 8 * c;
+        if (gn >= a.N) gn = a.N - 8;
+        ws[r] = a.w + (uint64_t)(kbeg + k) * a.ldw + gn;
+    }
+    const uint32_t lds0 = lds_addr(smem);
+    const uint32_t wave_off = (uint32_t)__builtin_amdgcn_readfirstlane(wave * 64 * 16);
+    const uint64_t wadv = (uint64_t)SK * a.ldw;
+    auto issue_all = [&](int src, int stage) {      // the LOADS DMAs of k-slice `src` into LDS stage `stage`
+        const uint32_t st = lds0 + (uint32_t)stage * (uint32_t)C::STAGE;
+#pragma unroll
+        for (int d = 0; d < C::XR; ++d) lds_dma16(xs[d] + (uint64_t)src * SK, st + d * 4096 + wave_off);
+#pragma unroll
+        for (int d = 0; d < C::WR; ++d) lds_dma16(ws[d] + (uint64_t)src * wadv, st + C::XCH * 16 + d * 4096 + wave_off);
+    };
+
+    sh_f16v acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = sh_f16v{};
+
+    const int q = lane >> 4, iq = lane & 15;
+    auto load_frags = [&](int stage, int s, sh_h8 (&af)[FM], sh_h8 (&bf)[FN]) {
+        const uint4 *X = (const uint4 *)((const char *)smem + (uint32_t)stage * (uint32_t)C::STAGE);
+        const uint32_t c = (uint32_t)(2 * s + g);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const uint32_t m = (uint32_t)(wm * C::TM + i * 32 + r32);
+            af[i] = __builtin_bit_cast(sh_h8, X[m * 4 + (c ^ sx4(m))]);
+        }
+        const uint32_t wbase = lds0 + (uint32_t)stage * (uint32_t)C::STAGE + C::XCH * 16;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const uint32_t n = (uint32_t)(wn * C::TN + j * 32 + 16 * (q & 1) + 4 * (iq & 3));
+            const uint32_t k0 = 16 * s + 8 * g + (iq >> 2), k1 = k0 + 4;
+            const sh_s4 lo = ds_read_tr(wbase + k0 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k0)) + 2 * (n & 7));
+            const sh_s4 hi = ds_read_tr(wbase + k1 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k1)) + 2 * (n & 7));
+            bf[j] = __builtin_bit_cast(sh_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+    };
+    auto mfmas = [&](const sh_h8 (&af)[FM], const sh_h8 (&bf)[FN]) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    };
+
+    // prologue: slices 0 .. STAGES-2 (past the end: the last slice again, into stages nobody reads), so every
+    // iteration waits for a constant number of outstanding DMAs
+    if (KT > 0) {
+#pragma unroll
+        for (int s = 0; s < STAGES - 1; ++s) issue_all(min(s, KT - 1), s);
+    }
+
+    sh_h8 a0[FM], b0[FN], a1[FM], b1[FN];
+    for (int kt = 0; kt < KT; ++kt) {
+        wait_vmcnt<(STAGES - 2) * C::LOADS>();        // slice kt has landed (this wave's share) ...
+        __builtin_amdgcn_s_waitcnt(0xC07F);           // ... and this wave's reads of slice kt - 1 are done
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();                 // every share landed; the stage of slice kt - 1 is free
+        __builtin_amdgcn_sched_barrier(0);
+        issue_all(min(kt + STAGES - 1, KT - 1), (kt + STAGES - 1) % STAGES);
+        const int st = kt % STAGES;
+        load_frags(st, 0, a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kt > 0) mfmas(a1, b1);                    // substep 1 of slice kt - 1, under the reads just issued
+        __builtin_amdgcn_sched_barrier(0);
+        load_frags(st, 1, a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(a0, b0);                                // substep 0 of slice kt
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (KT > 0) mfmas(a1, b1);
+    wait_vmcnt<0>();     // the clamped tail loads must land before the tile is staged in the same LDS
+    __syncthreads();
+    epilogue<BM, BN, true, SPLIT, FM, FN>(a, acc, m0, n0, split, (uint16_t *)smem);
+}
+
 template <bool VEC>
 __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs a, ShDiv div, uint32_t per_row, uint32_t items) {
     const uint32_t it = blockIdx.x * 256u + threadIdx.x;
@@ -791,6 +929,8 @@ struct KCfg { int bm, bn, stages; bool v2; KernelFn vec[2], scalar[2]; size_t ld
                                { k_gemm<BM, BN, false, false>, k_gemm<BM, BN, false, true> }, Cfg<BM, BN>::LDS, EFF, false }
 #define SH_KCFG2(BM, BN, ST, EFF) { BM, BN, ST, true, { k_gemm2<BM, BN, ST, false>, k_gemm2<BM, BN, ST, true> }, \
                                     { nullptr, nullptr }, Cfg2<BM, BN, ST>::LDS, EFF, false, 256 }
+#define SH_KCFG4(BN, ST, EFF) { 256, BN, ST, true, { k_gemm4<BN, ST, false>, k_gemm4<BN, ST, true> }, \
+                                { nullptr, nullptr }, Cfg4<BN, ST>::LDS, EFF, false, 256 }
 #define SH_KCFG3(BM, BN, EFF) { BM, BN, 2, true, { k_gemm3<BM, BN, false>, k_gemm3<BM, BN, true> }, \
                                 { nullptr, nullptr }, Cfg3<BM, BN>::LDS, EFF, false, 512 }
 // eff = sustained fraction of the MFMA peak per CU measured for each tile on MI355X (tile-time model of
@@ -812,10 +952,13 @@ KCfg g_cfgs[] = {
     SH_KCFG3(256, 128, 0.28f),
     SH_KCFG3(128, 256, 0.28f),
     SH_KCFG3(128, 128, 0.26f),
+    SH_KCFG4(256, 4, 0.36f),
+    SH_KCFG4(192, 5, 0.30f),
 };
 #undef SH_KCFG
 #undef SH_KCFG2
 #undef SH_KCFG3
+#undef SH_KCFG4
 constexpr int kNumCfg = sizeof(g_cfgs) / sizeof(g_cfgs[0]);
 
 int env_int(const char *name, int dflt) {

@@ -184,6 +184,62 @@ __global__ __launch_bounds__(256) void k_softmax(uint16_t *y, const uint16_t *x,
     store_row<NCH, VEC>(y + row * ld, cols, lane, v);
 }
 
+// Short rows (cols <= 8 LPR, 16-byte aligned): LPR lanes per row, 64 / LPR rows per wavefront and RIT such
+// groups per wavefront, every load of the RIT groups issued before the first reduction, so each lane keeps RIT
+// 16-byte loads in flight and no lane idles on a row narrower than a wavefront. Same arithmetic as k_softmax.
+template <int LPR, int RIT>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+template <int LPR, int RIT>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+template <int LPR, int RIT>
+__global__ __launch_bounds__(256) void k_softmax_narrow(uint16_t *y, const uint16_t *x, uint32_t rows, uint32_t cols, uint64_t ld, float c) {
+    constexpr int RPW = 64 / LPR;                     // rows per wavefront per group
+    const int lane = threadIdx.x & 63, sub = lane / LPR, l = lane % LPR;
+    const uint32_t row0 = (blockIdx.x * kRowWaves + (threadIdx.x >> 6)) * (uint32_t)(RPW * RIT) + (uint32_t)sub;
+    const uint32_t c0 = 8u * (uint32_t)l;
+    const bool colok = c0 < cols;
+    uint4 raw[RIT];
+#pragma unroll
+    for (int r = 0; r < RIT; ++r) {                   // rows past the end re-read row 0 and are not stored
+        const uint32_t row = row0 + (uint32_t)(r * RPW);
+        raw[r] = *(const uint4 *)(x + (row < rows ? row : 0u) * ld + (colok ? c0 : 0u));
+    }
+#pragma unroll
+    for (int r = 0; r < RIT; ++r) pin4(raw[r]);
+#pragma unroll
+    for (int r = 0; r < RIT; ++r) {
+        float v[8];
+        unpack8(raw[r], v);
+        float m = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v[i] *= c;
+            if (colok) m = fmaxf(m, v[i]);
+        }
+        m = group_max<LPR, RIT>(m);
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v[i] = colok ? sh_fast_exp2(v[i] - m) : 0.f;
+            sum += v[i];
+        }
+        const float inv = 1.f / group_sum<LPR, RIT>(sum);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] *= inv;
+        const uint32_t row = row0 + (uint32_t)(r * RPW);
+        if (row < rows && colok) *(uint4 *)(y + row * ld + c0) = pack8(v);
+    }
+}
+
 // Rows wider than the register-resident kernels hold: one 256-thread block per row, three passes over it.
 __device__ float block_reduce(float v, bool is_max, float *red) {
     v = is_max ? sh_wave_max(v) : sh_wave_sum(v);
@@ -561,8 +617,18 @@ void sh_softmax_rows(uint64_t y, uint64_t x, uint32_t rows, uint32_t cols, uint3
         sh_launch_ok("sh_softmax_rows");
         return;
     }
-    const dim3 grid(sh_cdiv(rows, kRowWaves)), block(256);
     const bool vec = vec_ok(cols, {y, x}, {ld});
+    if (vec && cols <= 256) {
+        constexpr int RIT = 4;
+        const uint32_t lpr = cols <= 64 ? 8 : cols <= 128 ? 16 : 32;
+        const dim3 g(sh_cdiv(rows, kRowWaves * (64 / lpr) * RIT));
+        if (lpr == 8) hipLaunchKernelGGL((k_softmax_narrow<8, RIT>), g, dim3(256), 0, st, Y, X, rows, cols, (uint64_t)ld, c);
+        else if (lpr == 16) hipLaunchKernelGGL((k_softmax_narrow<16, RIT>), g, dim3(256), 0, st, Y, X, rows, cols, (uint64_t)ld, c);
+        else hipLaunchKernelGGL((k_softmax_narrow<32, RIT>), g, dim3(256), 0, st, Y, X, rows, cols, (uint64_t)ld, c);
+        sh_launch_ok("sh_softmax_rows");
+        return;
+    }
+    const dim3 grid(sh_cdiv(rows, kRowWaves)), block(256);
 #define SH_SM(N) do { if (vec) hipLaunchKernelGGL((k_softmax<N, true>), grid, block, 0, st, Y, X, rows, cols, (uint64_t)ld, c); \
                       else hipLaunchKernelGGL((k_softmax<N, false>), grid, block, 0, st, Y, X, rows, cols, (uint64_t)ld, c); } while (0)
     if (cols <= 512) SH_SM(1); else if (cols <= 1024) SH_SM(2); else if (cols <= 2048) SH_SM(4); else if (cols <= 4096) SH_SM(8); else SH_SM(16);

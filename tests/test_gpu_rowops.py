@@ -184,3 +184,23 @@ def test_layernorm_many_rows_against_oracle(lib, gpu, rows, cols, inplace):
     lib.sh_layernorm(A(Y), A(X), A(to_dev(g)), A(to_dev(be)), rows, cols, cols, 1e-6, ALL)
     bad, err, _ = refs.close(to_np(Y), refs.layernorm(x, g, be, 1e-6))
     assert bad == 0, err
+
+
+@pytest.mark.parametrize("cols", [8, 64, 72, 136, 256])
+@pytest.mark.parametrize("scale", [0.125, -0.7])
+def test_softmax_short_rows(lib, gpu, cols, scale):
+    """Rows of at most 256 columns take the several-rows-per-wavefront kernel (8, 16 or 32 lanes per row):
+    ragged row count (not a multiple of the 32..128 rows a wavefront covers), ld > cols, the padding columns
+    of each row left untouched, and the same rows in place."""
+    rows, ld = 1001, cols + 24
+    x = data.normal((rows, ld), 40 + cols, 0.0, 3.0)
+    X = to_dev(x)
+    Y = _empty(rows, ld)
+    lib.sh_softmax_rows(A(Y), A(X), rows, cols, ld, scale, ALL)
+    y = to_np(Y)
+    assert refs.close(y[:, :cols], refs.softmax(x[:, :cols], scale))[0] == 0
+    assert (y[:, cols:] == 7.0).all()
+    lib.sh_softmax_rows(A(X), A(X), rows, cols, ld, scale, ALL)
+    xi = to_np(X)
+    assert (xi[:, :cols].view(np.uint16) == y[:, :cols].view(np.uint16)).all()
+    assert (xi[:, cols:].view(np.uint16) == x[:, cols:].view(np.uint16)).all()
