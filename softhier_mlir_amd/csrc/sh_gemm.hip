@@ -751,8 +751,9 @@ __global__ __launch_bounds__(512) void k_gemm3(GemmArgs a) {
 }
 
 // ---- v4: 256-row tiles, 32-k slices through a deep DMA ring ------------------------------------------------
-// Four wavefronts (2 x 2), each owning 128 x BN/2 outputs (16 or 12 or 8 accumulators of 32 x 32): the largest
-// tile one workgroup of a CU can hold, which keeps the per-CU operand feed at (256 + BN) x 32 x 2 bytes per 32-k
+// NT / 64 wavefronts: four as 2 x 2 (each owning 128 x BN/2 outputs, one wavefront per SIMD) or eight as 2 x 4
+// (128 x BN/4 each, two per SIMD: while one waits on LDS the other issues MFMAs). 256 x BN is the largest tile
+// one workgroup of a CU can hold, which keeps the per-CU operand feed at (256 + BN) x 32 x 2 bytes per 32-k
 // slice (about 70-90 GB/s per CU at the MFMA rate). Slices of 32 k flow through a STAGES-deep LDS ring, so
 // the loads of slice kt + STAGES - 1 are issued right after the barrier that opens slice kt and have
 // STAGES - 1 slices of MFMA time to land. The two k-substeps of a slice alternate fragment buffers, and the
@@ -762,29 +763,30 @@ __global__ __launch_bounds__(512) void k_gemm3(GemmArgs a) {
 // by 16 lanes of one ds_read_b128 then cover 16 distinct 16-byte bank groups. W rows (k-major, BN halves) are
 // laid out and read with ds_read_b64_tr_b16 as in k_gemm2. Every lane keeps the k order of k_gemm2 (substep s,
 // lane group g -> k chunk 2 s + g), so both kernels sum the products of one output element in the same order.
-template <int BN, int STAGES>
+template <int BN, int STAGES, int NT = 256>
 struct Cfg4 {
-    static constexpr int BM = 256, SK = 32, TM = 128, TN = BN / 2, FM = 4, FN = TN / 32;
+    static constexpr int WGN = NT / 128;               // wavefronts along N (2 x WGN grid)
+    static constexpr int BM = 256, SK = 32, TM = 128, TN = BN / WGN, FM = 4, FN = TN / 32;
     static constexpr int XCH = BM * 4;                 // 16-byte chunks per X slice
     static constexpr int WCPR = BN / 8;                // chunks per W row (k-major W)
-    static constexpr int WCH = SK * WCPR;              // chunks per W slice (= BN x 4 for W^T as well)
-    static constexpr int XR = XCH / 256, WR = WCH / 256;
+    static constexpr int WCH = SK * WCPR;              // chunks per W slice
+    static constexpr int XR = XCH / NT, WR = WCH / NT;
     static constexpr int LOADS = XR + WR;              // DMA instructions per wave per slice
     static constexpr size_t STAGE = (size_t)(XCH + WCH) * 16;
     static constexpr size_t LDS = STAGES * STAGE > (size_t)BM * BN * 2 ? STAGES * STAGE : (size_t)BM * BN * 2;
-    static_assert(BN % 64 == 0 && BN <= 256 && WCH % 256 == 0 && FN >= 1, "tile");
+    static_assert((NT == 256 || NT == 512) && BN % 64 == 0 && BN <= 256 && TN % 32 == 0 && WCH % NT == 0 && FN >= 1, "tile");
     static_assert(STAGES >= 3 && LOADS * (STAGES - 2) < 64 && LDS <= 160 * 1024, "resources");
 };
 
 __device__ __forceinline__ uint32_t sx4(uint32_t m) { return (m >> 2) & 3u; }
 
-template <int BN, int STAGES, bool SPLIT>
-__global__ __launch_bounds__(256) void k_gemm4(GemmArgs a) {
-    using C = Cfg4<BN, STAGES>;
+template <int BN, int STAGES, bool SPLIT, int NT = 256>
+__global__ __launch_bounds__(NT) void k_gemm4(GemmArgs a) {
+    using C = Cfg4<BN, STAGES, NT>;
     constexpr int BM = C::BM, SK = C::SK, FM = C::FM, FN = C::FN;
     extern __shared__ uint4 smem[];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int wm = wave >> 1, wn = wave & 1, g = lane >> 5, r32 = lane & 31;
+    const int wm = wave / C::WGN, wn = wave % C::WGN, g = lane >> 5, r32 = lane & 31;
 
     const uint32_t nblk = a.tiles_m * a.tiles_n * a.splits;
     uint32_t L = blockIdx.x;
@@ -802,12 +804,12 @@ __global__ __launch_bounds__(256) void k_gemm4(GemmArgs a) {
     const uint16_t *ws[C::WR];
 #pragma unroll
     for (int r = 0; r < C::XR; ++r) {
-        const uint32_t p = r * 256 + wave * 64 + lane, m = p >> 2, c = (p & 3) ^ sx4(m);
+        const uint32_t p = r * NT + wave * 64 + lane, m = p >> 2, c = (p & 3) ^ sx4(m);
         xs[r] = a.x + (uint64_t)min(m0 + m, a.M - 1) * a.ldx + kbeg + 8 * c;
     }
 #pragma unroll
     for (int r = 0; r < C::WR; ++r) {
-        const uint32_t p = r * 256 + wave * 64 + lane, k = p / C::WCPR, c = (p % C::WCPR) ^ fw<BN>(k);
+        const uint32_t p = r * NT + wave * 64 + lane, k = p / C::WCPR, c = (p % C::WCPR) ^ fw<BN>(k);
         uint32_t gn = n0 + 8 * c;
         if (gn >= a.N) gn = a.N - 8;
         ws[r] = a.w + (uint64_t)(kbeg + k) * a.ldw + gn;
@@ -818,9 +820,9 @@ __global__ __launch_bounds__(256) void k_gemm4(GemmArgs a) {
     auto issue_all = [&](int src, int stage) {      // the LOADS DMAs of k-slice `src` into LDS stage `stage`
         const uint32_t st = lds0 + (uint32_t)stage * (uint32_t)C::STAGE;
 #pragma unroll
-        for (int d = 0; d < C::XR; ++d) lds_dma16(xs[d] + (uint64_t)src * SK, st + d * 4096 + wave_off);
+        for (int d = 0; d < C::XR; ++d) lds_dma16(xs[d] + (uint64_t)src * SK, st + d * NT * 16 + wave_off);
 #pragma unroll
-        for (int d = 0; d < C::WR; ++d) lds_dma16(ws[d] + (uint64_t)src * wadv, st + C::XCH * 16 + d * 4096 + wave_off);
+        for (int d = 0; d < C::WR; ++d) lds_dma16(ws[d] + (uint64_t)src * wadv, st + C::XCH * 16 + d * NT * 16 + wave_off);
     };
 
     sh_f16v acc[FM][FN];
@@ -883,7 +885,8 @@ __global__ __launch_bounds__(256) void k_gemm4(GemmArgs a) {
     if (KT > 0) mfmas(a1, b1);
     wait_vmcnt<0>();     // the clamped tail loads must land before the tile is staged in the same LDS
     __syncthreads();
-    epilogue<BM, BN, true, SPLIT, FM, FN>(a, acc, m0, n0, split, (uint16_t *)smem);
+    if constexpr (NT == 256) epilogue<BM, BN, true, SPLIT, FM, FN>(a, acc, m0, n0, split, (uint16_t *)smem);
+    else epilogue8<BM, BN, NT, SPLIT, FM, FN>(a, acc, m0, n0, split, (uint16_t *)smem, (uint32_t)(wm * C::TM), (uint32_t)(wn * C::TN));
 }
 
 template <bool VEC>
@@ -929,8 +932,8 @@ struct KCfg { int bm, bn, stages; bool v2; KernelFn vec[2], scalar[2]; size_t ld
                                { k_gemm<BM, BN, false, false>, k_gemm<BM, BN, false, true> }, Cfg<BM, BN>::LDS, EFF, false }
 #define SH_KCFG2(BM, BN, ST, EFF) { BM, BN, ST, true, { k_gemm2<BM, BN, ST, false>, k_gemm2<BM, BN, ST, true> }, \
                                     { nullptr, nullptr }, Cfg2<BM, BN, ST>::LDS, EFF, false, 256 }
-#define SH_KCFG4(BN, ST, EFF) { 256, BN, ST, true, { k_gemm4<BN, ST, false>, k_gemm4<BN, ST, true> }, \
-                                { nullptr, nullptr }, Cfg4<BN, ST>::LDS, EFF, false, 256 }
+#define SH_KCFG4(BN, ST, NT, EFF) { 256, BN, ST, true, { k_gemm4<BN, ST, false, NT>, k_gemm4<BN, ST, true, NT> }, \
+                                    { nullptr, nullptr }, Cfg4<BN, ST, NT>::LDS, EFF, false, NT }
 #define SH_KCFG3(BM, BN, EFF) { BM, BN, 2, true, { k_gemm3<BM, BN, false>, k_gemm3<BM, BN, true> }, \
                                 { nullptr, nullptr }, Cfg3<BM, BN>::LDS, EFF, false, 512 }
 // eff = sustained fraction of the MFMA peak per CU measured for each tile on MI355X (tile-time model of
@@ -952,8 +955,10 @@ KCfg g_cfgs[] = {
     SH_KCFG3(256, 128, 0.28f),
     SH_KCFG3(128, 256, 0.28f),
     SH_KCFG3(128, 128, 0.26f),
-    SH_KCFG4(256, 4, 0.36f),
-    SH_KCFG4(192, 5, 0.30f),
+    SH_KCFG4(256, 4, 256, 0.36f),
+    SH_KCFG4(192, 5, 256, 0.30f),
+    SH_KCFG4(256, 4, 512, 0.45f),
+    SH_KCFG4(128, 6, 512, 0.40f),
 };
 #undef SH_KCFG
 #undef SH_KCFG2
