@@ -62,5 +62,19 @@ def build(verbose: bool = False) -> Path:
     return LIB
 
 
+def build_programs() -> list[Path]:
+    """Emit every example softhier program (programs/*.mlir) with the HIP target and link it against
+    libshops.so: programs/<name>.gen.c and the executable programs/<name>.exe (host code only: gcc)."""
+    from softhier_mlir_amd import emit_hip
+    out = []
+    for src in sorted((PKG / "programs").glob("*.mlir")):
+        c = src.with_suffix(".gen.c")
+        c.write_text(emit_hip.emit_hip(src.read_text()))
+        out.append(emit_hip.build_program(c, src.with_suffix(".exe")))
+    return out
+
+
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
+    for p in build_programs():
+        print(p)

@@ -1,0 +1,136 @@
+"""The emit_c HIP target (softhier_mlir_amd/emit_hip.py) on the CPU: op-by-op emission, loops and indexed
+buffers, phases, the reference's own translate tests (tests/filecheck/*_translate.mlir, checked with their
+CHECK lines where the reference is present), and that the emitted example programs compile and link."""
+from __future__ import annotations
+
+import re
+from pathlib import Path
+
+import pytest
+
+from softhier_mlir_amd import emit_hip
+from softhier_mlir_amd.emit_hip import EmitError, emit_hip as emit
+
+REF_FILECHECK = Path("/root/reference/tests/filecheck")
+IN_SCOPE = ["attention", "gemm512", "gemm_nonconst", "gemm_xmcast", "hbm_ops", "llm", "loop", "mark"]
+OUT_OF_SCOPE = ["gemm256", "mlp", "expert", "train"]      # TCDM / RedMulE level, expert and training families
+
+
+def filecheck(output: str, checks: list[tuple[str, str]]) -> str | None:
+    """FileCheck's CHECK / CHECK-NEXT / CHECK-NOT over output lines ({{regex}} blocks inside literal text).
+    Returns None when every directive holds, else a description of the first failure."""
+    lines = output.splitlines()
+    pos, nots = 0, []
+    for kind, pat in checks:
+        parts = re.split(r"\{\{(.*?)\}\}", pat.rstrip())
+        rx = re.compile("".join(re.escape(p) if i % 2 == 0 else p for i, p in enumerate(parts)))
+        if kind == "CHECK-NOT":
+            nots.append(rx)
+            continue
+        if kind == "CHECK-NEXT":
+            if pos >= len(lines) or not rx.search(lines[pos]):
+                return f"CHECK-NEXT {pat!r} against {lines[pos] if pos < len(lines) else '<end>'!r}"
+            pos += 1
+            continue
+        for i in range(pos, len(lines)):
+            if rx.search(lines[i]):
+                bad = [n.pattern for n in nots for ln in lines[pos:i] if n.search(ln)]
+                if bad:
+                    return f"CHECK-NOT {bad[0]!r} matched before {pat!r}"
+                nots, pos = [], i + 1
+                break
+        else:
+            return f"CHECK {pat!r} not found after line {pos}"
+    return None
+
+
+def test_filecheck_helper_semantics():
+    out = "a x1\nb y2\nc z3\n"
+    assert filecheck(out, [("CHECK", "a x{{[0-9]}}"), ("CHECK-NEXT", "b y2"), ("CHECK", "z3")]) is None
+    assert filecheck(out, [("CHECK", "a"), ("CHECK-NEXT", "c")]) is not None
+    assert filecheck(out, [("CHECK-NOT", "y2"), ("CHECK", "c z3")]) is not None
+    assert filecheck(out, [("CHECK", "c"), ("CHECK", "a")]) is not None
+
+
+PROGRAM = '''
+builtin.module {
+  func.func @small() {
+    %c0 = arith.constant 0 : index
+    %c1 = arith.constant 1 : index
+    %c4 = arith.constant 4 : index
+    %x = softhier.hbm_buffer {offset = 0 : i32} : memref<128x256xf16, "hbm_west">
+    %g = softhier.hbm_buffer {offset = 65536 : i32} : memref<1x256xf16, "hbm_west">
+    %y = softhier.hbm_buffer {offset = 69632 : i32} : memref<128x256xf16, "hbm_west">
+    softhier.hbm_fill_lcg %x {seed = 3 : i32, lo = -8 : i32, hi = 8 : i32, scale = 0.1 : f32} : memref<128x256xf16, "hbm_west">
+    softhier.layernorm %x, %g, %g -> %y {eps = 1.0e-5 : f32, cluster = -1 : i32}
+        : memref<128x256xf16, "hbm_west">, memref<1x256xf16, "hbm_west">, memref<1x256xf16, "hbm_west"> -> memref<128x256xf16, "hbm_west">
+    scf.for %i = %c0 to %c4 step %c1 {
+      %v = softhier.view %y, %i {stride = 64 : i32} : memref<128x256xf16, "hbm_west"> -> memref<128x64xf16, strided<[256, 1], offset: 0>, "hbm_west">
+      softhier.scale %v -> %v {scale = 0.3 : f32, cluster = 2 : i32} : memref<128x64xf16, strided<[256, 1], offset: 0>, "hbm_west"> -> memref<128x64xf16, strided<[256, 1], offset: 0>, "hbm_west">
+    }
+    softhier.dump_samples %y {seed = 5 : i32, n = 8 : i32, tag = "Y"} : memref<128x256xf16, "hbm_west">
+    func.return
+  }
+}
+'''
+
+
+def test_emits_phases_loops_views_and_f32_literals():
+    c = emit(PROGRAM)
+    inputs = c[c.index("static void small_inputs(void)"):c.index("static void small(void)")]
+    kernel = c[c.index("static void small(void)"):c.index("static void small_checks(void)")]
+    checks = c[c.index("static void small_checks(void)"):c.index("int main(void)")]
+    assert "sh_test_fill_fp16(hb1, 128, 256, 256, 3, -8, 8, 0.10000000149011612f);" in inputs       # f32 of 0.1
+    assert "sh_layernorm(hb3, hb1, hb2, hb2, 128, 256, 256, 9.999999747378752e-06f, SH_ALL);" in kernel
+    assert "for (uint32_t i1 = 0; i1 < 4; i1 += 1) {" in kernel
+    assert "sh_scale((hb3 + (uint64_t)(i1) * 128u), (hb3 + (uint64_t)(i1) * 128u), 128, 64, 256, 0.30000001192092896f, 2);" in kernel
+    assert "sh_test_dump_samples(hb3, 128, 256, 256, 5, 8, \"Y\");" in checks                       # y not touched later
+    assert "sh_timer_start();" in c and "sh_timer_end();" in c and "sh_call_on_core_stack" not in c
+
+
+def test_dump_of_a_buffer_used_later_stays_in_the_timed_region():
+    prog = PROGRAM.replace('''    func.return''', '''    softhier.gelu %y -> %y {cluster = -1 : i32} : memref<128x256xf16, "hbm_west"> -> memref<128x256xf16, "hbm_west">
+    func.return''')
+    c = emit(prog)
+    kernel = c[c.index("static void small(void)"):c.index("static void small_checks(void)")]
+    assert "sh_test_dump_samples(hb3" in kernel
+
+
+@pytest.mark.parametrize("bad, why", [
+    ('%b = softhier.l1_buffer : memref<64x64xf16, "tcdm">', "l1_buffer"),
+    ('softhier.frobnicate %x {cluster = -1 : i32} : memref<128x256xf16, "hbm_west">', "frobnicate"),
+])
+def test_ops_outside_the_library_raise(bad, why):
+    prog = PROGRAM.replace("    func.return", f"    {bad}\n    func.return")
+    with pytest.raises(EmitError, match=why):
+        emit(prog)
+
+
+def _checks(text: str) -> list[tuple[str, str]]:
+    return re.findall(r"//\s*(CHECK(?:-NEXT|-NOT)?):\s?(.*)$", text, re.M)
+
+
+@pytest.mark.skipif(not REF_FILECHECK.is_dir(), reason="the reference checkout is not present on this host")
+@pytest.mark.parametrize("name", IN_SCOPE)
+def test_reference_translate_tests(name):
+    """The reference's own softhier-translate tests, CHECK lines unchanged, against this target's output."""
+    text = (REF_FILECHECK / f"{name}_translate.mlir").read_text()
+    checks = _checks(text)
+    assert checks
+    err = filecheck(emit(text), checks)
+    assert err is None, err
+
+
+@pytest.mark.skipif(not REF_FILECHECK.is_dir(), reason="the reference checkout is not present on this host")
+@pytest.mark.parametrize("name", OUT_OF_SCOPE)
+def test_reference_translate_tests_out_of_scope_raise(name):
+    with pytest.raises(EmitError):
+        emit((REF_FILECHECK / f"{name}_translate.mlir").read_text())
+
+
+@pytest.mark.parametrize("prog", sorted((Path(emit_hip.PKG) / "programs").glob("*.mlir")), ids=lambda p: p.stem)
+def test_example_programs_emit_and_link(prog, tmp_path):
+    c = tmp_path / (prog.stem + ".c")
+    c.write_text(emit(prog.read_text()))
+    exe = emit_hip.build_program(c, tmp_path / prog.stem)
+    assert exe.exists()

@@ -1,0 +1,72 @@
+"""Example softhier programs emitted with the HIP target (softhier_mlir_amd/programs/*.mlir, linked against
+libshops.so by build()) run on the GPU as separate processes; their "<tag> r c hex" sample lines are checked
+against the oracle on the same LCG inputs."""
+from __future__ import annotations
+
+import os
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import lcg, refs
+
+pytestmark = pytest.mark.gpu
+PROGS = Path(__file__).resolve().parents[1] / "softhier_mlir_amd" / "programs"
+
+
+def run(name: str) -> tuple[str, dict]:
+    exe = PROGS / f"{name}.exe"
+    if not exe.exists():
+        pytest.fail(f"{exe} is missing: build() emits and links the example programs")
+    print(f"running {exe.name}", flush=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    samples: dict = {}
+    for m in re.finditer(r"^(\S+) (\d+) (\d+) ([0-9a-f]{4})$", r.stdout, re.M):
+        samples.setdefault(m.group(1), []).append((int(m.group(2)), int(m.group(3)), int(m.group(4), 16)))
+    assert "[Performance Counter]: Execution period is" in r.stdout
+    return r.stdout, samples
+
+
+def values(samples, tag, want: np.ndarray, nsamples: int, seed: int):
+    got = samples[tag]
+    assert [(i, j) for i, j, _ in got] == lcg.sample_positions(want.shape[0], want.shape[1], seed, nsamples)
+    g = np.array([v for _, _, v in got], np.uint16).view(np.float16).astype(np.float32)
+    w = np.array([want[i, j] for i, j, _ in got], np.float32)
+    return g, w
+
+
+def test_ops_check_program(gpu):
+    _, smp = run("ops_check")
+    x = lcg.fill_fp16(256, 768, 1, -16, 16, 0.125)
+    g = lcg.fill_fp16(1, 768, 14, 2, 6, 0.25)
+    be = lcg.fill_fp16(1, 768, 15, -4, 4, 0.125)
+    qkv = lcg.fill_fp16(256, 2304, 21, -16, 16, 0.0625)
+    y = refs.r16(refs.layernorm(x, g, be, 1e-6))
+    kT = y.T.copy()
+    s = refs.r16(refs.softmax(refs.r16(refs.gemm(y[:, 64:128], kT[64:128, :])), 0.125))
+    ge = refs.r16(refs.gelu(y))
+    ab = refs.r16(refs.add_bias(ge, be))
+    ad = refs.r16(refs.add(x, ab))
+    o = refs.attention(qkv[:, :768], qkv[:, 768:1536], qkv[:, 1536:], 12, 0.125)
+    for tag, want, seed in (("Y", y, 31), ("S", s, 33), ("GE", ge, 34), ("AB", ab, 35), ("AD", ad, 36), ("O", o, 37)):
+        got, w = values(smp, tag, want, 96, seed)
+        bad, err, _ = refs.close(got, w)
+        assert bad == 0, (tag, err)
+    got, w = values(smp, "KT", kT, 96, 32)
+    assert np.array_equal(got, w)                                      # transpose of the stored y: bit-exact
+
+
+def test_siglip_layers_program(gpu):
+    out, smp = run("siglip_layers")
+    x = refs.siglip_input_lcg(256, 768)
+    for L in range(2):
+        x = refs.encoder_layer(x, refs.siglip_params_lcg(768, 3072, layer=L), 12)
+        got, w = values(smp, f"OUT{L + 1}", x, 128, 205)
+        bad, err, _ = refs.close(got, w, atol=0.05, rtol=0.05)        # run.py:963: the siglip check's tolerance
+        assert bad == 0, (L, err)
+    assert re.search(r"^\[mark\] layer1 \d+$", out, re.M) and re.search(r"^\[mark\] layer2 \d+$", out, re.M)
