@@ -154,7 +154,7 @@ class Func:
     ops: list
 
 
-_STMT_START = re.compile(r"^(%[\w.$-]+\s*=\s*)?(softhier\.|scf\.|arith\.|func\.|\})")
+_STMT_START = re.compile(r"^(%[\w.$-]+(:\d+)?\s*=\s*)?([a-z_][\w]*\.[\w.]+|\})")   # "[%r =] dialect.op ..." or "}"
 
 
 def _statements(lines: list[str]) -> list[str]:

@@ -134,3 +134,19 @@ def test_example_programs_emit_and_link(prog, tmp_path):
     c.write_text(emit(prog.read_text()))
     exe = emit_hip.build_program(c, tmp_path / prog.stem)
     assert exe.exists()
+
+
+@pytest.mark.skipif(not REF_FILECHECK.is_dir(), reason="the reference checkout is not present on this host")
+def test_reference_siglip_example_emits_one_call_per_op():
+    """examples/siglip_encoder_layer.mlir (the full-resolution layer with per-head attention on strided views):
+    every softhier op becomes exactly one library call; linalg-level examples are refused (they need the passes)."""
+    import collections
+    text = (REF_FILECHECK.parents[1] / "examples" / "siglip_encoder_layer.mlir").read_text()
+    ops = collections.Counter(re.findall(r"softhier\.([a-z_]+)", text))
+    calls = collections.Counter(re.findall(r"\b(sh_[a-z_0-9]+)\(", emit(text)))
+    for op, fn in (("gemm", "sh_gemm"), ("softmax", "sh_softmax_rows"), ("add_bias", "sh_add_bias"), ("layernorm", "sh_layernorm"),
+                   ("add", "sh_add"), ("gelu", "sh_gelu"), ("transpose", "sh_transpose")):
+        assert calls[fn] == ops[op], (op, calls[fn], ops[op])
+    assert calls["sh_hbm_addr"] == 3 * ops["hbm_buffer"]          # declared in each of the three phases
+    with pytest.raises(EmitError, match="linalg"):
+        emit((REF_FILECHECK.parents[1] / "examples" / "gemm512_linalg.mlir").read_text())
