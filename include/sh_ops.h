@@ -48,6 +48,11 @@ uint64_t sh_hbm_addr(uint64_t byte_offset);             /* sh_ops.h:33   arena b
 uint64_t sh_hbm_malloc(uint32_t bytes);                 /* sh_ops.h:34   separate device allocation, 256 B aligned */
 uint32_t sh_l1_size(void);                              /* sh_ops.h:35   the reference cluster's TCDM bytes (0x100000) */
 void     sh_preload_wait(uint64_t sentinel);            /* sh_ops.h:36   drains the stream (data is resident) */
+/* Additive: copy the PT_LOAD segments of a preload image (ELF32, softhier_mlir/sim/preload.py:38-78: segment at
+ * physical address SH_PRELOAD_HBM_BASE + offset) into the sh_hbm_addr arena at those offsets. Returns the number of
+ * segments copied, -1 for an unreadable / malformed image or a segment beyond the arena, SH_EHIP on a HIP failure. */
+#define SH_PRELOAD_HBM_BASE 0xC0000000u
+int      sh_preload_load(const char *path);
 void     sh_call_on_core_stack(void (*fn)(void), uint32_t bytes_per_core);   /* sh_ops.h:48   calls fn() */
 
 #define SH_ALL 0xFFFFFFFFu                              /* sh_ops.h:39 */

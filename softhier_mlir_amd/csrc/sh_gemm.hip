@@ -763,10 +763,10 @@ __global__ __launch_bounds__(512) void k_gemm3(GemmArgs a) {
 // by 16 lanes of one ds_read_b128 then cover 16 distinct 16-byte bank groups. W rows (k-major, BN halves) are
 // laid out and read with ds_read_b64_tr_b16 as in k_gemm2. Every lane keeps the k order of k_gemm2 (substep s,
 // lane group g -> k chunk 2 s + g), so both kernels sum the products of one output element in the same order.
-template <int BN, int STAGES, int NT = 256>
+template <int BN, int STAGES, int NT = 256, int BM_ = 256>
 struct Cfg4 {
     static constexpr int WGN = NT / 128;               // wavefronts along N (2 x WGN grid)
-    static constexpr int BM = 256, SK = 32, TM = 128, TN = BN / WGN, FM = 4, FN = TN / 32;
+    static constexpr int BM = BM_, SK = 32, TM = BM / 2, TN = BN / WGN, FM = TM / 32, FN = TN / 32;
     static constexpr int XCH = BM * 4;                 // 16-byte chunks per X slice
     static constexpr int WCPR = BN / 8;                // chunks per W row (k-major W)
     static constexpr int WCH = SK * WCPR;              // chunks per W slice
@@ -774,15 +774,16 @@ struct Cfg4 {
     static constexpr int LOADS = XR + WR;              // DMA instructions per wave per slice
     static constexpr size_t STAGE = (size_t)(XCH + WCH) * 16;
     static constexpr size_t LDS = STAGES * STAGE > (size_t)BM * BN * 2 ? STAGES * STAGE : (size_t)BM * BN * 2;
-    static_assert((NT == 256 || NT == 512) && BN % 64 == 0 && BN <= 256 && TN % 32 == 0 && WCH % NT == 0 && FN >= 1, "tile");
+    static_assert((NT == 256 || NT == 512) && (BM == 128 || BM == 256) && BN % 64 == 0 && BN <= 256 && TN % 32 == 0 &&
+                  XCH % NT == 0 && WCH % NT == 0 && FN >= 1, "tile");
     static_assert(STAGES >= 3 && LOADS * (STAGES - 2) < 64 && LDS <= 160 * 1024, "resources");
 };
 
 __device__ __forceinline__ uint32_t sx4(uint32_t m) { return (m >> 2) & 3u; }
 
-template <int BN, int STAGES, bool SPLIT, int NT = 256>
+template <int BN, int STAGES, bool SPLIT, int NT = 256, int BM_ = 256>
 __global__ __launch_bounds__(NT) void k_gemm4(GemmArgs a) {
-    using C = Cfg4<BN, STAGES, NT>;
+    using C = Cfg4<BN, STAGES, NT, BM_>;
     constexpr int BM = C::BM, SK = C::SK, FM = C::FM, FN = C::FN;
     extern __shared__ uint4 smem[];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -932,8 +933,8 @@ struct KCfg { int bm, bn, stages; bool v2; KernelFn vec[2], scalar[2]; size_t ld
                                { k_gemm<BM, BN, false, false>, k_gemm<BM, BN, false, true> }, Cfg<BM, BN>::LDS, EFF, false }
 #define SH_KCFG2(BM, BN, ST, EFF) { BM, BN, ST, true, { k_gemm2<BM, BN, ST, false>, k_gemm2<BM, BN, ST, true> }, \
                                     { nullptr, nullptr }, Cfg2<BM, BN, ST>::LDS, EFF, false, 256 }
-#define SH_KCFG4(BN, ST, NT, EFF) { 256, BN, ST, true, { k_gemm4<BN, ST, false, NT>, k_gemm4<BN, ST, true, NT> }, \
-                                    { nullptr, nullptr }, Cfg4<BN, ST, NT>::LDS, EFF, false, NT }
+#define SH_KCFG4(BM, BN, ST, NT, EFF) { BM, BN, ST, true, { k_gemm4<BN, ST, false, NT, BM>, k_gemm4<BN, ST, true, NT, BM> }, \
+                                        { nullptr, nullptr }, Cfg4<BN, ST, NT, BM>::LDS, EFF, false, NT }
 #define SH_KCFG3(BM, BN, EFF) { BM, BN, 2, true, { k_gemm3<BM, BN, false>, k_gemm3<BM, BN, true> }, \
                                 { nullptr, nullptr }, Cfg3<BM, BN>::LDS, EFF, false, 512 }
 // eff = sustained fraction of the MFMA peak per CU measured for each tile on MI355X (tile-time model of
@@ -955,10 +956,13 @@ KCfg g_cfgs[] = {
     SH_KCFG3(256, 128, 0.28f),
     SH_KCFG3(128, 256, 0.28f),
     SH_KCFG3(128, 128, 0.26f),
-    SH_KCFG4(256, 4, 256, 0.36f),
-    SH_KCFG4(192, 5, 256, 0.30f),
-    SH_KCFG4(256, 4, 512, 0.45f),
-    SH_KCFG4(128, 6, 512, 0.40f),
+    SH_KCFG4(256, 256, 4, 256, 0.36f),
+    SH_KCFG4(256, 192, 5, 256, 0.30f),
+    SH_KCFG4(256, 256, 4, 512, 0.45f),
+    SH_KCFG4(256, 128, 6, 512, 0.40f),
+    SH_KCFG4(128, 192, 4, 256, 0.32f),
+    SH_KCFG4(128, 256, 4, 256, 0.32f),
+    SH_KCFG4(128, 128, 4, 256, 0.30f),
 };
 #undef SH_KCFG
 #undef SH_KCFG2

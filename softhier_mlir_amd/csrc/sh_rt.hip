@@ -183,6 +183,57 @@ uint64_t sh_hbm_malloc(uint32_t bytes) {
 
 void sh_preload_wait(uint64_t) { sh_barrier_global(); }
 
+// Preload image (reference softhier_mlir/sim/preload.py:38-78): an ELF32 whose PT_LOAD segments place data at
+// physical address SH_PRELOAD_HBM_BASE + offset. Every segment is copied into the arena at that offset, so the
+// program's sh_hbm_addr(offset) buffers hold it; the file is checked completely before the first copy.
+int sh_preload_load(const char *path) {
+    if (!path) { sh_set_error(-1, "[sh_preload_load] NULL path"); return -1; }
+    FILE *f = fopen(path, "rb");
+    if (!f) { sh_set_error(-1, "[sh_preload_load] cannot open %s", path); return -1; }
+    std::vector<uint8_t> img;
+    uint8_t buf[1 << 16];
+    size_t n;
+    while ((n = fread(buf, 1, sizeof buf, f)) > 0) img.insert(img.end(), buf, buf + n);
+    fclose(f);
+    auto u16 = [&](size_t o) { uint16_t v; memcpy(&v, &img[o], 2); return v; };
+    auto u32 = [&](size_t o) { uint32_t v; memcpy(&v, &img[o], 4); return v; };
+    if (img.size() < 52 || memcmp(img.data(), "\x7f" "ELF", 4) != 0 || img[4] != 1 || img[5] != 1) {
+        sh_set_error(-1, "[sh_preload_load] %s is not a little-endian ELF32 image", path);
+        return -1;
+    }
+    const size_t phoff = u32(28), phentsize = u16(42), phnum = u16(44);
+    if (phentsize < 32 || phoff + phnum * phentsize > img.size()) {
+        sh_set_error(-1, "[sh_preload_load] %s: program headers outside the file", path);
+        return -1;
+    }
+    struct Seg { uint64_t off; size_t file_off, bytes; };
+    std::vector<Seg> segs;
+    for (size_t i = 0; i < phnum; ++i) {
+        const size_t h = phoff + i * phentsize;
+        if (u32(h) != 1) continue;                                   // PT_LOAD only
+        const size_t fo = u32(h + 4), bytes = u32(h + 16);
+        const uint64_t paddr = u32(h + 12);
+        if (fo + bytes > img.size() || paddr < SH_PRELOAD_HBM_BASE) {
+            sh_set_error(-1, "[sh_preload_load] %s: segment %zu outside the file or below the HBM base", path, i);
+            return -1;
+        }
+        segs.push_back({paddr - SH_PRELOAD_HBM_BASE, fo, bytes});
+    }
+    if (!sh_hbm_addr(0)) return SH_EHIP;                           // the arena exists (allocated, zeroed)
+    for (const Seg &sg : segs)
+        if (sg.off + sg.bytes > g.arena_bytes) {
+            sh_set_error(-1, "[sh_preload_load] %s: segment at 0x%llx (+%zu B) beyond the %llu B arena (SH_HBM_ARENA_BYTES)", path,
+                         (unsigned long long)sg.off, sg.bytes, (unsigned long long)g.arena_bytes);
+            return -1;
+        }
+    sh_barrier_global();                                           // nothing queued still reads or writes the arena
+    for (const Seg &sg : segs)
+        if (sg.bytes && !sh_hip_ok(hipMemcpy((char *)g.arena + sg.off, img.data() + sg.file_off, sg.bytes, hipMemcpyHostToDevice),
+                                   "sh_preload_load copy"))
+            return SH_EHIP;
+    return (int)segs.size();
+}
+
 void sh_call_on_core_stack(void (*fn)(void), uint32_t) { if (fn) fn(); }
 
 int sh_last_error(void) { int e = g.last_err; g.last_err = 0; return e; }

@@ -12,6 +12,7 @@ timed region is bracketed by `sh_barrier_global()` (stream drain) and the refere
 
     python -m softhier_mlir_amd.emit_hip prog.mlir -o prog.c          # emit
     python -m softhier_mlir_amd.emit_hip prog.mlir --exe prog         # emit and link against libshops.so
+    ./prog [--preload image.elf]                                      # run (image: softhier_mlir_amd/preload.py)
 
 Ops outside the library (TCDM / RedMulE level, the expert and training families) make the reader raise.
 """
@@ -552,6 +553,8 @@ def _emit_phase(fn: Func, phase: str | None) -> str:
 
 _PROGRAM = '''\
 // Generated by softhier_mlir_amd.emit_hip (softhier dialect -> softhier-ops calls on the HIP library). Do not edit.
+// Usage: ./prog [--preload image.elf]   (an image in the reference's preload format, loaded into the HBM arena)
+#include <string.h>
 #include "sh_ops.h"
 
 static void {name}_inputs(void) {{   // test inputs / preload wait (not timed)
@@ -566,8 +569,10 @@ static void {name}_checks(void) {{   // test outputs (not timed)
 {checks}
 }}
 
-int main(void) {{
+int main(int argc, char **argv) {{
     sh_init();
+    for (int i = 1; i + 1 < argc; ++i)
+        if (strcmp(argv[i], "--preload") == 0 && sh_preload_load(argv[i + 1]) < 0) {{ sh_eoc(1); return 1; }}
     {name}_inputs();
     sh_barrier_global();
     sh_timer_start();

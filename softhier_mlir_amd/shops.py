@@ -48,7 +48,7 @@ _SIGS: dict[str, tuple] = {
     "sh_cluster_id": (u32, []), "sh_core_id": (u32, []), "sh_is_first_core": (i32, []), "sh_is_dm_core": (i32, []),
     "sh_num_clusters": (u32, []), "sh_timer_start": (None, []), "sh_timer_end": (None, []), "sh_eoc": (None, [u32]),
     "sh_cycles": (u32, []), "sh_hbm_addr": (u64, [u64]), "sh_hbm_malloc": (u64, [u32]), "sh_l1_size": (u32, []),
-    "sh_preload_wait": (None, [u64]),
+    "sh_preload_wait": (None, [u64]), "sh_preload_load": (i32, [_P]),
     # GEMM
     "sh_gemm": (i32, [u64, u64, u64, u32, u32, u32, u32, u32, u32, C.POINTER(sh_gemm_cfg), u32]),
     "sh_gemm_mesh": (i32, [u64, u64, u64, u32, u32, u32, u32, u32, u32, C.POINTER(sh_gemm_cfg)]),

@@ -79,7 +79,7 @@ def test_emits_phases_loops_views_and_f32_literals():
     c = emit(PROGRAM)
     inputs = c[c.index("static void small_inputs(void)"):c.index("static void small(void)")]
     kernel = c[c.index("static void small(void)"):c.index("static void small_checks(void)")]
-    checks = c[c.index("static void small_checks(void)"):c.index("int main(void)")]
+    checks = c[c.index("static void small_checks(void)"):c.index("int main(")]
     assert "sh_test_fill_fp16(hb1, 128, 256, 256, 3, -8, 8, 0.10000000149011612f);" in inputs       # f32 of 0.1
     assert "sh_layernorm(hb3, hb1, hb2, hb2, 128, 256, 256, 9.999999747378752e-06f, SH_ALL);" in kernel
     assert "for (uint32_t i1 = 0; i1 < 4; i1 += 1) {" in kernel

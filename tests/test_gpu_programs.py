@@ -70,3 +70,36 @@ def test_siglip_layers_program(gpu):
         bad, err, _ = refs.close(got, w, atol=0.05, rtol=0.05)        # run.py:963: the siglip check's tolerance
         assert bad == 0, (L, err)
     assert re.search(r"^\[mark\] layer1 \d+$", out, re.M) and re.search(r"^\[mark\] layer2 \d+$", out, re.M)
+
+
+def test_preload_gemm_program(gpu, tmp_path):
+    """Operands arrive through a preload image (sh_preload_load: segments copied into the sh_hbm_addr arena)."""
+    from softhier_mlir_amd import preload
+    x = lcg.fill_fp16(256, 512, 51, -16, 16, 0.0625)
+    w = lcg.fill_fp16(512, 384, 52, -16, 16, 0.03125)
+    img = preload.write_image(tmp_path / "operands.elf", {4096: x, 266240: w, 856064: preload.sentinel()})
+    exe = PROGS / "preload_gemm.exe"
+    r = subprocess.run([str(exe), "--preload", str(img)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    smp = {}
+    for m in re.finditer(r"^(\S+) (\d+) (\d+) ([0-9a-f]{4})$", r.stdout, re.M):
+        smp.setdefault(m.group(1), []).append((int(m.group(2)), int(m.group(3)), int(m.group(4), 16)))
+    got, want = values(smp, "Z", refs.gemm(x, w), 128, 41)
+    bad, err, _ = refs.close(got, want)
+    assert bad == 0, err
+
+
+def test_preload_load_places_segments_bit_exact(lib, gpu, tmp_path):
+    """sh_preload_load copies every segment to its arena offset; read back with the library's full dump."""
+    from softhier_mlir_amd import preload, shops
+    a = lcg.fill_fp16(33, 70, 61, -100, 100, 0.5)
+    b = np.arange(1000, dtype=np.uint16).reshape(1, 1000)
+    img = preload.write_image(tmp_path / "two.elf", {0x10000: a, 0x40000: b})
+    assert lib.sh_preload_load(str(img).encode()) == 2
+    for off, arr in ((0x10000, a.view(np.uint16)), (0x40000, b)):
+        with shops.capture() as cap:
+            lib.sh_test_dump_all(lib.sh_hbm_addr(off), arr.shape[0], arr.shape[1], arr.shape[1], b"P")
+        got = np.zeros(arr.shape, np.uint16)
+        for m in re.finditer(r"^P (\d+) (\d+) ([0-9a-f]{4})$", cap.text, re.M):
+            got[int(m.group(1)), int(m.group(2))] = int(m.group(3), 16)
+        assert np.array_equal(got, arr)
