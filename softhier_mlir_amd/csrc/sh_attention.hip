@@ -430,8 +430,10 @@ __global__ __launch_bounds__(256) void k_flash_dma(AttnArgs a) {
 // maximum known, needs no running rescale of O or l: p = 2^(c s - m), P (fp16) feeds O^T += V^T . P^T, and
 // the row sums l come from one more MFMA with an all-ones A operand (the sums of the fp16 numerators the
 // PV product used). Masking of keys past S happens only in the last, partial key block.
+// Occupancy: with a 2-stage ring (32 KB of LDS) a dh = 64 workgroup fits in 168 registers per lane, so three
+// workgroups share a CU (12 waves); the encoder's 768 (sequence, head, query block) workgroups then run in one round.
 template <int DH, int NST, bool MASK>
-__global__ __launch_bounds__(256) void k_flash2(AttnArgs a) {
+__global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a) {
     constexpr int DC = DH / 8, NS = DH / 16, DT = DH / 32;
     constexpr int KCH = KB * DC;                     // 16-byte chunks per K (or V) block
     constexpr int KR = KCH / 256;                    // DMA rounds per thread per block, per operand
@@ -704,7 +706,7 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
     static const int impl = [] { const char *e = getenv("SH_ATTN_IMPL"); return (e && *e) ? atoi(e) : 0; }();
     const dim3 grid(sh_cdiv(S, QPB), H, B);
     if (tok && (dh == 64 || dh == 128) && vec) {
-        if (dh == 64) go(k_flash2<64, 4, true>, grid, 0);
+        if (dh == 64) go(k_flash2<64, 2, true>, grid, 0);
         else go(k_flash2<128, 2, true>, grid, 0);
     } else if (tok) {
         if (S > 16384) { sh_set_error(-1, "[sh_attention] masked heads with dh=%u support S <= 16384", dh); return -1; }
@@ -712,7 +714,7 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
         if (!attr_m) { (void)hipFuncSetAttribute((const void *)k_attn_rows, hipFuncAttributeMaxDynamicSharedMemorySize, 16384 * 4); attr_m = true; }
         go(k_attn_rows, dim3(S, H, B), S * sizeof(float));
     } else if ((dh == 64 || dh == 128) && vec && impl == 0) {
-        if (dh == 64) go(k_flash2<64, 4, false>, grid, 0);
+        if (dh == 64) go(k_flash2<64, 2, false>, grid, 0);
         else go(k_flash2<128, 2, false>, grid, 0);
     } else if ((dh == 64 || dh == 128) && vec && impl == 1) {
         if (dh == 64) go(k_flash_dma<64, 4>, grid, 0);
