@@ -51,7 +51,30 @@ struct GemmArgs {
     uint32_t tiles_m, tiles_n, splits;
     uint32_t accumulate, bias_fp32, act;
     uint32_t xcd_groups;         // > 1: XCD-aware block remap with this many XCDs (requires divisibility)
+    uint32_t group_m;            // > 1: tiles ordered in bands of this many tile rows, column by column
 };
+
+// Logical tile L of a launch -> (split, tile row, tile column). Dispatch deals workgroups round-robin over the
+// XCDs, so block b first becomes logical index (b % X) (T / X) + b / X: each XCD walks a contiguous run of the
+// tile order and the operand panels it shares stay in that XCD's L2. The tile order itself is row-major, or
+// (group_m > 1) bands of group_m tile rows walked column by column, which keeps the X row panels and W column
+// panels touched at the same time by one XCD small (the band's rows plus the columns reached so far).
+__device__ __forceinline__ void tile_of(const GemmArgs &a, uint32_t b, uint32_t nblk, uint32_t &tm, uint32_t &tn, uint32_t &split) {
+    uint32_t L = b;
+    if (a.xcd_groups > 1) L = (b % a.xcd_groups) * (nblk / a.xcd_groups) + b / a.xcd_groups;
+    const uint32_t per = a.tiles_m * a.tiles_n;
+    split = L / per;
+    const uint32_t l = L - split * per;
+    if (a.group_m > 1) {
+        const uint32_t band = l / (a.group_m * a.tiles_n), first = band * a.group_m;
+        const uint32_t rows = min(a.tiles_m - first, a.group_m), r = l - band * a.group_m * a.tiles_n;
+        tm = first + r % rows;
+        tn = r / rows;
+    } else {
+        tm = l / a.tiles_n;
+        tn = l % a.tiles_n;
+    }
+}
 
 // Zero-filled stand-in read by the epilogue for operands a call does not have (never written).
 __device__ __align__(64) uint32_t g_epi_zero[16];
@@ -250,10 +273,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 
     // workgroup -> (split, tile_m, tile_n)
     const uint32_t nblk = a.tiles_m * a.tiles_n * a.splits;
-    uint32_t L = blockIdx.x;
-    if (a.xcd_groups > 1) L = (blockIdx.x % a.xcd_groups) * (nblk / a.xcd_groups) + blockIdx.x / a.xcd_groups;
-    const uint32_t tn = L % a.tiles_n, rest = L / a.tiles_n;
-    const uint32_t tm = rest % a.tiles_m, split = rest / a.tiles_m;
+    uint32_t tm, tn, split;
+    tile_of(a, blockIdx.x, nblk, tm, tn, split);
     const uint32_t m0 = tm * BM, n0 = tn * BN;
     const uint32_t kbeg = split * a.kps;
     const uint32_t kend = min(a.K, kbeg + a.kps);
@@ -404,10 +425,8 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs a) {
     const int wm = wave >> 1, wn = wave & 1, g = lane >> 5, r32 = lane & 31;
 
     const uint32_t nblk = a.tiles_m * a.tiles_n * a.splits;
-    uint32_t L = blockIdx.x;
-    if (a.xcd_groups > 1) L = (blockIdx.x % a.xcd_groups) * (nblk / a.xcd_groups) + blockIdx.x / a.xcd_groups;
-    const uint32_t tn = L % a.tiles_n, rest = L / a.tiles_n;
-    const uint32_t tm = rest % a.tiles_m, split = rest / a.tiles_m;
+    uint32_t tm, tn, split;
+    tile_of(a, blockIdx.x, nblk, tm, tn, split);
     const uint32_t m0 = tm * BM, n0 = tn * BN;
     const uint32_t kbeg = split * a.kps;
     const uint32_t kend = min(a.K, kbeg + a.kps);
@@ -645,10 +664,8 @@ __global__ __launch_bounds__(512) void k_gemm3(GemmArgs a) {
     const int lt = t & 255;                            // thread index within the group
 
     const uint32_t nblk = a.tiles_m * a.tiles_n * a.splits;
-    uint32_t L = blockIdx.x;
-    if (a.xcd_groups > 1) L = (blockIdx.x % a.xcd_groups) * (nblk / a.xcd_groups) + blockIdx.x / a.xcd_groups;
-    const uint32_t tn = L % a.tiles_n, rest = L / a.tiles_n;
-    const uint32_t tm = rest % a.tiles_m, split = rest / a.tiles_m;
+    uint32_t tm, tn, split;
+    tile_of(a, blockIdx.x, nblk, tm, tn, split);
     const uint32_t m0 = tm * BM, n0 = tn * BN;
     const uint32_t kbeg = split * a.kps;
     const uint32_t kend = min(a.K, kbeg + a.kps);
@@ -750,6 +767,157 @@ __global__ __launch_bounds__(512) void k_gemm3(GemmArgs a) {
     epilogue8<BM, BN, 512, SPLIT, C::FM, C::FN>(a, acc, m0, n0, split, (uint16_t *)smem, row0, col0);
 }
 
+// ---- epilogue from registers (Z^T accumulator layout) ------------------------------------------------------
+// Kernels that pass the MFMA operands swapped (first = W fragment, second = X fragment) hold every 32 x 32
+// accumulator as a block of Z^T: lane l has row l % 32 of Z and columns 8 q + 4 g + e in register 4 q + e
+// (q, e = 0..3, g = l / 32). One permlane32 swap per register pair hands each lane 8 consecutive columns of its
+// row, which pass through the epilogue chain and leave as one 16-byte store: no LDS staging and no barrier.
+// The products are the same k-ordered sums as with the operands in X, W order (the tests check every
+// configuration stores the same bits). The helpers take the wavefront's position (wm, wn) in the 2 x 2 grid of
+// (BM/2) x (BN/2) sub-tiles.
+
+// x's upper 32 lanes <-> y's lower 32 lanes (v_permlane32_swap_b32).
+__device__ __forceinline__ void swap_halves(uint32_t &x, uint32_t &y) {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, y, false, false);
+    x = r[0];
+    y = r[1];
+}
+
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
+    return (uint32_t)sh_dev_f2h(lo) | ((uint32_t)sh_dev_f2h(hi) << 16);
+}
+
+// 8 consecutive fp16 products of row block i, column block j, half p of one lane, in the Z^T layout above.
+// Both 16-byte chunks (p = 0, 1) of the 32 x 32 block come out of the same four swaps.
+template <int FM, int FN>
+__device__ __forceinline__ void zt_chunks(const sh_f16v (&acc)[FM][FN], int i, int j, uint4 (&q)[2]) {
+    uint32_t P[4][2];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        P[u][0] = pack_h2(acc[i][j][4 * u], acc[i][j][4 * u + 1]);
+        P[u][1] = pack_h2(acc[i][j][4 * u + 2], acc[i][j][4 * u + 3]);
+    }
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        swap_halves(P[2 * p][0], P[2 * p + 1][0]);
+        swap_halves(P[2 * p][1], P[2 * p + 1][1]);
+        q[p] = make_uint4(P[2 * p][0], P[2 * p][1], P[2 * p + 1][0], P[2 * p + 1][1]);
+    }
+}
+
+// The epilogue chain on a tile's chunks in place (q from zt_chunks of every block; chunk (i, j, p) of a lane is
+// row m0 + wm TM + 32 i + r32, columns n0 + wn TN + 32 j + 16 p + 8 g). Converting every accumulator first
+// halves the registers the epilogue holds. For the common chains (fp16 or no bias, optional residual) every
+// operand load of the tile is issued in one batch, so the epilogue waits for one memory latency.
+template <int BM, int BN, int FM, int FN>
+__device__ __forceinline__ void chain_chunks(const GemmArgs &a, uint4 (&q)[FM][FN][2], uint32_t m0, uint32_t n0, int wm, int wn) {
+    constexpr int TM = BM / 2, TN = BN / 2;
+    const int lane = threadIdx.x & 63, g = lane >> 5, r32 = lane & 31;
+    if (!a.accumulate && !a.bias && !a.res && a.act == SH_ACT_NONE) return;
+    if (!a.accumulate && !(a.bias && a.bias_fp32)) {
+        uint4 bq[FN][2];
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const uint32_t gn = n0 + wn * TN + 32 * j + 16 * p + 8 * g, gc = min(gn, a.N - 8);
+                bq[j][p] = a.bias ? *(const uint4 *)((const uint16_t *)a.bias + gc) : zero4();
+            }
+        uint4 rq[FM][FN][2];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const uint32_t gm = m0 + wm * TM + 32 * i + r32;
+            const uint64_t rowr = (uint64_t)min(gm, a.M - 1) * a.ldr;
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    const uint32_t gn = n0 + wn * TN + 32 * j + 16 * p + 8 * g, gc = min(gn, a.N - 8);
+                    rq[i][j][p] = a.res ? *(const uint4 *)(a.res + rowr + gc) : zero4();
+                }
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int p = 0; p < 2; ++p) q[i][j][p] = epi_chain8(a, q[i][j][p], zero4(), bq[j][p], zero4(), rq[i][j][p]);
+        return;
+    }
+    // z_old (accumulate) or a 32-byte fp32 bias per chunk: one (row block, column block) at a time
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const uint32_t gm = m0 + wm * TM + 32 * i + r32;
+        const uint32_t gmc = min(gm, a.M - 1);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            uint4 zo[2], b0[2], b1[2], rq[2];
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const uint32_t gn = n0 + wn * TN + 32 * j + 16 * p + 8 * g, gc = min(gn, a.N - 8);
+                zo[p] = a.accumulate ? *(const uint4 *)(a.z + (uint64_t)gmc * a.ldz + gc) : zero4();
+                if (a.bias && a.bias_fp32) {
+                    b0[p] = *(const uint4 *)((const float *)a.bias + gc);
+                    b1[p] = *(const uint4 *)((const float *)a.bias + gc + 4);
+                } else {
+                    b0[p] = a.bias ? *(const uint4 *)((const uint16_t *)a.bias + gc) : zero4();
+                    b1[p] = zero4();
+                }
+                rq[p] = a.res ? *(const uint4 *)(a.res + (uint64_t)gmc * a.ldr + gc) : zero4();
+            }
+#pragma unroll
+            for (int p = 0; p < 2; ++p) q[i][j][p] = epi_chain8(a, q[i][j][p], zo[p], b0[p], b1[p], rq[p]);
+        }
+    }
+}
+
+// Accumulators (Z^T layout) -> fp16 chunks with the epilogue chain applied.
+template <int BM, int BN, int FM, int FN>
+__device__ __forceinline__ void finish_chunks(const GemmArgs &a, const sh_f16v (&acc)[FM][FN], uint32_t m0, uint32_t n0,
+                                              uint4 (&q)[FM][FN][2], int wm, int wn) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) zt_chunks<FM, FN>(acc, i, j, q[i][j]);
+    chain_chunks<BM, BN, FM, FN>(a, q, m0, n0, wm, wn);
+}
+
+// Store a finished tile's chunks (origin m0, n0).
+template <int BM, int BN, int FM, int FN>
+__device__ __forceinline__ void store_all(const GemmArgs &a, const uint4 (&q)[FM][FN][2], uint32_t m0, uint32_t n0, int wm, int wn) {
+    constexpr int TM = BM / 2, TN = BN / 2;
+    const int lane = threadIdx.x & 63, g = lane >> 5, r32 = lane & 31;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const uint32_t gm = m0 + wm * TM + 32 * i + r32, gn = n0 + wn * TN + 32 * j + 16 * p + 8 * g;
+                if (gm < a.M && gn < a.N) *(uint4 *)(a.z + (uint64_t)gm * a.ldz + gn) = q[i][j][p];
+            }
+}
+
+// Split-K: the fp32 partial tile straight from the Z^T layout, 4 consecutive columns (16 bytes) per store.
+template <int BM, int BN, int FM, int FN>
+__device__ __forceinline__ void store_partials_zt(const GemmArgs &a, const sh_f16v (&acc)[FM][FN], uint32_t m0, uint32_t n0,
+                                                  uint32_t split, int wm, int wn) {
+    constexpr int TM = BM / 2, TN = BN / 2;
+    const int lane = threadIdx.x & 63, g = lane >> 5, r32 = lane & 31;
+    float *P = a.part + (uint64_t)split * a.M * a.N;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t gm = m0 + wm * TM + 32 * i + r32, gn = n0 + wn * TN + 32 * j + 8 * u + 4 * g;
+                if (gm < a.M && gn < a.N)
+                    *(float4 *)(P + (uint64_t)gm * a.N + gn) =
+                        make_float4(acc[i][j][4 * u], acc[i][j][4 * u + 1], acc[i][j][4 * u + 2], acc[i][j][4 * u + 3]);
+            }
+}
+
 // ---- v4: 256-row tiles, 32-k slices through a deep DMA ring ------------------------------------------------
 // NT / 64 wavefronts: four as 2 x 2 (each owning 128 x BN/2 outputs, one wavefront per SIMD) or eight as 2 x 4
 // (128 x BN/4 each, two per SIMD: while one waits on LDS the other issues MFMAs). 256 x BN is the largest tile
@@ -763,11 +931,13 @@ __global__ __launch_bounds__(512) void k_gemm3(GemmArgs a) {
 // by 16 lanes of one ds_read_b128 then cover 16 distinct 16-byte bank groups. W rows (k-major, BN halves) are
 // laid out and read with ds_read_b64_tr_b16 as in k_gemm2. Every lane keeps the k order of k_gemm2 (substep s,
 // lane group g -> k chunk 2 s + g), so both kernels sum the products of one output element in the same order.
-template <int BN, int STAGES, int NT = 256, int BM_ = 256>
+template <int BN, int STAGES, int NT = 256, int BM_ = 256, int SK_ = 32>
 struct Cfg4 {
     static constexpr int WGN = NT / 128;               // wavefronts along N (2 x WGN grid)
-    static constexpr int BM = BM_, SK = 32, TM = BM / 2, TN = BN / WGN, FM = TM / 32, FN = TN / 32;
-    static constexpr int XCH = BM * 4;                 // 16-byte chunks per X slice
+    static constexpr int BM = BM_, SK = SK_, TM = BM / 2, TN = BN / WGN, FM = TM / 32, FN = TN / 32;
+    static constexpr int XCPR = SK / 8;                // 16-byte chunks per X row of a slice
+    static constexpr int NS = SK / 16;                 // MFMA k-substeps per slice
+    static constexpr int XCH = BM * XCPR;              // 16-byte chunks per X slice
     static constexpr int WCPR = BN / 8;                // chunks per W row (k-major W)
     static constexpr int WCH = SK * WCPR;              // chunks per W slice
     static constexpr int XR = XCH / NT, WR = WCH / NT;
@@ -775,27 +945,33 @@ struct Cfg4 {
     static constexpr size_t STAGE = (size_t)(XCH + WCH) * 16;
     static constexpr size_t LDS = STAGES * STAGE > (size_t)BM * BN * 2 ? STAGES * STAGE : (size_t)BM * BN * 2;
     static_assert((NT == 256 || NT == 512) && (BM == 128 || BM == 256) && BN % 64 == 0 && BN <= 256 && TN % 32 == 0 &&
-                  XCH % NT == 0 && WCH % NT == 0 && FN >= 1, "tile");
+                  (SK == 32 || SK == 64) && XCH % NT == 0 && WCH % NT == 0 && FN >= 1, "tile");
     static_assert(STAGES >= 2 && LOADS * (STAGES - 2) < 64 && LDS <= 160 * 1024, "resources");
 };
 
 __device__ __forceinline__ uint32_t sx4(uint32_t m) { return (m >> 2) & 3u; }
+// X row swizzle of a slice: 64-byte rows (32-k slices) as above, 128-byte rows (64-k slices) as in k_gemm2
+template <int SK>
+__device__ __forceinline__ uint32_t xswz(uint32_t m) { return SK == 32 ? sx4(m) : swz(m); }
 
 // MINW: minimum wavefronts per SIMD the register allocation must allow (3 lets three 128 x 192 workgroups with a
 // 2-stage ring share a CU: 40 KB of LDS and <= 168 registers each).
-template <int BN, int STAGES, bool SPLIT, int NT = 256, int BM_ = 256, int MINW = 1>
+// REG (four wavefronts only): MFMA operands swapped and the epilogue straight from registers (see above).
+// SK: k per slice. With 64 (four k-substeps per slice) every X row segment a DMA instruction fetches is one
+// whole 128-byte line: the global -> LDS path costs per cache line touched, and 32-k slices (64-byte segments,
+// 16 rows per instruction) halve its throughput for X. The k order, hence every stored bit, is the same.
+template <int BN, int STAGES, bool SPLIT, int NT = 256, int BM_ = 256, int MINW = 1, bool REG = false, int SK_ = 32>
 __global__ __launch_bounds__(NT, MINW) void k_gemm4(GemmArgs a) {
-    using C = Cfg4<BN, STAGES, NT, BM_>;
+    static_assert(!REG || NT == 256, "register epilogue: 2 x 2 wavefronts");
+    using C = Cfg4<BN, STAGES, NT, BM_, SK_>;
     constexpr int BM = C::BM, SK = C::SK, FM = C::FM, FN = C::FN;
     extern __shared__ uint4 smem[];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int wm = wave / C::WGN, wn = wave % C::WGN, g = lane >> 5, r32 = lane & 31;
 
     const uint32_t nblk = a.tiles_m * a.tiles_n * a.splits;
-    uint32_t L = blockIdx.x;
-    if (a.xcd_groups > 1) L = (blockIdx.x % a.xcd_groups) * (nblk / a.xcd_groups) + blockIdx.x / a.xcd_groups;
-    const uint32_t tn = L % a.tiles_n, rest = L / a.tiles_n;
-    const uint32_t tm = rest % a.tiles_m, split = rest / a.tiles_m;
+    uint32_t tm, tn, split;
+    tile_of(a, blockIdx.x, nblk, tm, tn, split);
     const uint32_t m0 = tm * BM, n0 = tn * BN;
     const uint32_t kbeg = split * a.kps;
     const uint32_t kend = min(a.K, kbeg + a.kps);
@@ -807,7 +983,7 @@ __global__ __launch_bounds__(NT, MINW) void k_gemm4(GemmArgs a) {
     const uint16_t *ws[C::WR];
 #pragma unroll
     for (int r = 0; r < C::XR; ++r) {
-        const uint32_t p = r * NT + wave * 64 + lane, m = p >> 2, c = (p & 3) ^ sx4(m);
+        const uint32_t p = r * NT + wave * 64 + lane, m = p / C::XCPR, c = (p % C::XCPR) ^ xswz<SK>(m);
         xs[r] = a.x + (uint64_t)min(m0 + m, a.M - 1) * a.ldx + kbeg + 8 * c;
     }
 #pragma unroll
@@ -841,7 +1017,7 @@ __global__ __launch_bounds__(NT, MINW) void k_gemm4(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
             const uint32_t m = (uint32_t)(wm * C::TM + i * 32 + r32);
-            af[i] = __builtin_bit_cast(sh_h8, X[m * 4 + (c ^ sx4(m))]);
+            af[i] = __builtin_bit_cast(sh_h8, X[m * C::XCPR + (c ^ xswz<SK>(m))]);
         }
         const uint32_t wbase = lds0 + (uint32_t)stage * (uint32_t)C::STAGE + C::XCH * 16;
 #pragma unroll
@@ -857,7 +1033,10 @@ __global__ __launch_bounds__(NT, MINW) void k_gemm4(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
-            for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < FN; ++j) {
+                if constexpr (REG) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[j], af[i], acc[i][j], 0, 0, 0);
+                else acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+            }
     };
 
     // prologue: slices 0 .. STAGES-2 (past the end: the last slice again, into stages nobody reads), so every
@@ -878,14 +1057,30 @@ __global__ __launch_bounds__(NT, MINW) void k_gemm4(GemmArgs a) {
         const int st = kt % STAGES;
         load_frags(st, 0, a0, b0);
         __builtin_amdgcn_sched_barrier(0);
-        if (kt > 0) mfmas(a1, b1);                    // substep 1 of slice kt - 1, under the reads just issued
+        if (kt > 0) mfmas(a1, b1);                    // last substep of slice kt - 1, under the reads just issued
         __builtin_amdgcn_sched_barrier(0);
-        load_frags(st, 1, a1, b1);
-        __builtin_amdgcn_sched_barrier(0);
-        mfmas(a0, b0);                                // substep 0 of slice kt
-        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ss = 1; ss < C::NS; ++ss) {          // substep ss loads while substep ss - 1 computes
+            if (ss & 1) load_frags(st, ss, a1, b1);
+            else load_frags(st, ss, a0, b0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (ss & 1) mfmas(a0, b0);
+            else mfmas(a1, b1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
     if (KT > 0) mfmas(a1, b1);
+    if constexpr (REG) {
+        if constexpr (SPLIT) {
+            store_partials_zt<BM, BN, FM, FN>(a, acc, m0, n0, split, wm, wn);
+        } else {
+            uint4 q[FM][FN][2];
+            finish_chunks<BM, BN, FM, FN>(a, acc, m0, n0, q, wm, wn);
+            store_all<BM, BN, FM, FN>(a, q, m0, n0, wm, wn);
+        }
+        wait_vmcnt<0>();     // no DMA may still target this workgroup's LDS when it exits
+        return;
+    }
     wait_vmcnt<0>();     // the clamped tail loads must land before the tile is staged in the same LDS
     __syncthreads();
     if constexpr (NT == 256) epilogue<BM, BN, true, SPLIT, FM, FN>(a, acc, m0, n0, split, (uint16_t *)smem);
@@ -937,6 +1132,10 @@ struct KCfg { int bm, bn, stages; bool v2; KernelFn vec[2], scalar[2]; size_t ld
                                     { nullptr, nullptr }, Cfg2<BM, BN, ST>::LDS, EFF, false, 256 }
 #define SH_KCFG4(BM, BN, ST, NT, W, EFF) { BM, BN, ST, true, { k_gemm4<BN, ST, false, NT, BM, W>, k_gemm4<BN, ST, true, NT, BM, W> }, \
                                            { nullptr, nullptr }, Cfg4<BN, ST, NT, BM>::LDS, EFF, false, NT }
+#define SH_KCFG4R(BM, BN, ST, W, EFF) { BM, BN, ST, true, { k_gemm4<BN, ST, false, 256, BM, W, true>, k_gemm4<BN, ST, true, 256, BM, W, true> }, \
+                                       { nullptr, nullptr }, (size_t)(ST) * Cfg4<BN, ST, 256, BM>::STAGE, EFF, false, 256 }
+#define SH_KCFG4S(BM, BN, ST, W, EFF) { BM, BN, ST, true, { k_gemm4<BN, ST, false, 256, BM, W, true, 64>, k_gemm4<BN, ST, true, 256, BM, W, true, 64> }, \
+                                       { nullptr, nullptr }, (size_t)(ST) * Cfg4<BN, ST, 256, BM, 64>::STAGE, EFF, false, 256 }
 #define SH_KCFG3(BM, BN, EFF) { BM, BN, 2, true, { k_gemm3<BM, BN, false>, k_gemm3<BM, BN, true> }, \
                                 { nullptr, nullptr }, Cfg3<BM, BN>::LDS, EFF, false, 512 }
 // eff = sustained fraction of the MFMA peak per CU measured for each tile on MI355X (tile-time model of
@@ -967,11 +1166,17 @@ KCfg g_cfgs[] = {
     SH_KCFG4(128, 128, 4, 256, 1, 0.30f),
     SH_KCFG4(128, 192, 2, 256, 3, 0.33f),
     SH_KCFG4(128, 192, 3, 256, 2, 0.33f),
+    SH_KCFG4R(128, 192, 2, 3, 0.34f),
+    SH_KCFG4R(128, 192, 3, 2, 0.34f),
+    SH_KCFG4R(128, 192, 4, 1, 0.34f),
+    SH_KCFG4S(128, 192, 2, 2, 0.36f),
 };
 #undef SH_KCFG
 #undef SH_KCFG2
 #undef SH_KCFG3
 #undef SH_KCFG4
+#undef SH_KCFG4R
+#undef SH_KCFG4S
 constexpr int kNumCfg = sizeof(g_cfgs) / sizeof(g_cfgs[0]);
 
 int env_int(const char *name, int dflt) {
@@ -1012,16 +1217,16 @@ Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t wa
         }
     }
     const int fc = env_int("SH_GEMM_CFG", -1);
-    if (fc >= 0 && fc < kNumCfg && eligible(g_cfgs[fc], vec, fast)) best.cfg = fc;
     const int fs = env_int("SH_GEMM_SPLITS", 0);
     if (fs > 0 && !want_splits) best.splits = (uint32_t)fs;
+    if (fc >= 0 && fc < kNumCfg && eligible(g_cfgs[fc], vec, fast)) best.cfg = fc;
     return best;
 }
 
 void set_attrs(KCfg &c) {
     if (c.attr_set) return;
     for (int v = 0; v < 2; ++v) {
-        (void)hipFuncSetAttribute((const void *)c.vec[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
+        if (c.vec[v]) (void)hipFuncSetAttribute((const void *)c.vec[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
         if (c.scalar[v]) (void)hipFuncSetAttribute((const void *)c.scalar[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
     }
     c.attr_set = true;
@@ -1032,6 +1237,7 @@ void set_grid(GemmArgs &a, const KCfg &c) {
     const uint32_t nblk = a.tiles_m * a.tiles_n * a.splits;
     const int X = sh_num_xcds();
     a.xcd_groups = (X > 1 && nblk % (uint32_t)X == 0) ? (uint32_t)X : 1;
+    a.group_m = (uint32_t)env_int("SH_GEMM_GROUP_M", 0);
 }
 
 // One-time timing of the tile configurations for a large unsplit problem. Every unsplit configuration
@@ -1132,6 +1338,7 @@ int launch(const GemmReq &r, const char *name) {
     const uint32_t nblk = (uint32_t)nblk64;
     const int X = sh_num_xcds();
     a.xcd_groups = (X > 1 && nblk % (uint32_t)X == 0) ? (uint32_t)X : 1;
+    a.group_m = (uint32_t)env_int("SH_GEMM_GROUP_M", 0);
 
     hipStream_t st = sh_stream();
     const bool split = splits > 1;

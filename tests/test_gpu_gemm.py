@@ -72,7 +72,7 @@ def test_real_data_fills(lib, gpu):
 
 
 @pytest.mark.parametrize("K", [136, 192])
-@pytest.mark.parametrize("cfg_index", range(25))
+@pytest.mark.parametrize("cfg_index", range(29))
 def test_every_tile_config(lib, gpu, cfg_index, K, monkeypatch):
     """Each compiled tile shape on a problem with partial tiles in M and N; K = 136 has a K tail (only the
     general kernels take it), K = 192 is a multiple of 64 (the direct-to-LDS kernels take it)."""
@@ -99,18 +99,19 @@ def test_unsplit_tile_configs_store_identical_bits(lib, gpu, monkeypatch):
     x, w = data.normal((M, K), 21), data.normal((K, N), 22, std=1 / np.sqrt(K))
     X, W = to_dev(x), to_dev(w)
     outs = []
-    for cfg_index in range(25):
+    for cfg_index in range(29):
         monkeypatch.setenv("SH_GEMM_CFG", str(cfg_index))
         Z = torch.zeros((M, N), dtype=torch.float16, device="cuda")
         assert lib.sh_gemm_ex(A(X), A(W), A(Z), M, N, K, K, N, N, None, None) == 0, shops.last_error()
         outs.append(to_np(Z).view(np.uint16))
-    # the direct-to-LDS kernels (configurations 6-24, the ones the one-time timing chooses between: 64-k and
-    # 32-k slices, 4 and 8 wavefronts) agree bit for bit; so do the register-staged fallbacks (0-5) among themselves
-    for lo, hi in ((6, 25), (0, 6)):
+    # the direct-to-LDS kernels the one-time timing chooses between (configurations 6-28: 64-k and 32-k slices,
+    # 4 and 8 wavefronts, LDS-staged or register epilogue) agree bit for bit; so do the register-staged fallbacks
+    # (0-5) among themselves
+    for lo, hi in ((6, 29), (0, 6)):
         for i in range(lo, hi):
             assert (outs[i] == outs[lo]).all(), f"config {i} differs from config {lo}"
-    assert refs.close(outs[0].view(np.float16), refs.gemm(x, w))[0] == 0
-    assert refs.close(outs[6].view(np.float16), refs.gemm(x, w))[0] == 0
+    for i in (0, 6):
+        assert refs.close(outs[i].view(np.float16), refs.gemm(x, w))[0] == 0
 
 
 def test_scalar_path_unaligned_views(lib, gpu):
