@@ -51,29 +51,19 @@ struct GemmArgs {
     uint32_t tiles_m, tiles_n, splits;
     uint32_t accumulate, bias_fp32, act;
     uint32_t xcd_groups;         // > 1: XCD-aware block remap with this many XCDs (requires divisibility)
-    uint32_t group_m;            // > 1: tiles ordered in bands of this many tile rows, column by column
 };
 
-// Logical tile L of a launch -> (split, tile row, tile column). Dispatch deals workgroups round-robin over the
-// XCDs, so block b first becomes logical index (b % X) (T / X) + b / X: each XCD walks a contiguous run of the
-// tile order and the operand panels it shares stay in that XCD's L2. The tile order itself is row-major, or
-// (group_m > 1) bands of group_m tile rows walked column by column, which keeps the X row panels and W column
-// panels touched at the same time by one XCD small (the band's rows plus the columns reached so far).
+// Logical tile of block b -> (split, tile row, tile column). Dispatch deals workgroups round-robin over the
+// XCDs, so block b becomes logical index (b % X) (T / X) + b / X: each XCD walks a contiguous run of the
+// row-major tile order and the operand panels it shares stay in that XCD's L2.
 __device__ __forceinline__ void tile_of(const GemmArgs &a, uint32_t b, uint32_t nblk, uint32_t &tm, uint32_t &tn, uint32_t &split) {
     uint32_t L = b;
     if (a.xcd_groups > 1) L = (b % a.xcd_groups) * (nblk / a.xcd_groups) + b / a.xcd_groups;
     const uint32_t per = a.tiles_m * a.tiles_n;
     split = L / per;
     const uint32_t l = L - split * per;
-    if (a.group_m > 1) {
-        const uint32_t band = l / (a.group_m * a.tiles_n), first = band * a.group_m;
-        const uint32_t rows = min(a.tiles_m - first, a.group_m), r = l - band * a.group_m * a.tiles_n;
-        tm = first + r % rows;
-        tn = r / rows;
-    } else {
-        tm = l / a.tiles_n;
-        tn = l % a.tiles_n;
-    }
+    tm = l / a.tiles_n;
+    tn = l % a.tiles_n;
 }
 
 // Zero-filled stand-in read by the epilogue for operands a call does not have (never written).
@@ -1237,7 +1227,6 @@ void set_grid(GemmArgs &a, const KCfg &c) {
     const uint32_t nblk = a.tiles_m * a.tiles_n * a.splits;
     const int X = sh_num_xcds();
     a.xcd_groups = (X > 1 && nblk % (uint32_t)X == 0) ? (uint32_t)X : 1;
-    a.group_m = (uint32_t)env_int("SH_GEMM_GROUP_M", 0);
 }
 
 // One-time timing of the tile configurations for a large unsplit problem. Every unsplit configuration
@@ -1338,7 +1327,6 @@ int launch(const GemmReq &r, const char *name) {
     const uint32_t nblk = (uint32_t)nblk64;
     const int X = sh_num_xcds();
     a.xcd_groups = (X > 1 && nblk % (uint32_t)X == 0) ? (uint32_t)X : 1;
-    a.group_m = (uint32_t)env_int("SH_GEMM_GROUP_M", 0);
 
     hipStream_t st = sh_stream();
     const bool split = splits > 1;
