@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--no-rowops", action="store_true", help="skip the row-op bandwidth measurement")
     ap.add_argument("--graph", action="store_true",
                     help="replay a captured HIP graph of the layer instead of launching its kernels one by one")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the 12-layer stack and the S=1024 attention measurements")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 3 plain device copies of 512 MiB (a known-size kernel for scaling HBM counters)")
     return ap.parse_args()
@@ -134,6 +136,48 @@ def rowops_bandwidth(lib, torch, B: int, S: int, D: int, F: int, H: int, reps: i
                      "frac_of_copy": round(gbs / (cbytes / (cus * 1e-6) / 1e9), 3)}
         del sets
         torch.cuda.empty_cache()
+    return out
+
+
+def extra_configs(lib, torch, enc, x, lp, p, B: int, S: int, D: int, F: int, H: int) -> dict:
+    """The other BASELINE config-4/5 measurements, outside the timed region: the 12-layer stack (layer l reads
+    layer l-1's output; weights of layer l seeded 100 + l) and batched attention at B=8, S=1024."""
+    from softhier_mlir_amd import data, encoder, shops
+    out = {}
+    layers = [encoder.LayerParams.from_host(data.encoder_params(D, F, seed=100 + l)) for l in range(12)]
+    y = torch.empty_like(x)
+    enc.forward(x, layers, B, S, out=y)                 # warm-up (buffers, tile choices)
+    torch.cuda.synchronize()
+    reps = 5
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        enc.forward(x, layers, B, S, out=y)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / reps
+    flop = 12 * encoder.flops_per_layer(B, S, D, F)
+    out["stack12"] = {"layers": 12, "ms_per_forward": round(ms, 3), "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 1)}
+    del layers, y
+    Bl, Sl = 8, 1024
+    A = shops.addr
+    qkv = torch.randn((Bl * Sl, 3 * D), dtype=torch.float16, device="cuda")
+    o = torch.empty((Bl * Sl, D), dtype=torch.float16, device="cuda")
+    D3 = 3 * D
+    def run():
+        rc = lib.sh_attention_batched(A(qkv), A(qkv, D), A(qkv, 2 * D), A(o), Bl, Sl, D, H, D3, D3, D3, D,
+                                      Sl * D3, Sl * D3, Sl * D3, Sl * D, 1.0 / (D // H) ** 0.5, 0)
+        if rc != 0:
+            raise RuntimeError(f"sh_attention_batched failed: {shops.last_error()}")
+    for _ in range(3):
+        run()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(20):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / 20
+    aflop = 4 * Bl * H * Sl * Sl * (D // H)
+    out["attention_b8_s1024"] = {"us": round(us, 2), "TFLOP/s": round(aflop / (us * 1e-6) / 1e12, 1)}
     return out
 
 
@@ -295,6 +339,7 @@ def main() -> int:
                         "frac": round(ach / PEAK_GBS, 4), "traffic": counted_traffic(dom),
                         "algorithmic_bytes_per_launch": c["bytes"], "avg_launch_us": round(us, 2)}
 
+    extra = {} if args.no_extra else extra_configs(lib, torch, enc, x, lp, p, B, S, D, F, H)
     rowops = None if args.no_rowops else rowops_bandwidth(lib, torch, B, S, D, F, H)
     cpu = None if args.no_cpu else cpu_baseline(B, S, D, F, H, p, xh)
 
@@ -307,7 +352,7 @@ def main() -> int:
                    "seq_len": S, "d_model": D, "ffn": F, "heads": H, "layers": 1, "parallelism": "single GPU"},
         "mfma_frac_of_peak": round(value / PEAK_TFLOPS, 4),
         "eager_ms_per_step": round(eager_ms, 4) if eager_ms is not None else None,
-        "roofline": roofline, "breakdown": breakdown, "rowops": rowops, "cpu_baseline": cpu,
+        "roofline": roofline, "breakdown": breakdown, **extra, "rowops": rowops, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -58,7 +58,7 @@ class Encoder:
         self.lib = shops.load()
         self.lib.sh_init()
         self._bufs: dict = {}
-        self._plan = None                    # (key, calls) of the last fused layer's argument set
+        self._plans: dict = {}               # fused-layer call lists by argument set (a stack has one per layer)
         self.gemm_cfg = shops.cfg()          # tile hints 256^3 (library default), as the reference's default policy
         self.tap = None                      # optional tap(name) -> context manager around each op (timing)
 
@@ -69,7 +69,7 @@ class Encoder:
         if self._bufs.get("rows") != rows:
             z = lambda c: torch.empty((rows, c), dtype=torch.float16, device=self.device)  # noqa: E731
             D, F = self.D, self.F
-            self._plan = None
+            self._plans = {}
             self._bufs = {"rows": rows, "ln1": z(D), "qkv": z(3 * D), "q": z(D), "k": z(D), "v": z(D), "o": z(D),
                           "ao": z(D), "h": z(D), "ln2": z(D), "f1": z(F), "g": z(F), "f2": z(D)}
         return self._bufs
@@ -106,8 +106,9 @@ class Encoder:
     def _fused_plan(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int) -> list:
         """The layer's library calls with every argument converted once: (op name, function, args, what)."""
         key = (x.data_ptr(), out.data_ptr(), B, S) + tuple(t.data_ptr() for t in p.t.values())
-        if self._plan is not None and self._plan[0] == key:
-            return self._plan[1]
+        hit = self._plans.get(key)
+        if hit is not None:
+            return hit
         L, A = self.lib, shops.addr
         D, F, H, rows = self.D, self.F, self.H, B * S
         b = self.buffers(rows)
@@ -128,7 +129,9 @@ class Encoder:
             ("ffn_down", L.sh_gemm_ex, (A(b["g"]), A(p["w2"]), A(out), rows, D, F, F, D, D, cfg,
                                         shops.epi(bias=A(p["b2"]), residual=A(b["h"]), ldr=D)), "sh_gemm_ex w2"),
         ]
-        self._plan = (key, calls)
+        if len(self._plans) >= 64:            # bounded: argument sets of retired buffers are dropped
+            self._plans.clear()
+        self._plans[key] = calls
         return calls
 
     def layer_fused(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int) -> torch.Tensor:
@@ -179,7 +182,12 @@ class Encoder:
         step = self.layer_fused if sequence == "fused" else self.layer_reference
         n = len(params)
         out = out if out is not None else torch.empty_like(x)
-        tmp = torch.empty_like(x) if n > 1 else None
+        tmp = None
+        if n > 1:                               # the ping-pong buffer persists, so the call plans stay valid
+            tmp = self._bufs.get("pingpong")
+            if tmp is None or tmp.shape != x.shape or tmp.dtype != x.dtype:
+                tmp = torch.empty_like(x)
+                self._bufs["pingpong"] = tmp
         cur = x
         for i, p in enumerate(params):          # ping-pong so that the last layer writes `out`
             dst = out if (n - 1 - i) % 2 == 0 else tmp
