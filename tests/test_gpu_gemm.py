@@ -178,6 +178,59 @@ def test_fused_epilogue_is_the_library_sequence_bitwise(lib, gpu, act, accumulat
     assert len(bad) == 0, f"{len(bad)} differ, e.g. " + ", ".join(f"{tuple(ix)}: {z1[tuple(ix)]:04x} vs {z2[tuple(ix)]:04x}" for ix in bad[:6])
 
 
+# (bias format, act, residual, accumulate): every branch of the epilogue chain, including the register epilogue's
+# two load paths (fp16 bias / residual in one batch; z_old or an fp32 bias per row and column block)
+EPI_CASES = [(shops.SH_BIAS_FP16, shops.SH_ACT_GELU, True, 0), (shops.SH_BIAS_FP32, shops.SH_ACT_NONE, True, 1),
+             (shops.SH_BIAS_FP32, shops.SH_ACT_GELU, False, 0), (None, shops.SH_ACT_NONE, False, 1),
+             (None, shops.SH_ACT_NONE, False, 0)]
+
+
+@pytest.mark.parametrize("splits", [1, 3])
+@pytest.mark.parametrize("case", range(len(EPI_CASES)))
+def test_epilogue_chain_same_bits_on_every_tile(lib, gpu, monkeypatch, case, splits):
+    """Each epilogue combination on partial tiles (M, N not multiples of any tile), on the LDS-staged and the
+    register-epilogue tile configurations (6: k_gemm2; 23, 24: k_gemm4 staged; 25-28: k_gemm4 register epilogue,
+    32- and 64-k slices): every configuration stores the same bits (split or not), nothing outside the output view
+    changes, and the result is within tolerance of the oracle's unfused sequence."""
+    import torch
+    bias_fmt, act, res, accumulate = EPI_CASES[case]
+    M, N, K, ldz = 328, 200, 192, 208
+    x, w = data.normal((M, K), 51), data.normal((K, N), 52, std=1 / np.sqrt(K))
+    b32 = data.normal((1, N), 53, std=0.3).astype(np.float32)
+    r, z0 = data.normal((M, N), 54), data.normal((M, N), 55)
+    X, W, R = to_dev(x), to_dev(w), to_dev(r)
+    bias = None
+    if bias_fmt == shops.SH_BIAS_FP32:
+        bias = torch.from_numpy(b32).cuda()
+    elif bias_fmt == shops.SH_BIAS_FP16:
+        bias = to_dev(b32.astype(np.float16))
+    outs = {}
+    for cfg_index in (6, 23, 24, 25, 26, 27, 28):
+        monkeypatch.setenv("SH_GEMM_CFG", str(cfg_index))
+        Z = torch.full((M + 3, ldz), 7.0, dtype=torch.float16, device="cuda")
+        Z[:M, :N] = to_dev(z0)
+        e = shops.epi(bias=A(bias) if bias is not None else 0, bias_fmt=bias_fmt or 0, act=act,
+                      residual=A(R) if res else 0, ldr=N if res else 0, splits=splits)
+        c = shops.cfg(accumulate=accumulate)
+        assert lib.sh_gemm_ex(A(X), A(W), A(Z), M, N, K, K, N, ldz, c, e) == 0, shops.last_error()
+        z = to_np(Z)
+        assert (z[:M, N:] == 7.0).all() and (z[M:] == 7.0).all(), f"config {cfg_index} wrote outside the view"
+        outs[cfg_index] = z[:M, :N].view(np.uint16).copy()
+    for cfg_index, o in outs.items():
+        assert (o == outs[6]).all(), f"config {cfg_index} differs from config 6 in {(o != outs[6]).sum()} elements"
+    # the reference's unfused order: Z (+)= XW, + bias, GELU, + residual, each stored in fp16
+    want = refs.gemm(x, w, z0 if accumulate else None)
+    if bias is not None:
+        bb = b32 if bias_fmt == shops.SH_BIAS_FP32 else b32.astype(np.float16).astype(np.float32)
+        want = refs.r16(want + bb)
+    if act == shops.SH_ACT_GELU:
+        want = refs.r16(refs.gelu(want))
+    if res:
+        want = want + r.astype(np.float32)
+    bad, err, _ = refs.close(outs[6].view(np.float16), want)
+    assert bad == 0, err
+
+
 def test_splitk_matches_and_is_deterministic(lib, gpu):
     """BASELINE config 2 FFN-down: M=256, K=3072, N=768, split-K = 4."""
     M, N, K = 256, 768, 3072
