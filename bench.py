@@ -41,6 +41,9 @@ def parse():
     ap.add_argument("--no-rowops", action="store_true", help="skip the row-op bandwidth measurement")
     ap.add_argument("--graph", action="store_true",
                     help="replay a captured HIP graph of the layer instead of launching its kernels one by one")
+    ap.add_argument("--configs", action="store_true",
+                    help="instead of the layer line: every BASELINE config on its own (time, parity, CPU oracle time), "
+                         "one JSON line each")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the 12-layer stack and the S=1024 attention measurements")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -181,6 +184,192 @@ def extra_configs(lib, torch, enc, x, lp, p, B: int, S: int, D: int, F: int, H: 
     return out
 
 
+def config_table(lib, torch) -> list:
+    """Every BASELINE.json config on its own (`--configs`): GPU time (median of 60 single launches with HIP events
+    around each, after warm-up), parity against the oracle's restatement (which is also the timed CPU baseline:
+    median of 5 runs, 3 for the long ones), and the roofline fraction: FLOP-type ops against min(MFMA peak,
+    AI x HBM peak), byte-type ops against the HBM peak."""
+    import numpy as np
+
+    from oracle import refs
+    from softhier_mlir_amd import data, encoder, shops
+    A = shops.addr
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    host = lambda t: t.cpu().numpy()  # noqa: E731
+    rows = []
+
+    batched = {}
+
+    def gpu_us(fn, n=60):
+        """Median of n single launches with events around each; the average of n launches back to back (events
+        around all of them, dispatch pipelined) is kept for the record."""
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(n):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            ts.append((e0, e1))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        batched["us"] = e0.elapsed_time(e1) * 1e3 / n
+        ms = sorted(a.elapsed_time(b) for a, b in ts)
+        return ms[len(ms) // 2] * 1e3
+
+    def cpu_ms(fn, n=5):
+        fn()
+        ts = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[len(ts) // 2] * 1e3
+
+    def record(name, shape, us, flop, nbytes, got, want, cpu, exact=False, note=""):
+        bad, err, _ = refs.close(got, want)
+        g32, w32 = np.asarray(got, np.float32), np.asarray(want, np.float32)
+        rel = float(np.max(np.abs(g32 - w32) / np.maximum(np.abs(w32), 1e-3)))
+        row = {"config": name, "shape": shape, "us": round(us, 2), "us_batched": round(batched["us"], 2),
+               "max_abs_err": round(err, 6), "max_rel_err": round(rel, 5), "outside_tol": bad, "cpu_ms": round(cpu, 3)}
+        if exact:
+            row["bit_exact"] = bool(np.array_equal(np.asarray(got).view(np.uint16), np.asarray(want).view(np.uint16)))
+        ub = batched["us"]
+        if flop:
+            ai = flop / nbytes
+            bound = min(PEAK_TFLOPS * 1e12, ai * PEAK_GBS * 1e9)
+            row.update({"TFLOP/s": round(flop / (us * 1e-6) / 1e12, 2), "TFLOP/s_batched": round(flop / (ub * 1e-6) / 1e12, 2),
+                        "AI": round(ai, 1), "roofline_TFLOP/s": round(bound / 1e12, 1), "frac": round(flop / (us * 1e-6) / bound, 3)})
+        else:
+            row.update({"GB/s": round(nbytes / (us * 1e-6) / 1e9, 1), "GB/s_batched": round(nbytes / (ub * 1e-6) / 1e9, 1),
+                        "frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_GBS, 3)})
+        if note:
+            row["note"] = note
+        rows.append(row)
+        print(json.dumps(row), flush=True)
+
+    # config 1: Z[256x256] = X.W, uniform [-1, 1] from the seeded LCG
+    x, w = data.uniform(256, 256, 1), data.uniform(256, 256, 2)
+    X, W = dev(x), dev(w)
+    Z = torch.empty((256, 256), dtype=torch.float16, device="cuda")
+    us = gpu_us(lambda: lib.sh_gemm(A(X), A(W), A(Z), 256, 256, 256, 256, 256, 256, None, shops.SH_ALL))
+    cpu = cpu_ms(lambda: refs.r16(refs.gemm(x, w)))
+    record("1 gemm 256^3", [256, 256, 256], us, 2 * 256 ** 3, 3 * 256 * 256 * 2, host(Z), refs.r16(refs.gemm(x, w)), cpu)
+
+    # config 2: the encoder's GEMM shapes at M = 256 with an fp32 bias U[-0.1, 0.1]; weights scaled by 1/sqrt(K)
+    for name, (M, N, K, act, splits) in {"2 qkv 256x768->2304 +bias": (256, 2304, 768, 0, 1),
+                                          "2 ffn_up 256x768->3072 +bias+gelu": (256, 3072, 768, shops.SH_ACT_GELU, 1),
+                                          "2 ffn_down 256x3072->768 +bias split-K 4": (256, 768, 3072, 0, 4)}.items():
+        x = data.uniform(M, K, 3)
+        w = (data.uniform(K, N, 4).astype(np.float32) / np.sqrt(K)).astype(np.float16)
+        b = (data.uniform(1, N, 5).astype(np.float32) * np.float32(0.1))
+        X, W, Bb = dev(x), dev(w), dev(b)
+        Z = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        e = shops.epi(bias=A(Bb), bias_fmt=shops.SH_BIAS_FP32, act=act, splits=splits)
+        us = gpu_us(lambda: lib.sh_gemm_ex(A(X), A(W), A(Z), M, N, K, K, N, N, None, e))
+
+        def ref(x=x, w=w, b=b, act=act):
+            z = refs.r16(refs.r16(refs.gemm(x, w)) + b)
+            return refs.r16(refs.gelu(z)) if act else z
+        cpu = cpu_ms(ref)
+        record(name, [M, K, N], us, 2 * M * N * K, 2 * (M * K + K * N + M * N) + 4 * N, host(Z), ref(), cpu)
+    x = np.full((1024, 1024), 1.0, np.float16)
+    w = np.full((1024, 1024), 1.0 / 1024, np.float16)
+    X, W = dev(x), dev(w)
+    Z = torch.empty((1024, 1024), dtype=torch.float16, device="cuda")
+    cfg = shops.cfg(256, 256, 256)
+    us = gpu_us(lambda: lib.sh_gemm_mesh(A(X), A(W), A(Z), 1024, 1024, 1024, 1024, 1024, 1024, cfg))
+    xs, ws = data.uniform(1024, 1024, 6), (data.uniform(1024, 1024, 7).astype(np.float32) / 32).astype(np.float16)
+    Xs, Ws = dev(xs), dev(ws)
+    assert lib.sh_gemm_mesh(A(Xs), A(Ws), A(Z), 1024, 1024, 1024, 1024, 1024, 1024, cfg) == 0
+    cpu = cpu_ms(lambda: refs.r16(refs.gemm(xs, ws)))
+    record("2 summa 1024^3 (mesh mode)", [1024, 1024, 1024], us, 2 * 1024 ** 3, 3 * 1024 * 1024 * 2, host(Z),
+           refs.r16(refs.gemm(xs, ws)), cpu, note="timed on X=1, W=1/1024 (examples/gemm1024_summa.mlir:5), parity on LCG data")
+
+    # config 3: row ops at the configured shapes, values N(0, 1) unless stated
+    M, D, F = 256, 768, 3072
+    x = data.normal((M, D), 11)
+    g, be = data.normal((1, D), 12, 1.0, 0.02), data.normal((1, D), 13, 0.0, 0.02)
+    Xd, G, Be = dev(x), dev(g), dev(be)
+    Y = torch.empty_like(Xd)
+    us = gpu_us(lambda: lib.sh_layernorm(A(Y), A(Xd), A(G), A(Be), M, D, D, 1e-6, shops.SH_ALL))
+    cpu = cpu_ms(lambda: refs.r16(refs.layernorm(x, g, be, 1e-6)))
+    record("3 layernorm [256x768]", [M, D], us, 0, 2 * (2 * M * D + 2 * D), host(Y), refs.r16(refs.layernorm(x, g, be, 1e-6)), cpu)
+    xs_ = data.normal((12 * 256, 256), 14, 0.0, 3.0)
+    Xs_ = dev(xs_)
+    Ys_ = torch.empty_like(Xs_)
+    us = gpu_us(lambda: lib.sh_softmax_rows(A(Ys_), A(Xs_), 12 * 256, 256, 256, 0.125, shops.SH_ALL))
+    cpu = cpu_ms(lambda: refs.r16(refs.softmax(xs_, 0.125)))
+    record("3 softmax [12x256x256] scale 1/8", [12 * 256, 256], us, 0, 2 * 2 * 12 * 256 * 256, host(Ys_),
+           refs.r16(refs.softmax(xs_, 0.125)), cpu)
+    xg = data.normal((M, F), 15)
+    Xg = dev(xg)
+    Yg = torch.empty_like(Xg)
+    us = gpu_us(lambda: lib.sh_gelu(A(Yg), A(Xg), M, F, F, shops.SH_ALL))
+    cpu = cpu_ms(lambda: refs.r16(refs.gelu(xg)))
+    record("3 gelu [256x3072]", [M, F], us, 0, 2 * 2 * M * F, host(Yg), refs.r16(refs.gelu(xg)), cpu)
+    a2 = data.normal((M, D), 16)
+    A2 = dev(a2)
+    us = gpu_us(lambda: lib.sh_add(A(Y), A(Xd), A(A2), M, D, D, shops.SH_ALL))
+    cpu = cpu_ms(lambda: refs.r16(refs.add(x, a2)))
+    record("3 add [256x768]", [M, D], us, 0, 2 * 3 * M * D, host(Y), refs.r16(refs.add(x, a2)), cpu)
+    us = gpu_us(lambda: lib.sh_add_bias(A(Y), A(Xd), A(Be), M, D, D, shops.SH_ALL))
+    cpu = cpu_ms(lambda: refs.r16(refs.add_bias(x, be)))
+    record("3 add_bias [256x768]", [M, D], us, 0, 2 * (2 * M * D + D), host(Y), refs.r16(refs.add_bias(x, be)), cpu)
+    # transpose of a [768 x 256] view (ld 264) into a [256 x 768] view (ld 776): bit-exact
+    src = data.normal((768, 264), 17)
+    Src = dev(src)
+    Dst = torch.zeros((256, 776), dtype=torch.float16, device="cuda")
+    us = gpu_us(lambda: lib.sh_transpose(A(Dst), A(Src), 768, 256, 264, 776, shops.SH_ALL))
+    cpu = cpu_ms(lambda: np.ascontiguousarray(src[:, :256].T))
+    record("3 transpose [768x256] strided views", [768, 256], us, 0, 2 * 2 * 768 * 256, host(Dst)[:, :768],
+           np.ascontiguousarray(src[:, :256].T), cpu, exact=True)
+
+    # config 4: attention, q/k/v ~ N(0, 1) [B*S, 768], 12 heads, scale 0.125
+    for Bq, Sq in ((32, 256), (8, 1024)):
+        q, k, v = (data.normal((Bq * Sq, 768), s_) for s_ in (21, 22, 23))
+        Q, Kt, V = dev(q), dev(k), dev(v)
+        O = torch.empty_like(Q)
+        us = gpu_us(lambda: lib.sh_attention_batched(A(Q), A(Kt), A(V), A(O), Bq, Sq, 768, 12, 768, 768, 768, 768,
+                                                       Sq * 768, Sq * 768, Sq * 768, Sq * 768, 0.125, 0))
+        cpu = cpu_ms(lambda: refs.attention_batched(q, k, v, Bq, 12, 0.125), n=3)
+        record(f"4 attention B={Bq} S={Sq}", [Bq, Sq, 12, 64], us, 4 * Bq * 12 * Sq * Sq * 64, 2 * 4 * Bq * Sq * 768,
+               host(O), refs.attention_batched(q, k, v, Bq, 12, 0.125), cpu)
+
+    # config 5: the encoder layer (B = 32) and the 12-layer stack (parity on B = 2 sequences)
+    Dm, Fm, Hm, Bm, Sm = 768, 3072, 12, 32, 256
+    enc = encoder.Encoder(Dm, Fm, Hm)
+    p = data.encoder_params(Dm, Fm, seed=100)
+    lp = encoder.LayerParams.from_host(p)
+    xh = data.normal((Bm * Sm, Dm), 7)
+    Xe = dev(xh)
+    Oe = torch.empty_like(Xe)
+    us = gpu_us(lambda: enc.layer_fused(Xe, Oe, lp, Bm, Sm), n=50)
+    cpu = cpu_ms(lambda: refs.encoder_layer(xh, p, Hm, B=Bm), n=3)
+    fl = encoder.flops_per_layer(Bm, Sm, Dm, Fm)
+    lb = sum(c["bytes"] for c in encoder.Encoder.op_costs(Bm, Sm, Dm, Fm, Hm).values())   # algorithmic bytes per layer
+    record("5 encoder layer B=32 (fused sequence)", [Bm, Sm, Dm, Fm, Hm], us, fl, lb,
+           host(Oe), refs.encoder_layer(xh, p, Hm, B=Bm), cpu)
+    ps = [data.encoder_params(Dm, Fm, seed=100 + l) for l in range(12)]
+    lps = [encoder.LayerParams.from_host(pp) for pp in ps]
+    us = gpu_us(lambda: enc.forward(Xe, lps, Bm, Sm, out=Oe), n=10)
+    x2 = xh[: 2 * Sm]
+    X2 = dev(x2)
+    O2 = torch.empty_like(X2)
+    enc.forward(X2, lps, 2, Sm, out=O2)
+    cpu = cpu_ms(lambda: refs.encoder_stack(x2, ps, Hm, B=2), n=3)
+    record("5 encoder 12 layers B=32 (parity on 2 sequences)", [Bm, Sm, Dm, Fm, Hm, 12], us, 12 * fl,
+           12 * lb, host(O2), refs.encoder_stack(x2, ps, Hm, B=2), cpu,
+           note="cpu_ms is the oracle on 2 sequences")
+    return rows
+
+
 def cpu_baseline(B: int, S: int, D: int, F: int, H: int, p: dict, x) -> dict:
     """The oracle's numpy restatement of one encoder layer, timed on this host's cores (median of 5)."""
     import numpy as np
@@ -221,6 +410,9 @@ def main() -> int:
 
     lib = shops.load()
     lib.sh_init()
+    if args.configs:
+        config_table(lib, torch)
+        return 0
     B, S, D, F, H = args.batch, args.seq, 768, 3072, 12
     p = data.encoder_params(D, F, seed=100)
     xh = data.normal((B * S, D), 7)
