@@ -1174,13 +1174,43 @@ int env_int(const char *name, int dflt) {
     return (e && *e) ? atoi(e) : dflt;
 }
 
-// Estimated seconds of config c for an (M, N, K) problem cut into `splits` K ranges: rounds of tiles
-// over the CUs at the config's sustained MFMA fraction, plus the split-K partial traffic.
-double est_time(const KCfg &c, uint32_t M, uint32_t N, uint32_t K, uint32_t splits, int cus) {
+void set_attrs(KCfg &c);
+
+// Workgroups of config i resident on one CU (HIP's occupancy query, once per config; 1 if it fails).
+int resident(int i) {
+    static int occ[kNumCfg] = {};
+    if (!occ[i]) {
+        KCfg &c = g_cfgs[i];
+        set_attrs(c);
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void *)c.vec[0], c.threads, c.lds) != hipSuccess || n < 1) {
+            (void)hipGetLastError();
+            n = 1;
+        }
+        occ[i] = n;
+    }
+    return occ[i];
+}
+
+// Estimated seconds of config i for an (M, N, K) problem cut into `splits` K ranges: the larger of
+//  - throughput: rounds of tiles over the CUs at the config's sustained MFMA fraction, and
+//  - latency: one workgroup's start-up and epilogue plus its chain of BK slices, once per wave of resident
+//    workgroups. Both costs grow with the tile area A (in units of 1024 outputs); fitted to single-round
+//    kernel traces on MI355X (256 x {256, 2304, 768} x {256, 768, 3072} and 1024^3): direct-to-LDS kernels
+//    3.0 + 0.16 A us + (0.17 + 0.02 A) us per slice, the register-staged kernel 1.0 + 0.32 A us +
+//    (0.88 + 0.013 A) us per slice. Small problems are latency-bound, large ones throughput-bound;
+// plus the split-K partial traffic and the reduction launch.
+double est_time(int i, uint32_t M, uint32_t N, uint32_t K, uint32_t splits, int cus) {
+    const KCfg &c = g_cfgs[i];
     const double tiles = (double)sh_cdiv(M, c.bm) * sh_cdiv(N, c.bn) * splits;
     const double rounds = std::ceil(tiles / cus);
     const double k_len = (double)sh_cdiv(sh_cdiv(std::max<uint32_t>(K, 1), splits), BK) * BK;
     double t = rounds * c.bm * c.bn * k_len / (c.eff * 2048.0 * 2.4e9);
+    const double A = c.bm * c.bn / 1024.0;
+    const double fixed_us = c.v2 ? 3.0 + 0.16 * A : 1.0 + 0.32 * A;
+    const double slice_us = c.v2 ? 0.17 + 0.02 * A : 0.88 + 0.013 * A;
+    const double waves = std::ceil(tiles / ((double)cus * resident(i)));
+    t = std::max(t, 1e-6 * (fixed_us + waves * (k_len / BK) * slice_us));
     if (splits > 1) t += ((double)splits * M * N * 8.0 + (double)M * N * 2.0) / 5e12 + 4e-6;
     return t;
 }
@@ -1202,7 +1232,7 @@ Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t wa
         if (want_splits) lo = hi = want_splits;
         else hi = std::max<uint32_t>(1, std::min<uint32_t>(16, K / 128));
         for (uint32_t s = lo; s <= hi; ++s) {
-            const double tt = est_time(g_cfgs[i], M, N, K, s, cus);
+            const double tt = est_time(i, M, N, K, s, cus);
             if (tt < bt * 0.97) { bt = tt; best = {i, s}; }
         }
     }
@@ -1240,7 +1270,7 @@ int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st) {
     static const int enabled = env_int("SH_GEMM_TUNE", 1);
     if (!enabled || env_int("SH_GEMM_CFG", -1) >= 0) return heur;
     const int cus = sh_num_cus() > 0 ? sh_num_cus() : 256;
-    if (est_time(g_cfgs[heur], call.M, call.N, call.K, 1, cus) < 12e-6) return heur;
+    if (est_time(heur, call.M, call.N, call.K, 1, cus) < 12e-6) return heur;
     const TuneKey key{call.M, call.N, call.K, call.ldx, call.ldw, call.bias ? 1u + call.bias_fp32 : 0u, call.act};
     auto it = g_tuned.find(key);
     if (it != g_tuned.end()) return it->second;
