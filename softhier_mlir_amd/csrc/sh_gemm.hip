@@ -23,6 +23,7 @@
 #include "sh_common.h"
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -1174,33 +1175,16 @@ int env_int(const char *name, int dflt) {
     return (e && *e) ? atoi(e) : dflt;
 }
 
-void set_attrs(KCfg &c);
-
-// Workgroups of config i resident on one CU (HIP's occupancy query, once per config; 1 if it fails).
-int resident(int i) {
-    static int occ[kNumCfg] = {};
-    if (!occ[i]) {
-        KCfg &c = g_cfgs[i];
-        set_attrs(c);
-        int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void *)c.vec[0], c.threads, c.lds) != hipSuccess || n < 1) {
-            (void)hipGetLastError();
-            n = 1;
-        }
-        occ[i] = n;
-    }
-    return occ[i];
-}
-
 // Estimated seconds of config i for an (M, N, K) problem cut into `splits` K ranges: the larger of
-//  - throughput: rounds of tiles over the CUs at the config's sustained MFMA fraction, and
-//  - latency: one workgroup's start-up and epilogue plus its chain of BK slices, once per wave of resident
-//    workgroups. Both costs grow with the tile area A (in units of 1024 outputs); fitted to single-round
+//  - throughput: rounds of tiles over the CUs at the config's sustained MFMA fraction (also returned alone
+//    in *thr), and
+//  - latency: no workgroup finishes before its start-up and epilogue plus its chain of BK slices, counted
+//    once per round of tiles. Both costs grow with the tile area A (in units of 1024 outputs); fitted to
 //    kernel traces on MI355X (256 x {256, 2304, 768} x {256, 768, 3072} and 1024^3): direct-to-LDS kernels
-//    3.0 + 0.16 A us + (0.17 + 0.02 A) us per slice, the register-staged kernel 1.0 + 0.32 A us +
-//    (0.88 + 0.013 A) us per slice. Small problems are latency-bound, large ones throughput-bound;
-// plus the split-K partial traffic and the reduction launch.
-double est_time(int i, uint32_t M, uint32_t N, uint32_t K, uint32_t splits, int cus) {
+//    3.0 + 0.16 A us + (0.17 + 0.02 A) us per slice, the register-staged kernel 1.0 + 0.32 A us + (0.88 +
+//    0.013 A) us per slice;
+// plus, in both, the split-K partial traffic and the reduction launch. Small problems are latency-bound.
+double est_time(int i, uint32_t M, uint32_t N, uint32_t K, uint32_t splits, int cus, double *thr = nullptr) {
     const KCfg &c = g_cfgs[i];
     const double tiles = (double)sh_cdiv(M, c.bm) * sh_cdiv(N, c.bn) * splits;
     const double rounds = std::ceil(tiles / cus);
@@ -1209,10 +1193,10 @@ double est_time(int i, uint32_t M, uint32_t N, uint32_t K, uint32_t splits, int 
     const double A = c.bm * c.bn / 1024.0;
     const double fixed_us = c.v2 ? 3.0 + 0.16 * A : 1.0 + 0.32 * A;
     const double slice_us = c.v2 ? 0.17 + 0.02 * A : 0.88 + 0.013 * A;
-    const double waves = std::ceil(tiles / ((double)cus * resident(i)));
-    t = std::max(t, 1e-6 * (fixed_us + waves * (k_len / BK) * slice_us));
-    if (splits > 1) t += ((double)splits * M * N * 8.0 + (double)M * N * 2.0) / 5e12 + 4e-6;
-    return t;
+    const double lat = 1e-6 * (fixed_us + rounds * (k_len / BK) * slice_us);
+    const double split_cost = splits > 1 ? ((double)splits * M * N * 8.0 + (double)M * N * 2.0) / 5e12 + 4e-6 : 0.0;
+    if (thr) *thr = t + split_cost;
+    return std::max(t, lat) + split_cost;
 }
 
 struct Plan { int cfg; uint32_t splits; };
@@ -1224,18 +1208,29 @@ bool eligible(const KCfg &c, bool vec, bool fast) {
 
 Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t want_splits) {
     const int cus = sh_num_cus() > 0 ? sh_num_cus() : 256;
-    Plan best{4, 1};
-    double bt = 1e300;
+    // Every eligible (config, splits) is estimated; among those within 3 % of the fastest estimate the one with
+    // the lowest throughput term wins (tiles of one size share one latency floor; the throughput term ranks
+    // them), the earlier config and fewer splits on a tie.
+    struct Cand { double t, thr; int cfg; uint32_t splits; };
+    Cand cand[kNumCfg * 16];
+    int n = 0;
+    double tmin = 1e300;
     for (int i = 0; i < kNumCfg; ++i) {
         if (!eligible(g_cfgs[i], vec, fast)) continue;
         uint32_t lo = 1, hi = 1;
         if (want_splits) lo = hi = want_splits;
         else hi = std::max<uint32_t>(1, std::min<uint32_t>(16, K / 128));
-        for (uint32_t s = lo; s <= hi; ++s) {
-            const double tt = est_time(i, M, N, K, s, cus);
-            if (tt < bt * 0.97) { bt = tt; best = {i, s}; }
+        for (uint32_t s = lo; s <= hi && n < kNumCfg * 16; ++s) {
+            double thr = 0.0;
+            const double tt = est_time(i, M, N, K, s, cus, &thr);
+            cand[n++] = {tt, thr, i, s};
+            tmin = std::min(tmin, tt);
         }
     }
+    Plan best{4, 1};
+    double bthr = 1e300;
+    for (int j = 0; j < n; ++j)
+        if (cand[j].t <= tmin * 1.03 && cand[j].thr < bthr) { bthr = cand[j].thr; best = {cand[j].cfg, cand[j].splits}; }
     const int fc = env_int("SH_GEMM_CFG", -1);
     const int fs = env_int("SH_GEMM_SPLITS", 0);
     if (fs > 0 && !want_splits) best.splits = (uint32_t)fs;
@@ -1270,7 +1265,9 @@ int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st) {
     static const int enabled = env_int("SH_GEMM_TUNE", 1);
     if (!enabled || env_int("SH_GEMM_CFG", -1) >= 0) return heur;
     const int cus = sh_num_cus() > 0 ? sh_num_cus() : 256;
-    if (est_time(heur, call.M, call.N, call.K, 1, cus) < 12e-6) return heur;
+    double thr = 0.0;
+    (void)est_time(heur, call.M, call.N, call.K, 1, cus, &thr);
+    if (thr < 12e-6) return heur;                    // the throughput estimate: small problems keep the model's tile
     const TuneKey key{call.M, call.N, call.K, call.ldx, call.ldw, call.bias ? 1u + call.bias_fp32 : 0u, call.act};
     auto it = g_tuned.find(key);
     if (it != g_tuned.end()) return it->second;
@@ -1306,6 +1303,13 @@ int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st) {
             float best_ms = 1e30f;
             for (int i = 0; i < kNumCfg; ++i)
                 if (g_cfgs[i].v2 && mins[i] < best_ms) { best_ms = mins[i]; best = i; }
+            if (env_int("SH_GEMM_VERBOSE", 0)) {      // the one-time choice on stderr: model pick, winner, all times
+                fprintf(stderr, "[sh_gemm] tuned %ux%ux%u: model cfg %d (%.2f us), chose cfg %d (%.2f us);", call.M, call.N, call.K,
+                        heur, 500.f * mins[heur], best, 500.f * best_ms);
+                for (int i = 0; i < kNumCfg; ++i)
+                    if (g_cfgs[i].v2) fprintf(stderr, " %d:%.2f", i, 500.f * mins[i]);
+                fprintf(stderr, "\n");
+            }
         }
     }
     if (e0) (void)hipEventDestroy(e0);
