@@ -430,9 +430,16 @@ __global__ __launch_bounds__(256) void k_flash_dma(AttnArgs a) {
 // maximum known, needs no running rescale of O or l: p = 2^(c s - m), P (fp16) feeds O^T += V^T . P^T, and
 // the row sums l come from one more MFMA with an all-ones A operand (the sums of the fp16 numerators the
 // PV product used). Masking of keys past S happens only in the last, partial key block.
+// FOLD (|c| <= 1, so c q stays in fp16 range): the softmax VALU work shrinks by folding c and m into the score
+// MFMAs. The query fragments are scaled once, q' = r16(c q), so the scores come out as c s (pass 1 then takes
+// a plain maximum for either sign of c), and pass 2 adds one more 16-k MFMA step per score tile whose
+// operands are ones (keys) and -m_hi, -m_lo (queries; m_hi = r16(m), m_lo = r16(m - m_hi)), so the
+// accumulator already holds c s - m and p = 2^acc needs no VALU multiply-add. An error in m common to a
+// query's row scales its numerators and its row sum alike and cancels in O / l; the rounding of c q changes
+// each exponent by ~1e-4 relative.
 // Occupancy: with a 2-stage ring (32 KB of LDS) a dh = 64 workgroup fits in 168 registers per lane, so three
 // workgroups share a CU (12 waves); the encoder's 768 (sequence, head, query block) workgroups then run in one round.
-template <int DH, int NST, bool MASK>
+template <int DH, int NST, bool MASK, bool FOLD>
 __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a) {
     constexpr int DC = DH / 8, NS = DH / 16, DT = DH / 32;
     constexpr int KCH = KB * DC;                     // 16-byte chunks per K (or V) block
@@ -483,13 +490,25 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a) {
     sh_h8 qf[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) qf[s] = __builtin_bit_cast(sh_h8, ld8<true>(Q, a.ldq, myq, 16 * s + 8 * g, S, DH));
+    if constexpr (FOLD) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qf[s][e] = (_Float16)((float)qf[s][e] * a.c);
+    }
+    // FOLD: operands of the bias step (k elements 0 and 1 of lane group 0): ones for every key, -m_hi, -m_lo
+    // of this lane's query (set once m is known)
+    sh_h8 kbias = {}, qbias = {};
+    if (FOLD && g == 0) { kbias[0] = (_Float16)1.0f; kbias[1] = (_Float16)1.0f; }
 
     // S^T tile pair of key block in stage st: sacc[tt][r] = s(key 32 tt + 8 (r/4) + 4 g + r%4, query r32)
-    auto scores = [&](int st, sh_f16v (&sacc)[2]) {
+    // (FOLD: c s, and with bias, c s - m)
+    auto scores = [&](int st, sh_f16v (&sacc)[2], bool bias) {
         const uint4 *sk = smem + st * 2 * KCH;
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
             sacc[tt] = sh_f16v{};
+            if (FOLD && bias) sacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kbias, qbias, sacc[tt], 0, 0, 0);
             const uint32_t key = 32 * tt + r32;
 #pragma unroll
             for (int s = 0; s < NS; ++s) {
@@ -505,8 +524,8 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a) {
         return key < S && (uint32_t)a.tok[min(key, S - 1)] <= tq;
     };
 
-    // ---- pass 1: extreme of s over all keys (max for c >= 0, min for c < 0), K blocks only ----
-    const bool pos = a.c >= 0.f;
+    // ---- pass 1: extreme of s over all keys (max for c >= 0, min for c < 0; FOLD: max of c s), K blocks only ----
+    const bool pos = FOLD || a.c >= 0.f;
 #pragma unroll
     for (int s = 0; s < NST - 1; ++s) issue(min((uint32_t)s, nkb - 1), s, false);
     float ext = pos ? -INFINITY : INFINITY;
@@ -515,7 +534,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a) {
         __syncthreads();
         issue(min(kb + NST - 1, nkb - 1), (int)((kb + NST - 1) % NST), false);
         sh_f16v sacc[2];
-        scores((int)(kb % NST), sacc);
+        scores((int)(kb % NST), sacc, false);
         if (MASK || (ragged && kb == nkb - 1)) {
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt)
@@ -537,7 +556,12 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a) {
     }
     ext = pos ? fmaxf(ext, __shfl_xor(ext, 32, 64)) : fminf(ext, __shfl_xor(ext, 32, 64));
     if (MASK) uni = uni || ext == -INFINITY;
-    const float m = (MASK && uni) ? 0.f : a.c * ext;   // max over keys of c s
+    const float m = (MASK && uni) ? 0.f : (FOLD ? ext : a.c * ext);   // max over keys of c s
+    if (FOLD && g == 0) {
+        const _Float16 mh = (_Float16)m;
+        qbias[0] = -mh;
+        qbias[1] = -(_Float16)(m - (float)mh);
+    }
     attn_wait_vmcnt<0>();                            // the ring is idle before pass 2 refills it
     __syncthreads();
 
@@ -557,14 +581,14 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a) {
         issue(min(kb + NST - 1, nkb - 1), (int)((kb + NST - 1) % NST), true);
         const int st = (int)(kb % NST);
         sh_f16v sacc[2];
-        scores(st, sacc);
+        scores(st, sacc, true);
         sh_h8 pf[4];
         const bool tail = ragged && kb == nkb - 1;
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                float p = sh_fast_exp2(fmaf(sacc[tt][r], a.c, -m));
+                float p = FOLD ? sh_fast_exp2(sacc[tt][r]) : sh_fast_exp2(fmaf(sacc[tt][r], a.c, -m));
                 if (MASK) {
                     if (uni) p = key_of(kb, tt, r) < S ? 1.f : 0.f;
                     else if (!key_ok(kb, tt, r)) p = 0.f;
@@ -705,17 +729,18 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
                      sh_aligned16(q) && sh_aligned16(k) && sh_aligned16(v) && sh_aligned16(o);
     static const int impl = [] { const char *e = getenv("SH_ATTN_IMPL"); return (e && *e) ? atoi(e) : 0; }();
     const dim3 grid(sh_cdiv(S, QPB), H, B);
+    const bool fold = fabsf(a.c) <= 1.f;            // c q stays in fp16 range
     if (tok && (dh == 64 || dh == 128) && vec) {
-        if (dh == 64) go(k_flash2<64, 2, true>, grid, 0);
-        else go(k_flash2<128, 2, true>, grid, 0);
+        if (dh == 64) fold ? go(k_flash2<64, 2, true, true>, grid, 0) : go(k_flash2<64, 2, true, false>, grid, 0);
+        else fold ? go(k_flash2<128, 2, true, true>, grid, 0) : go(k_flash2<128, 2, true, false>, grid, 0);
     } else if (tok) {
         if (S > 16384) { sh_set_error(-1, "[sh_attention] masked heads with dh=%u support S <= 16384", dh); return -1; }
         static bool attr_m = false;
         if (!attr_m) { (void)hipFuncSetAttribute((const void *)k_attn_rows, hipFuncAttributeMaxDynamicSharedMemorySize, 16384 * 4); attr_m = true; }
         go(k_attn_rows, dim3(S, H, B), S * sizeof(float));
     } else if ((dh == 64 || dh == 128) && vec && impl == 0) {
-        if (dh == 64) go(k_flash2<64, 2, false>, grid, 0);
-        else go(k_flash2<128, 2, false>, grid, 0);
+        if (dh == 64) fold ? go(k_flash2<64, 2, false, true>, grid, 0) : go(k_flash2<64, 2, false, false>, grid, 0);
+        else fold ? go(k_flash2<128, 2, false, true>, grid, 0) : go(k_flash2<128, 2, false, false>, grid, 0);
     } else if ((dh == 64 || dh == 128) && vec && impl == 1) {
         if (dh == 64) go(k_flash_dma<64, 4>, grid, 0);
         else go(k_flash_dma<128, 2>, grid, 0);
