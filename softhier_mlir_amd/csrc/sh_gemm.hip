@@ -1086,18 +1086,35 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs a, ShDiv div, ui
     const uint64_t plane = (uint64_t)a.M * a.N;
     constexpr int W = VEC ? 8 : 1;
     const uint32_t gn = VEC ? 8 * cc : cc;
+    // v = 0, then v += partial_0, partial_1, ... in split order. The loads of SB splits are issued before the
+    // adds that use them (one memory latency per SB splits, not per split); a split past a.splits reads
+    // element 0 and adds +0, which leaves every sum as it was (after its first add v is never -0).
+    constexpr int SB = 4;
     float v[W];
 #pragma unroll
     for (int e = 0; e < W; ++e) v[e] = 0.f;
-    for (uint32_t s = 0; s < a.splits; ++s) {
-        const float *p = a.part + s * plane + (uint64_t)gm * a.N + gn;
-        if (VEC) {
-            const float4 u0 = *(const float4 *)p, u1 = *(const float4 *)(p + 4);
-            v[0] += u0.x; v[1] += u0.y; v[2] += u0.z; v[3] += u0.w;
-            v[4 % W] += u1.x; v[5 % W] += u1.y; v[6 % W] += u1.z; v[7 % W] += u1.w;
-        } else {
-            v[0] += p[0];
+    const float *base = a.part + (uint64_t)gm * a.N + gn;
+    for (uint32_t s = 0; s < a.splits; s += SB) {
+        float u[SB][W];
+#pragma unroll
+        for (int q = 0; q < SB; ++q) {
+            const bool in = s + q < a.splits;
+            const float *p = in ? base + (uint64_t)(s + q) * plane : a.part;
+            if (VEC) {
+                const float4 u0 = *(const float4 *)p, u1 = *(const float4 *)(p + 4);
+                u[q][0] = u0.x; u[q][1 % W] = u0.y; u[q][2 % W] = u0.z; u[q][3 % W] = u0.w;
+                u[q][4 % W] = u1.x; u[q][5 % W] = u1.y; u[q][6 % W] = u1.z; u[q][7 % W] = u1.w;
+            } else {
+                u[q][0] = p[0];
+            }
+            const uint32_t mk = in ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+            for (int e = 0; e < W; ++e) u[q][e] = __uint_as_float(__float_as_uint(u[q][e]) & mk);
         }
+#pragma unroll
+        for (int q = 0; q < SB; ++q)
+#pragma unroll
+            for (int e = 0; e < W; ++e) v[e] += u[q][e];
     }
     uint16_t out[W];
 #pragma unroll
