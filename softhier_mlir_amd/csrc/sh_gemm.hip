@@ -1079,8 +1079,10 @@ __global__ __launch_bounds__(NT, MINW) void k_gemm4(GemmArgs a) {
 }
 
 template <bool VEC>
-__global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs a, ShDiv div, uint32_t per_row, uint32_t items) {
-    const uint32_t it = blockIdx.x * 256u + threadIdx.x;
+// One item per thread in 64-thread workgroups: a split-K output is usually small (M of a few hundred), and
+// single-wave workgroups spread its items over every CU.
+__global__ __launch_bounds__(64) void k_splitk_reduce(GemmArgs a, ShDiv div, uint32_t per_row, uint32_t items) {
+    const uint32_t it = blockIdx.x * 64u + threadIdx.x;
     if (it >= items) return;
     const uint32_t gm = sh_div(it, div), cc = it - gm * per_row;
     const uint64_t plane = (uint64_t)a.M * a.N;
@@ -1396,8 +1398,8 @@ int launch(const GemmReq &r, const char *name) {
         const uint64_t items = (uint64_t)r.M * per_row;
         if (items > 0xFFFFFF00ull) { sh_set_error(-1, "[%s] problem too large", name); return -1; }
         const ShDiv div = sh_make_div(per_row);
-        if (rvec) hipLaunchKernelGGL(k_splitk_reduce<true>, dim3(sh_cdiv((uint32_t)items, 256)), dim3(256), 0, st, a, div, per_row, (uint32_t)items);
-        else hipLaunchKernelGGL(k_splitk_reduce<false>, dim3(sh_cdiv((uint32_t)items, 256)), dim3(256), 0, st, a, div, per_row, (uint32_t)items);
+        if (rvec) hipLaunchKernelGGL(k_splitk_reduce<true>, dim3(sh_cdiv((uint32_t)items, 64)), dim3(64), 0, st, a, div, per_row, (uint32_t)items);
+        else hipLaunchKernelGGL(k_splitk_reduce<false>, dim3(sh_cdiv((uint32_t)items, 64)), dim3(64), 0, st, a, div, per_row, (uint32_t)items);
         if (!sh_launch_ok(name)) return SH_EHIP;
     }
     return 0;
