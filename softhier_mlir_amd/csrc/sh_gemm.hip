@@ -1180,6 +1180,10 @@ KCfg g_cfgs[] = {
     SH_KCFG4R(128, 192, 3, 2, 0.34f),
     SH_KCFG4R(128, 192, 4, 1, 0.34f),
     SH_KCFG4S(128, 192, 2, 2, 0.36f),
+    SH_KCFG2(64, 64, 2, 0.12f),             // small tiles: many workgroups for small problems (latency-bound)
+    SH_KCFG2(64, 64, 3, 0.13f),
+    SH_KCFG2(64, 128, 2, 0.16f),
+    SH_KCFG2(128, 64, 2, 0.16f),
 };
 #undef SH_KCFG
 #undef SH_KCFG2

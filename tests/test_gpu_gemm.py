@@ -17,6 +17,7 @@ from oracle import lcg, refs
 from softhier_mlir_amd import data, shops
 
 pytestmark = pytest.mark.gpu
+NUM_TILE_CFGS = 33      # entries of the GEMM tile table (g_cfgs in sh_gemm.hip)
 A = shops.addr
 
 
@@ -72,7 +73,7 @@ def test_real_data_fills(lib, gpu):
 
 
 @pytest.mark.parametrize("K", [136, 192])
-@pytest.mark.parametrize("cfg_index", range(29))
+@pytest.mark.parametrize("cfg_index", range(NUM_TILE_CFGS))
 def test_every_tile_config(lib, gpu, cfg_index, K, monkeypatch):
     """Each compiled tile shape on a problem with partial tiles in M and N; K = 136 has a K tail (only the
     general kernels take it), K = 192 is a multiple of 64 (the direct-to-LDS kernels take it)."""
@@ -99,15 +100,15 @@ def test_unsplit_tile_configs_store_identical_bits(lib, gpu, monkeypatch):
     x, w = data.normal((M, K), 21), data.normal((K, N), 22, std=1 / np.sqrt(K))
     X, W = to_dev(x), to_dev(w)
     outs = []
-    for cfg_index in range(29):
+    for cfg_index in range(NUM_TILE_CFGS):
         monkeypatch.setenv("SH_GEMM_CFG", str(cfg_index))
         Z = torch.zeros((M, N), dtype=torch.float16, device="cuda")
         assert lib.sh_gemm_ex(A(X), A(W), A(Z), M, N, K, K, N, N, None, None) == 0, shops.last_error()
         outs.append(to_np(Z).view(np.uint16))
-    # the direct-to-LDS kernels the one-time timing chooses between (configurations 6-28: 64-k and 32-k slices,
-    # 4 and 8 wavefronts, LDS-staged or register epilogue) agree bit for bit; so do the register-staged fallbacks
-    # (0-5) among themselves
-    for lo, hi in ((6, 29), (0, 6)):
+    # the direct-to-LDS kernels the cost model and the one-time timing choose between (configurations 6-32:
+    # 64-row to 256-row tiles, 64-k and 32-k slices, 4 and 8 wavefronts, LDS-staged or register epilogue) agree
+    # bit for bit; so do the register-staged fallbacks (0-5) among themselves
+    for lo, hi in ((6, NUM_TILE_CFGS), (0, 6)):
         for i in range(lo, hi):
             assert (outs[i] == outs[lo]).all(), f"config {i} differs from config {lo}"
     for i in (0, 6):
@@ -190,7 +191,8 @@ EPI_CASES = [(shops.SH_BIAS_FP16, shops.SH_ACT_GELU, True, 0), (shops.SH_BIAS_FP
 def test_epilogue_chain_same_bits_on_every_tile(lib, gpu, monkeypatch, case, splits):
     """Each epilogue combination on partial tiles (M, N not multiples of any tile), on the LDS-staged and the
     register-epilogue tile configurations (6: k_gemm2; 23, 24: k_gemm4 staged; 25-28: k_gemm4 register epilogue,
-    32- and 64-k slices): every configuration stores the same bits (split or not), nothing outside the output view
+    32- and 64-k slices; 30-32: k_gemm2 64x64, 64x128, 128x64): every configuration stores the same bits (split or
+    not), nothing outside the output view
     changes, and the result is within tolerance of the oracle's unfused sequence."""
     import torch
     bias_fmt, act, res, accumulate = EPI_CASES[case]
@@ -205,7 +207,7 @@ def test_epilogue_chain_same_bits_on_every_tile(lib, gpu, monkeypatch, case, spl
     elif bias_fmt == shops.SH_BIAS_FP16:
         bias = to_dev(b32.astype(np.float16))
     outs = {}
-    for cfg_index in (6, 23, 24, 25, 26, 27, 28):
+    for cfg_index in (6, 23, 24, 25, 26, 27, 28, 30, 31, 32):
         monkeypatch.setenv("SH_GEMM_CFG", str(cfg_index))
         Z = torch.full((M + 3, ldz), 7.0, dtype=torch.float16, device="cuda")
         Z[:M, :N] = to_dev(z0)
