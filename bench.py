@@ -292,6 +292,18 @@ def config_table(lib, torch) -> list:
     record("2 summa 1024^3 (mesh mode)", [1024, 1024, 1024], us, 2 * 1024 ** 3, 3 * 1024 * 1024 * 2, host(Z),
            refs.r16(refs.gemm(xs, ws)), cpu, note="timed on X=1, W=1/1024 (examples/gemm1024_summa.mlir:5), parity on LCG data")
 
+    # the reference's small-M GEMM (sh_gemm_xmcast, sh_gemm.inc.c:192-344) on the SmolVLA expert / prefix shapes
+    # its schedule notes list; uniform data, weights scaled by 1/sqrt(K)
+    for M, N, K in [(50, 1600, 720), (50, 720, 2048), (200, 720, 960), (241, 960, 960), (200, 4096, 720)]:
+        x = data.uniform(M, K, 8)
+        w = (data.uniform(K, N, 9).astype(np.float32) / np.sqrt(K)).astype(np.float16)
+        X, W = dev(x), dev(w)
+        Z = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        us = gpu_us(lambda: lib.sh_gemm_xmcast(A(X), A(W), A(Z), M, N, K, K, N, N, None))
+        cpu = cpu_ms(lambda: refs.r16(refs.gemm(x, w)))
+        record(f"xmcast {M}x{K}->{N}", [M, K, N], us, 2 * M * N * K, 2 * (M * K + K * N + M * N), host(Z),
+               refs.r16(refs.gemm(x, w)), cpu)
+
     # config 3: row ops at the configured shapes, values N(0, 1) unless stated
     M, D, F = 256, 768, 3072
     x = data.normal((M, D), 11)

@@ -408,7 +408,7 @@ __device__ __forceinline__ uint32_t fw(uint32_t k) {
     return ((BN / 8) % 16 == 0) ? 4u * (k & 3u) : 4u * ((k >> 1) & 1u);
 }
 
-template <int BM, int BN, int STAGES, bool SPLIT>
+template <int BM, int BN, int STAGES, bool SPLIT, bool KTAIL = false>
 __global__ __launch_bounds__(256) void k_gemm2(GemmArgs a) {
     using C = Cfg2<BM, BN, STAGES>;
     extern __shared__ uint4 smem[];
@@ -421,16 +421,23 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs a) {
     const uint32_t m0 = tm * BM, n0 = tn * BN;
     const uint32_t kbeg = split * a.kps;
     const uint32_t kend = min(a.K, kbeg + a.kps);
-    const int KT = kend > kbeg ? (int)((kend - kbeg) / BK) : 0;
+    const int KT = kend > kbeg ? (int)((kend - kbeg + (KTAIL ? BK - 1 : 0)) / BK) : 0;
+    // KTAIL (K % 64 != 0): the last slice holds `rem` < 64 valid k (a multiple of 8); its X chunks and W rows
+    // past kend are read from the zero block, so both operands are 0 there and add nothing
+    const uint32_t rem = KT > 0 ? (kend - kbeg) - (uint32_t)(KT - 1) * BK : BK;
+    const uint16_t *zero = (const uint16_t *)g_epi_zero;
 
-    // per-lane source pointers of every DMA round (the k0 advance is added per slice)
+    // per-lane source pointers of every DMA round (the k0 advance is added per slice), and whether the round's
+    // chunk lies past kend in the last slice
     const uint16_t *xs[C::XR];
     const uint16_t *ws[C::WR];
+    bool xpast[C::XR], wpast[C::WR];
 #pragma unroll
     for (int r = 0; r < C::XR; ++r) {
         const uint32_t p = r * 256 + wave * 64 + lane, m = p >> 3, c = (p & 7) ^ swz(m);
         const uint32_t gm = min(m0 + m, a.M - 1);
         xs[r] = a.x + (uint64_t)gm * a.ldx + kbeg + 8 * c;
+        xpast[r] = 8 * c >= rem;
     }
 #pragma unroll
     for (int r = 0; r < C::WR; ++r) {
@@ -438,6 +445,7 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs a) {
         uint32_t gn = n0 + 8 * c;
         if (gn >= a.N) gn = a.N - 8;
         ws[r] = a.w + (uint64_t)(kbeg + k) * a.ldw + gn;
+        wpast[r] = k >= rem;
     }
     const uint32_t lds0 = lds_addr(smem);
     const uint32_t wave_off = (uint32_t)__builtin_amdgcn_readfirstlane(wave * 64 * 16);
@@ -445,8 +453,10 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs a) {
     // DMA instruction d of the loads of k-slice `src` into LDS stage `stage`: X rounds first, then W rounds
     auto issue_one = [&](int d, int src, int stage) {
         const uint32_t st = lds0 + (uint32_t)stage * (uint32_t)C::STAGE;
-        if (d < C::XR) lds_dma16(xs[d] + (uint64_t)src * BK, st + d * 4096 + wave_off);
-        else lds_dma16(ws[d - C::XR] + (uint64_t)src * BK * a.ldw, st + C::XCH * 16 + (d - C::XR) * 4096 + wave_off);
+        const bool last = KTAIL && src == KT - 1;
+        if (d < C::XR) lds_dma16(last && xpast[d] ? zero : xs[d] + (uint64_t)src * BK, st + d * 4096 + wave_off);
+        else lds_dma16(last && wpast[d - C::XR] ? zero : ws[d - C::XR] + (uint64_t)src * BK * a.ldw,
+                       st + C::XCH * 16 + (d - C::XR) * 4096 + wave_off);
     };
 
     sh_f16v acc[C::FM][C::FN];
@@ -1134,12 +1144,17 @@ __global__ __launch_bounds__(64) void k_splitk_reduce(GemmArgs a, ShDiv div, uin
 // ---- host side ------------------------------------------------------------------------------------------
 typedef void (*KernelFn)(GemmArgs);
 // v2 entries need vec operands and K % 64 == 0; v1 entries take anything (scalar variants for small tiles).
-struct KCfg { int bm, bn, stages; bool v2; KernelFn vec[2], scalar[2]; size_t lds; float eff; bool attr_set; int threads = 256; };
+// ktail: the kernel also takes K % 64 != 0 (vector operands; the last, partial k-slice reads zeros past K).
+struct KCfg {
+    int bm, bn, stages; bool v2; KernelFn vec[2], scalar[2]; size_t lds; float eff; bool attr_set; int threads = 256;
+    bool ktail = false; KernelFn tail[2] = {nullptr, nullptr};     // the K % 64 != 0 variants (unsplit, split)
+};
 
 #define SH_KCFG(BM, BN, EFF) { BM, BN, 2, false, { k_gemm<BM, BN, true, false>, k_gemm<BM, BN, true, true> }, \
                                { k_gemm<BM, BN, false, false>, k_gemm<BM, BN, false, true> }, Cfg<BM, BN>::LDS, EFF, false }
 #define SH_KCFG2(BM, BN, ST, EFF) { BM, BN, ST, true, { k_gemm2<BM, BN, ST, false>, k_gemm2<BM, BN, ST, true> }, \
-                                    { nullptr, nullptr }, Cfg2<BM, BN, ST>::LDS, EFF, false, 256 }
+                                    { nullptr, nullptr }, Cfg2<BM, BN, ST>::LDS, EFF, false, 256, true, \
+                                    { k_gemm2<BM, BN, ST, false, true>, k_gemm2<BM, BN, ST, true, true> } }
 #define SH_KCFG4(BM, BN, ST, NT, W, EFF) { BM, BN, ST, true, { k_gemm4<BN, ST, false, NT, BM, W>, k_gemm4<BN, ST, true, NT, BM, W> }, \
                                            { nullptr, nullptr }, Cfg4<BN, ST, NT, BM>::LDS, EFF, false, NT }
 #define SH_KCFG4R(BM, BN, ST, W, EFF) { BM, BN, ST, true, { k_gemm4<BN, ST, false, 256, BM, W, true>, k_gemm4<BN, ST, true, 256, BM, W, true> }, \
@@ -1224,12 +1239,14 @@ double est_time(int i, uint32_t M, uint32_t N, uint32_t K, uint32_t splits, int 
 
 struct Plan { int cfg; uint32_t splits; };
 
-bool eligible(const KCfg &c, bool vec, bool fast) {
-    if (c.v2) return fast;
+// fast: vector operands and K % 64 == 0; ktail: vector operands with a partial last k-slice
+bool eligible(const KCfg &c, bool vec, bool fast, bool ktail) {
+    if (c.v2) return fast || (ktail && c.ktail);
     return vec || c.bm * c.bn <= 128 * 128;
 }
 
 Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t want_splits) {
+    const bool ktail = vec && K > 0 && K % BK != 0;
     const int cus = sh_num_cus() > 0 ? sh_num_cus() : 256;
     // Every eligible (config, splits) is estimated; among those within 3 % of the fastest estimate the one with
     // the lowest throughput term wins (tiles of one size share one latency floor; the throughput term ranks
@@ -1239,7 +1256,7 @@ Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t wa
     int n = 0;
     double tmin = 1e300;
     for (int i = 0; i < kNumCfg; ++i) {
-        if (!eligible(g_cfgs[i], vec, fast)) continue;
+        if (!eligible(g_cfgs[i], vec, fast, ktail)) continue;
         uint32_t lo = 1, hi = 1;
         if (want_splits) lo = hi = want_splits;
         else hi = std::max<uint32_t>(1, std::min<uint32_t>(16, K / 128));
@@ -1257,7 +1274,7 @@ Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t wa
     const int fc = env_int("SH_GEMM_CFG", -1);
     const int fs = env_int("SH_GEMM_SPLITS", 0);
     if (fs > 0 && !want_splits) best.splits = (uint32_t)fs;
-    if (fc >= 0 && fc < kNumCfg && eligible(g_cfgs[fc], vec, fast)) best.cfg = fc;
+    if (fc >= 0 && fc < kNumCfg && eligible(g_cfgs[fc], vec, fast, ktail)) best.cfg = fc;
     return best;
 }
 
@@ -1266,6 +1283,7 @@ void set_attrs(KCfg &c) {
     for (int v = 0; v < 2; ++v) {
         if (c.vec[v]) (void)hipFuncSetAttribute((const void *)c.vec[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
         if (c.scalar[v]) (void)hipFuncSetAttribute((const void *)c.scalar[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
+        if (c.tail[v]) (void)hipFuncSetAttribute((const void *)c.tail[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
     }
     c.attr_set = true;
 }
@@ -1387,7 +1405,7 @@ int launch(const GemmReq &r, const char *name) {
 
     hipStream_t st = sh_stream();
     const bool split = splits > 1;
-    KernelFn fn = (vec || c.v2) ? c.vec[split] : c.scalar[split];
+    KernelFn fn = (c.v2 && !fast) ? c.tail[split] : (vec || c.v2) ? c.vec[split] : c.scalar[split];   // !fast: K % 64 != 0
     set_attrs(c);
     if (split) {
         const size_t ws = (size_t)splits * r.M * r.N * sizeof(float);

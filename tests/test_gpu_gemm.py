@@ -370,3 +370,32 @@ def test_xmcast_small_m_shapes(lib, gpu, M, N, K, mode, tm, acc):
         else:
             bad, err, _ = refs.close(got, want)
             assert bad == 0, err
+
+
+@pytest.mark.parametrize("K", [8, 40, 136, 720])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_k_tail_on_direct_to_lds_tiles(lib, gpu, monkeypatch, K, splits):
+    """K % 64 != 0 with vector operands (K % 8 == 0) on the direct-to-LDS k_gemm2 tiles: the last, partial 64-k
+    slice reads zeros past K, so every k_gemm2 tile (128x128 to 128x256, 64x64 to 128x64; 2 or 3 stages) stores
+    the same bits, within tolerance of the oracle, with a bias + GELU epilogue, and nothing outside the view
+    changes. K = 8 is a single partial slice; K = 720 is the SmolVLA width (11 slices + 16)."""
+    import torch
+    M, N, ldz = 200, 328, 336
+    x, w = data.normal((M, K), 91), data.normal((K, N), 92, std=1 / np.sqrt(K))
+    b = data.normal((1, N), 93, std=0.3).astype(np.float16)
+    X, W, Bb = to_dev(x), to_dev(w), to_dev(b)
+    outs = {}
+    for cfg_index in (6, 7, 8, 9, 10, 11, 12, 29, 30, 31, 32):
+        monkeypatch.setenv("SH_GEMM_CFG", str(cfg_index))
+        Z = torch.full((M + 2, ldz), 7.0, dtype=torch.float16, device="cuda")
+        e = shops.epi(bias=A(Bb), act=shops.SH_ACT_GELU, splits=splits)
+        assert lib.sh_gemm_ex(A(X), A(W), A(Z), M, N, K, K, N, ldz, None, e) == 0, shops.last_error()
+        z = to_np(Z)
+        assert (z[:M, N:] == 7.0).all() and (z[M:] == 7.0).all(), cfg_index
+        outs[cfg_index] = z[:M, :N].copy()
+    ref = outs[6]
+    for i, z in outs.items():
+        assert np.array_equal(z.view(np.uint16), ref.view(np.uint16)), f"config {i} differs from config 6"
+    want = refs.gelu(refs.r16(refs.r16(refs.gemm(x, w)) + b.astype(np.float32)))
+    bad, err, _ = refs.close(ref, want)
+    assert bad == 0, err
