@@ -412,8 +412,8 @@ def cpu_baseline(B: int, S: int, D: int, F: int, H: int, p: dict, x) -> dict:
 def main() -> int:
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build (the path shards by "
-              f"sequence across GPUs; see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build (the encoder path would "
+              f"shard by sequence, one GPU per group of sequences, with no exchange)", file=sys.stderr)
         return 2
     import numpy as np
     import torch
