@@ -203,6 +203,12 @@ typedef struct {
 int sh_gemm_ex(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
                uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg, const sh_gemm_epi *epi);
 
+/* Additive (no counterpart in the reference): the GEMM cost model's plan for an (M, N, K) problem with
+ * 16-byte-aligned operands and a split request (0 = library choice): out[0] tile configuration, out[1] /
+ * out[2] its tile rows / columns, out[3] the split count. A large problem's first call may still replace the
+ * configuration by its one-time timing. Runs no GPU work. 0, or -1 for an empty problem / NULL out. */
+int sh_gemm_plan(uint32_t M, uint32_t N, uint32_t K, uint32_t splits, uint32_t *out);
+
 /* Batched multi-head attention (the reference has no batch dimension): sequence b uses q + b*bsq*2 bytes,
  * likewise k/v/o with their own batch strides in elements (e.g. S*ld for rows stacked as [B*S, ld]).
  * Constraints as sh_attention_q except the TCDM budget; sq == 0 -> the library's choice. */

@@ -1481,6 +1481,20 @@ int sh_gemm_splitk(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, u
     return launch(r, "sh_gemm_splitk");
 }
 
+// The cost model's plan for 16-byte-aligned operands (what a call would launch before the one-time timing of a
+// large problem): out = {tile configuration, tile rows, tile columns, split count}. No GPU work; 256 CUs are
+// assumed when no GPU is visible. SH_GEMM_CFG / SH_GEMM_SPLITS apply as for a call.
+int sh_gemm_plan(uint32_t M, uint32_t N, uint32_t K, uint32_t splits, uint32_t *out) {
+    if (!M || !N || !K || !out) { sh_set_error(-1, "[sh_gemm_plan] empty problem or NULL output"); return -1; }
+    const bool vec = N % 8 == 0 && K % 8 == 0;
+    const Plan p = choose(M, N, K, vec, vec && K % BK == 0, splits);
+    out[0] = (uint32_t)p.cfg;
+    out[1] = (uint32_t)g_cfgs[p.cfg].bm;
+    out[2] = (uint32_t)g_cfgs[p.cfg].bn;
+    out[3] = p.splits;
+    return 0;
+}
+
 int sh_gemm_ex(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
                uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg, const sh_gemm_epi *epi) {
     sh_gemm_cfg c;

@@ -146,3 +146,24 @@ def test_capture_collects_library_text(lib):
     with shops.capture() as cap:
         lib.sh_printf(b"hello %d\n", C.c_int(7))
     assert cap.text == "hello 7\n"
+
+
+def test_gemm_tile_plan_without_gpu(lib):
+    """The GEMM cost model (sh_gemm_plan, no GPU work): small problems take the small direct-to-LDS tiles
+    (latency-bound: many short workgroups), the encoder's M = 8192 shapes the 128 x 192 tiles whose choice the
+    one-time timing refines, explicit split requests are kept, and K % 64 != 0 stays on a direct-to-LDS tile."""
+    import ctypes as C
+
+    def plan(M, N, K, splits=0):
+        out = (C.c_uint32 * 4)()
+        assert lib.sh_gemm_plan(M, N, K, splits, out) == 0
+        return tuple(out)
+    for M, N, K in [(256, 2304, 768), (256, 3072, 768), (256, 256, 256), (1024, 1024, 1024), (200, 4096, 720)]:
+        cfg, bm, bn, splits = plan(M, N, K)
+        assert (bm, bn, splits) == (64, 64, 1), (M, N, K, cfg, bm, bn, splits)
+    assert plan(256, 768, 3072, 4)[1:] == (64, 64, 4)
+    for M, N, K in [(8192, 2304, 768), (8192, 768, 768), (8192, 768, 3072)]:
+        assert plan(M, N, K)[1:] == (128, 192, 1), (M, N, K)
+    assert plan(8192, 3072, 768)[3] == 1
+    out = (C.c_uint32 * 4)()
+    assert lib.sh_gemm_plan(0, 8, 8, 0, out) == -1
