@@ -80,8 +80,9 @@ int sh_gemm(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t
 
 /* sh_ops.h:72-73 (sh_gemm.inc.c:127-189): SUMMA mode over a virtual SH_MESH_P x SH_MESH_P mesh of output
  * tiles (the reference's 4 x 4 cluster mesh). Same constraints and codes: tm == tn, M == N == P * tm,
- * K % tk == 0 (-1), TCDM budget (-2). Mesh row py owns X row-panel py; its workgroups run on one XCD so the
- * panel is fetched from HBM once into that XCD's L2 and re-read from there by the whole row. */
+ * K % tk == 0 (-1), TCDM budget (-2). The launch is the tiled GEMM with its XCD-aware tile order (each XCD
+ * walks a contiguous band of output tile rows, so an X row panel is fetched into one XCD's L2 and re-read there
+ * by the whole band); there is no separate mesh schedule and no broadcast step on one GPU. */
 #define SH_MESH_P 4u
 int sh_gemm_mesh(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
                  uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg);
@@ -100,7 +101,9 @@ int sh_gemm_xmcast_ex(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N
 uint32_t sh_gemm_xmcast_l1_bytes(uint32_t M, uint32_t N, uint32_t K, const sh_gemm_cfg *cfg, uint32_t mode);  /* sh_ops.h:84, ~0u: no plan */
 
 /* ---- row-wise / elementwise ops (sh_ops.h:90-100, runtime/sh_rowops.inc.c:383-465) -------------------
- * fp16 in/out, fp32 arithmetic, one pass over HBM. Parameter rows (gamma, beta, bias) are fp16 rows. */
+ * fp16 in/out, one pass over HBM. Parameter rows (gamma, beta, bias) are fp16 rows. LayerNorm, softmax and
+ * scale compute in fp32; add / add_bias use packed fp16 adds (which round exactly as the fp32 sum rounded to
+ * fp16); GELU is the tanh form evaluated on packed fp16 (a few fp16 ulps from the fp32 form). */
 void sh_layernorm(uint64_t y, uint64_t x, uint64_t gamma, uint64_t beta, uint32_t rows, uint32_t cols, uint32_t ld, float eps, uint32_t cluster);  /* sh_ops.h:94 */
 void sh_softmax_rows(uint64_t y, uint64_t x, uint32_t rows, uint32_t cols, uint32_t ld, float scale, uint32_t cluster);  /* sh_ops.h:95 */
 void sh_gelu(uint64_t y, uint64_t x, uint32_t rows, uint32_t cols, uint32_t ld, uint32_t cluster);                     /* sh_ops.h:96 tanh form */

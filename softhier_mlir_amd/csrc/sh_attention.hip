@@ -246,24 +246,6 @@ __global__ __launch_bounds__(256) void k_flash(AttnArgs a) {
 // lane) with two ds_read_b64_tr_b16: lane group g of a 16-key substep supplies keys 4g..4g+3 and 8+4g..8+4g+3,
 // the order in which the score accumulators hold P. Keys past S are fetched from row S-1 (valid memory) and
 // get zero weight.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void attn_dma16(const void *src, uint32_t lds_wave_base) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_wave_base), "v"(src) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-template <int N>
-__device__ __forceinline__ void attn_wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt");
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-__device__ __forceinline__ uint32_t attn_lds_addr(const void *p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
-typedef short attn_s4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ attn_s4 attn_read_tr(uint32_t addr) {
-    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) attn_s4 *)(uintptr_t)addr);
-}
 // V rows are DC chunks wide; chunk c of row k sits at c ^ vfw(k) so a transpose read's 4 rows x 64 bytes
 // land on distinct banks (row pitch 128 B: alternate rows share a bank half; 256 B: every row starts at bank 0)
 template <int DH>
@@ -302,7 +284,7 @@ __global__ __launch_bounds__(256) void k_flash_dma(AttnArgs a) {
         kcol[r] = Kp + 8 * (pc ^ kswz<DH>(key));
         vcol[r] = Vp + 8 * (pc ^ vfw<DH>(key));
     }
-    const uint32_t lds0 = attn_lds_addr(smem);
+    const uint32_t lds0 = sh_lds_addr(smem);
     const uint32_t wave_off = (uint32_t)__builtin_amdgcn_readfirstlane(wave * 64 * 16);
     auto issue = [&](uint32_t kb, int stage) {
         const uint32_t st = lds0 + (uint32_t)stage * STAGE;
@@ -310,8 +292,8 @@ __global__ __launch_bounds__(256) void k_flash_dma(AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < KR; ++r) {
             const uint64_t row = min(k0 + kkey[r], S - 1);                      // rows past S read row S-1
-            attn_dma16(kcol[r] + row * a.ldk, st + r * 4096 + wave_off);
-            attn_dma16(vcol[r] + row * a.ldv, st + KCH * 16 + r * 4096 + wave_off);
+            sh_lds_dma16(kcol[r] + row * a.ldk, st + r * 4096 + wave_off);
+            sh_lds_dma16(vcol[r] + row * a.ldv, st + KCH * 16 + r * 4096 + wave_off);
         }
     };
 
@@ -327,7 +309,7 @@ __global__ __launch_bounds__(256) void k_flash_dma(AttnArgs a) {
     for (int s = 0; s < NST - 1; ++s) issue(min((uint32_t)s, nkb - 1), s);
 
     for (uint32_t kb = 0; kb < nkb; ++kb) {
-        attn_wait_vmcnt<(NST - 2) * LOADS>();
+        sh_wait_vmcnt<(NST - 2) * LOADS>();
         __syncthreads();
         issue(min(kb + NST - 1, nkb - 1), (int)((kb + NST - 1) % NST));
         const int st = (int)(kb % NST);
@@ -392,14 +374,14 @@ __global__ __launch_bounds__(256) void k_flash_dma(AttnArgs a) {
 #pragma unroll
             for (int sp = 0; sp < 4; ++sp) {
                 const uint32_t k0 = 16 * sp + 4 * g + (iq >> 2), k1 = k0 + 8;
-                const attn_s4 lo = attn_read_tr(vbase + k0 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k0)) + 2 * (d & 7));
-                const attn_s4 hi = attn_read_tr(vbase + k1 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k1)) + 2 * (d & 7));
+                const sh_s4 lo = sh_ds_read_tr(vbase + k0 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k0)) + 2 * (d & 7));
+                const sh_s4 hi = sh_ds_read_tr(vbase + k1 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k1)) + 2 * (d & 7));
                 const sh_h8 vf = __builtin_bit_cast(sh_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[sp], oacc[dt], 0, 0, 0);
             }
         }
     }
-    attn_wait_vmcnt<0>();      // clamped tail loads land before the LDS is reused below
+    sh_wait_vmcnt<0>();      // clamped tail loads land before the LDS is reused below
     __syncthreads();
 
     const float l = l_run + __shfl_xor(l_run, 32, 64);
@@ -474,7 +456,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a) {
         kcol[r] = Kp + 8 * (pc ^ kswz<DH>(key));
         vcol[r] = Vp + 8 * (pc ^ vfw<DH>(key));
     }
-    const uint32_t lds0 = attn_lds_addr(smem);
+    const uint32_t lds0 = sh_lds_addr(smem);
     const uint32_t wave_off = (uint32_t)__builtin_amdgcn_readfirstlane(wave * 64 * 16);
     auto issue = [&](uint32_t kb, int stage, bool with_v) {
         const uint32_t st = lds0 + (uint32_t)stage * STAGE;
@@ -482,8 +464,8 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < KR; ++r) {
             const uint64_t row = min(k0 + kkey[r], S - 1);                      // rows past S read row S-1
-            attn_dma16(kcol[r] + row * a.ldk, st + r * 4096 + wave_off);
-            if (with_v) attn_dma16(vcol[r] + row * a.ldv, st + KCH * 16 + r * 4096 + wave_off);
+            sh_lds_dma16(kcol[r] + row * a.ldk, st + r * 4096 + wave_off);
+            if (with_v) sh_lds_dma16(vcol[r] + row * a.ldv, st + KCH * 16 + r * 4096 + wave_off);
         }
     };
 
@@ -530,7 +512,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a) {
     for (int s = 0; s < NST - 1; ++s) issue(min((uint32_t)s, nkb - 1), s, false);
     float ext = pos ? -INFINITY : INFINITY;
     for (uint32_t kb = 0; kb < nkb; ++kb) {
-        attn_wait_vmcnt<(NST - 2) * KR>();
+        sh_wait_vmcnt<(NST - 2) * KR>();
         __syncthreads();
         issue(min(kb + NST - 1, nkb - 1), (int)((kb + NST - 1) % NST), false);
         sh_f16v sacc[2];
@@ -562,7 +544,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a) {
         qbias[0] = -mh;
         qbias[1] = -(_Float16)(m - (float)mh);
     }
-    attn_wait_vmcnt<0>();                            // the ring is idle before pass 2 refills it
+    sh_wait_vmcnt<0>();                            // the ring is idle before pass 2 refills it
     __syncthreads();
 
     // ---- pass 2: p = 2^(c s - m); O^T += V^T P^T; l += 1^T P^T ----
@@ -576,7 +558,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a) {
 #pragma unroll
     for (int s = 0; s < NST - 1; ++s) issue(min((uint32_t)s, nkb - 1), s, true);
     for (uint32_t kb = 0; kb < nkb; ++kb) {
-        attn_wait_vmcnt<(NST - 2) * 2 * KR>();
+        sh_wait_vmcnt<(NST - 2) * 2 * KR>();
         __syncthreads();
         issue(min(kb + NST - 1, nkb - 1), (int)((kb + NST - 1) % NST), true);
         const int st = (int)(kb % NST);
@@ -606,14 +588,14 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a) {
 #pragma unroll
             for (int sp = 0; sp < 4; ++sp) {
                 const uint32_t k0 = 16 * sp + 4 * g + (iq >> 2), k1 = k0 + 8;
-                const attn_s4 lo = attn_read_tr(vbase + k0 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k0)) + 2 * (d & 7));
-                const attn_s4 hi = attn_read_tr(vbase + k1 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k1)) + 2 * (d & 7));
+                const sh_s4 lo = sh_ds_read_tr(vbase + k0 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k0)) + 2 * (d & 7));
+                const sh_s4 hi = sh_ds_read_tr(vbase + k1 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k1)) + 2 * (d & 7));
                 const sh_h8 vf = __builtin_bit_cast(sh_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[sp], oacc[dt], 0, 0, 0);
             }
         }
     }
-    attn_wait_vmcnt<0>();      // clamped tail loads land before the LDS is reused below
+    sh_wait_vmcnt<0>();      // clamped tail loads land before the LDS is reused below
     __syncthreads();
 
     const float inv = 1.f / lacc[0];                 // every row of the ones product holds this query's l

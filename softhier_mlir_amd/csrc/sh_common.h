@@ -26,7 +26,8 @@ void sh_set_error(int code, const char *fmt, ...) __attribute__((format(printf, 
 bool sh_hip_ok(hipError_t e, const char *what);
 // Check the last kernel launch.
 bool sh_launch_ok(const char *what);
-// Library-owned device workspace of at least `bytes` (grown on demand, freed at exit).
+// Library-owned device workspace of at least `bytes` for the library stream: one buffer per stream, grown on
+// demand (never under stream capture: that is an error), outgrown buffers kept until the process ends.
 void *sh_workspace(size_t bytes);
 
 // ---- device helpers ---------------------------------------------------------------------------------
@@ -74,6 +75,38 @@ __device__ __forceinline__ float sh_wave_sum(float v) {
 __device__ __forceinline__ float sh_wave_max(float v) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
     return v;
+}
+
+// ---- global -> LDS DMA and LDS transpose reads (GEMM and attention kernels) ----------------------------
+// One global_load_lds_dwordx4: each lane's 16 bytes at `src` land in LDS at lds_wave_base + 16 * lane (M0 holds
+// the wave's LDS base). Completion is counted by vmcnt like any vector memory load.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void sh_lds_dma16(const void *src, uint32_t lds_wave_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_wave_base), "v"(src) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt vmcnt(N) with expcnt / lgkmcnt left unconstrained (gfx9 encoding: vmcnt[3:0], [15:14]).
+template <int N>
+__device__ __forceinline__ void sh_wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+// s_waitcnt lgkmcnt(0) with vmcnt / expcnt left unconstrained.
+__device__ __forceinline__ void sh_wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Byte address of a __shared__ object in the LDS aperture.
+__device__ __forceinline__ uint32_t sh_lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// ds_read_b64_tr_b16: in a group of 16 lanes, lane i supplies the address of an 8-byte segment (4 halves) that
+// is row i / 4, columns 4 (i % 4) .. 4 (i % 4) + 3 of a 4 x 16 block of halves; lane i receives column i of that
+// block (its 4 halves, rows 0..3).
+typedef short sh_s4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ sh_s4 sh_ds_read_tr(uint32_t addr) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) sh_s4 *)(uintptr_t)addr);
 }
 
 static inline bool sh_aligned16(uint64_t p) { return (p & 15u) == 0; }

@@ -366,29 +366,6 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 // (chunk c of row k at c ^ fW(k)) so the 4-row x 64-byte footprint of such a read hits distinct banks.
 // Rows of X beyond M and columns of W beyond N are fetched from clamped (valid) addresses; they only feed
 // outputs that are never stored.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void lds_dma16(const void *src, uint32_t lds_wave_base) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_wave_base), "v"(src) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-// s_waitcnt vmcnt(n) with expcnt / lgkmcnt left unconstrained (gfx9 encoding: vmcnt[3:0], [15:14]).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt");
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
-
-typedef short sh_s4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ sh_s4 ds_read_tr(uint32_t addr) {
-    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) sh_s4 *)(uintptr_t)addr);
-}
-
 template <int BM, int BN, int STAGES>
 struct Cfg2 {
     static constexpr int TM = BM / 2, TN = BN / 2, FM = TM / 32, FN = TN / 32;
@@ -447,15 +424,15 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs a) {
         ws[r] = a.w + (uint64_t)(kbeg + k) * a.ldw + gn;
         wpast[r] = k >= rem;
     }
-    const uint32_t lds0 = lds_addr(smem);
+    const uint32_t lds0 = sh_lds_addr(smem);
     const uint32_t wave_off = (uint32_t)__builtin_amdgcn_readfirstlane(wave * 64 * 16);
 
     // DMA instruction d of the loads of k-slice `src` into LDS stage `stage`: X rounds first, then W rounds
     auto issue_one = [&](int d, int src, int stage) {
         const uint32_t st = lds0 + (uint32_t)stage * (uint32_t)C::STAGE;
         const bool last = KTAIL && src == KT - 1;
-        if (d < C::XR) lds_dma16(last && xpast[d] ? zero : xs[d] + (uint64_t)src * BK, st + d * 4096 + wave_off);
-        else lds_dma16(last && wpast[d - C::XR] ? zero : ws[d - C::XR] + (uint64_t)src * BK * a.ldw,
+        if (d < C::XR) sh_lds_dma16(last && xpast[d] ? zero : xs[d] + (uint64_t)src * BK, st + d * 4096 + wave_off);
+        else sh_lds_dma16(last && wpast[d - C::XR] ? zero : ws[d - C::XR] + (uint64_t)src * BK * a.ldw,
                        st + C::XCH * 16 + (d - C::XR) * 4096 + wave_off);
     };
 
@@ -483,7 +460,7 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs a) {
     constexpr int NM = C::FM * C::FN;                 // MFMAs per k-substep
     constexpr int MT = 4 * NM;                        // per slice
     for (int kt = 0; kt < KT; ++kt) {
-        wait_vmcnt<(STAGES - 2) * C::LOADS>();        // this slice has landed (own wave) ...
+        sh_wait_vmcnt<(STAGES - 2) * C::LOADS>();        // this slice has landed (own wave) ...
         __syncthreads();                              // ... for every wave; the oldest stage is free again
         const int kn = min(kt + STAGES - 1, KT - 1);  // slice whose loads are spread over this slice's MFMAs ...
         const int kst = (kt + STAGES - 1) % STAGES;   // ... into the stage freed by the barrier above
@@ -505,8 +482,8 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs a) {
             for (int j = 0; j < C::FN; ++j) {
                 const uint32_t n = (uint32_t)(wn * C::TN + j * 32 + 16 * (q & 1) + 4 * (iq & 3));
                 const uint32_t k0 = 16 * s + 8 * g + (iq >> 2), k1 = k0 + 4;
-                const sh_s4 lo = ds_read_tr(wbase + k0 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k0)) + 2 * (n & 7));
-                const sh_s4 hi = ds_read_tr(wbase + k1 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k1)) + 2 * (n & 7));
+                const sh_s4 lo = sh_ds_read_tr(wbase + k0 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k0)) + 2 * (n & 7));
+                const sh_s4 hi = sh_ds_read_tr(wbase + k1 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k1)) + 2 * (n & 7));
                 bf[j] = __builtin_bit_cast(sh_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
             }
         };
@@ -536,7 +513,7 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs a) {
             __builtin_amdgcn_sched_barrier(0);
         }
     }
-    wait_vmcnt<0>();     // the clamped tail loads must land before the tile is staged in the same LDS
+    sh_wait_vmcnt<0>();     // the clamped tail loads must land before the tile is staged in the same LDS
     __syncthreads();     // every wavefront is done with the slices before the tile is staged in the same LDS
     epilogue<BM, BN, true, SPLIT, C::FM, C::FN>(a, acc, m0, n0, split, (uint16_t *)smem);
 }
@@ -688,7 +665,7 @@ __global__ __launch_bounds__(512) void k_gemm3(GemmArgs a) {
             src[r] = a.w + (uint64_t)(kbeg + k) * a.ldw + gn;
         }
     }
-    const uint32_t lds0 = lds_addr(smem);
+    const uint32_t lds0 = sh_lds_addr(smem);
     const uint32_t wave_off = (uint32_t)__builtin_amdgcn_readfirstlane(w4 * 64 * 16);
     const int my_rounds = grp == 0 ? C::XR : C::WR;
     auto issue = [&](int slice, int stage) {        // this thread's share of slice `slice` into `stage`
@@ -697,7 +674,7 @@ __global__ __launch_bounds__(512) void k_gemm3(GemmArgs a) {
         for (int r = 0; r < NR; ++r) {
             if (r >= my_rounds) break;
             const uint64_t adv = grp == 0 ? (uint64_t)slice * BK : (uint64_t)slice * BK * a.ldw;
-            lds_dma16(src[r] + adv, st + r * 4096 + wave_off);
+            sh_lds_dma16(src[r] + adv, st + r * 4096 + wave_off);
         }
     };
 
@@ -724,8 +701,8 @@ __global__ __launch_bounds__(512) void k_gemm3(GemmArgs a) {
             for (int j = 0; j < C::FN; ++j) {
                 const uint32_t n = (uint32_t)(col0 + j * 32 + 16 * (q & 1) + 4 * (iq & 3));
                 const uint32_t k0 = 16 * s + 8 * g + (iq >> 2), k1 = k0 + 4;
-                const sh_s4 lo = ds_read_tr(wbase + k0 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k0)) + 2 * (n & 7));
-                const sh_s4 hi = ds_read_tr(wbase + k1 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k1)) + 2 * (n & 7));
+                const sh_s4 lo = sh_ds_read_tr(wbase + k0 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k0)) + 2 * (n & 7));
+                const sh_s4 hi = sh_ds_read_tr(wbase + k1 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k1)) + 2 * (n & 7));
                 bf[s][j] = __builtin_bit_cast(sh_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
             }
         }
@@ -745,8 +722,8 @@ __global__ __launch_bounds__(512) void k_gemm3(GemmArgs a) {
     // prologue: slice 0 complete at barrier 0; group 1 also has its share of slice 1 in flight
     if (KT > 0) {
         issue(0, 0);
-        if (grp == 1 && KT > 1) { issue(1, 1); wait_vmcnt<C::WR>(); }
-        else wait_vmcnt<0>();
+        if (grp == 1 && KT > 1) { issue(1, 1); sh_wait_vmcnt<C::WR>(); }
+        else sh_wait_vmcnt<0>();
     }
     hard_barrier();                                   // barrier 0
     if (grp == 1) hard_barrier();                     // barrier 1: group 1 runs one phase behind
@@ -755,13 +732,13 @@ __global__ __launch_bounds__(512) void k_gemm3(GemmArgs a) {
         // memory phase
         if (grp == 0 && k + 1 < KT) issue(k + 1, st ^ 1);
         read_slice(st);
-        if (grp == 1) wait_vmcnt<0>();                // group 1's share of slice k+1 (issued a phase ago)
+        if (grp == 1) sh_wait_vmcnt<0>();                // group 1's share of slice k+1 (issued a phase ago)
         __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0): the fragments are in registers
         hard_barrier();
         // compute phase
         if (grp == 1 && k + 2 < KT) issue(k + 2, st);
         compute_slice();
-        if (grp == 0) wait_vmcnt<0>();                // group 0's share of slice k+1
+        if (grp == 0) sh_wait_vmcnt<0>();                // group 0's share of slice k+1
         hard_barrier();
     }
     if (grp == 0) hard_barrier();                     // both groups end on the same barrier count
@@ -994,15 +971,15 @@ __global__ __launch_bounds__(NT, MINW) void k_gemm4(GemmArgs a) {
         if (gn >= a.N) gn = a.N - 8;
         ws[r] = a.w + (uint64_t)(kbeg + k) * a.ldw + gn;
     }
-    const uint32_t lds0 = lds_addr(smem);
+    const uint32_t lds0 = sh_lds_addr(smem);
     const uint32_t wave_off = (uint32_t)__builtin_amdgcn_readfirstlane(wave * 64 * 16);
     const uint64_t wadv = (uint64_t)SK * a.ldw;
     auto issue_all = [&](int src, int stage) {      // the LOADS DMAs of k-slice `src` into LDS stage `stage`
         const uint32_t st = lds0 + (uint32_t)stage * (uint32_t)C::STAGE;
 #pragma unroll
-        for (int d = 0; d < C::XR; ++d) lds_dma16(xs[d] + (uint64_t)src * SK, st + d * NT * 16 + wave_off);
+        for (int d = 0; d < C::XR; ++d) sh_lds_dma16(xs[d] + (uint64_t)src * SK, st + d * NT * 16 + wave_off);
 #pragma unroll
-        for (int d = 0; d < C::WR; ++d) lds_dma16(ws[d] + (uint64_t)src * wadv, st + C::XCH * 16 + d * NT * 16 + wave_off);
+        for (int d = 0; d < C::WR; ++d) sh_lds_dma16(ws[d] + (uint64_t)src * wadv, st + C::XCH * 16 + d * NT * 16 + wave_off);
     };
 
     sh_f16v acc[FM][FN];
@@ -1025,8 +1002,8 @@ __global__ __launch_bounds__(NT, MINW) void k_gemm4(GemmArgs a) {
         for (int j = 0; j < FN; ++j) {
             const uint32_t n = (uint32_t)(wn * C::TN + j * 32 + 16 * (q & 1) + 4 * (iq & 3));
             const uint32_t k0 = 16 * s + 8 * g + (iq >> 2), k1 = k0 + 4;
-            const sh_s4 lo = ds_read_tr(wbase + k0 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k0)) + 2 * (n & 7));
-            const sh_s4 hi = ds_read_tr(wbase + k1 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k1)) + 2 * (n & 7));
+            const sh_s4 lo = sh_ds_read_tr(wbase + k0 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k0)) + 2 * (n & 7));
+            const sh_s4 hi = sh_ds_read_tr(wbase + k1 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k1)) + 2 * (n & 7));
             bf[j] = __builtin_bit_cast(sh_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         }
     };
@@ -1049,7 +1026,7 @@ __global__ __launch_bounds__(NT, MINW) void k_gemm4(GemmArgs a) {
 
     sh_h8 a0[FM], b0[FN], a1[FM], b1[FN];
     for (int kt = 0; kt < KT; ++kt) {
-        wait_vmcnt<(STAGES - 2) * C::LOADS>();        // slice kt has landed (this wave's share) ...
+        sh_wait_vmcnt<(STAGES - 2) * C::LOADS>();        // slice kt has landed (this wave's share) ...
         __builtin_amdgcn_s_waitcnt(0xC07F);           // ... and this wave's reads of slice kt - 1 are done
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();                 // every share landed; the stage of slice kt - 1 is free
@@ -1079,10 +1056,10 @@ __global__ __launch_bounds__(NT, MINW) void k_gemm4(GemmArgs a) {
             finish_chunks<BM, BN, FM, FN>(a, acc, m0, n0, q, wm, wn);
             store_all<BM, BN, FM, FN>(a, q, m0, n0, wm, wn);
         }
-        wait_vmcnt<0>();     // no DMA may still target this workgroup's LDS when it exits
+        sh_wait_vmcnt<0>();     // no DMA may still target this workgroup's LDS when it exits
         return;
     }
-    wait_vmcnt<0>();     // the clamped tail loads must land before the tile is staged in the same LDS
+    sh_wait_vmcnt<0>();     // the clamped tail loads must land before the tile is staged in the same LDS
     __syncthreads();
     if constexpr (NT == 256) epilogue<BM, BN, true, SPLIT, FM, FN>(a, acc, m0, n0, split, (uint16_t *)smem);
     else epilogue8<BM, BN, NT, SPLIT, FM, FN>(a, acc, m0, n0, split, (uint16_t *)smem, (uint32_t)(wm * C::TM), (uint32_t)(wn * C::TN));
@@ -1213,7 +1190,19 @@ int env_int(const char *name, int dflt) {
     return (e && *e) ? atoi(e) : dflt;
 }
 
-// Estimated seconds of config i for an (M, N, K) problem cut into `splits` K ranges: the larger of
+// The K ranges a request for `want` splits launches: each range is a whole number of 64-k slices (kps), at
+// most one range per slice, and no trailing range is empty. Every consumer of a split count (the cost model,
+// sh_gemm_plan, the launch) goes through this, so what is priced and reported is what runs.
+struct SplitK { uint32_t splits, kps; };
+SplitK split_k(uint32_t K, uint32_t want) {
+    const uint32_t k = std::max<uint32_t>(K, 1);
+    const uint32_t s = std::max<uint32_t>(1, std::min<uint32_t>(want, sh_cdiv(k, BK)));
+    const uint32_t kps = sh_cdiv(sh_cdiv(k, s), BK) * BK;
+    return {sh_cdiv(k, kps), kps};
+}
+
+// Estimated seconds of config i for an (M, N, K) problem cut into `splits` K ranges (as split_k launches them):
+// the larger of
 //  - throughput: rounds of tiles over the CUs at the config's sustained MFMA fraction (also returned alone
 //    in *thr), and
 //  - latency: no workgroup finishes before its start-up and epilogue plus its chain of BK slices, counted
@@ -1222,11 +1211,13 @@ int env_int(const char *name, int dflt) {
 //    3.0 + 0.16 A us + (0.17 + 0.02 A) us per slice, the register-staged kernel 1.0 + 0.32 A us + (0.88 +
 //    0.013 A) us per slice;
 // plus, in both, the split-K partial traffic and the reduction launch. Small problems are latency-bound.
-double est_time(int i, uint32_t M, uint32_t N, uint32_t K, uint32_t splits, int cus, double *thr = nullptr) {
+double est_time(int i, uint32_t M, uint32_t N, uint32_t K, uint32_t want_splits, int cus, double *thr = nullptr) {
     const KCfg &c = g_cfgs[i];
+    const SplitK sk = split_k(K, want_splits);
+    const uint32_t splits = sk.splits;
     const double tiles = (double)sh_cdiv(M, c.bm) * sh_cdiv(N, c.bn) * splits;
     const double rounds = std::ceil(tiles / cus);
-    const double k_len = (double)sh_cdiv(sh_cdiv(std::max<uint32_t>(K, 1), splits), BK) * BK;
+    const double k_len = (double)sk.kps;
     double t = rounds * c.bm * c.bn * k_len / (c.eff * 2048.0 * 2.4e9);
     const double A = c.bm * c.bn / 1024.0;
     const double fixed_us = c.v2 ? 3.0 + 0.16 * A : 1.0 + 0.32 * A;
@@ -1260,10 +1251,14 @@ Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t wa
         uint32_t lo = 1, hi = 1;
         if (want_splits) lo = hi = want_splits;
         else hi = std::max<uint32_t>(1, std::min<uint32_t>(16, K / 128));
+        uint32_t prev = 0;
         for (uint32_t s = lo; s <= hi && n < kNumCfg * 16; ++s) {
+            const uint32_t eff = split_k(K, s).splits;          // requests that launch the same ranges count once
+            if (eff == prev) continue;
+            prev = eff;
             double thr = 0.0;
-            const double tt = est_time(i, M, N, K, s, cus, &thr);
-            cand[n++] = {tt, thr, i, s};
+            const double tt = est_time(i, M, N, K, eff, cus, &thr);
+            cand[n++] = {tt, thr, i, eff};
             tmin = std::min(tmin, tt);
         }
     }
@@ -1273,7 +1268,7 @@ Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t wa
         if (cand[j].t <= tmin * 1.03 && cand[j].thr < bthr) { bthr = cand[j].thr; best = {cand[j].cfg, cand[j].splits}; }
     const int fc = env_int("SH_GEMM_CFG", -1);
     const int fs = env_int("SH_GEMM_SPLITS", 0);
-    if (fs > 0 && !want_splits) best.splits = (uint32_t)fs;
+    if (fs > 0 && !want_splits) best.splits = split_k(K, (uint32_t)fs).splits;
     if (fc >= 0 && fc < kNumCfg && eligible(g_cfgs[fc], vec, fast, ktail)) best.cfg = fc;
     return best;
 }
@@ -1386,9 +1381,8 @@ int launch(const GemmReq &r, const char *name) {
         p.cfg = tuned_cfg(t, p.cfg, sh_stream());
     }
     KCfg &c = g_cfgs[p.cfg];
-    uint32_t splits = std::max<uint32_t>(1, std::min<uint32_t>(p.splits, sh_cdiv(std::max<uint32_t>(r.K, 1), BK)));
-    const uint32_t kps = sh_cdiv(sh_cdiv(std::max<uint32_t>(r.K, 1), splits), BK) * BK;
-    splits = sh_cdiv(std::max<uint32_t>(r.K, 1), kps);         // no empty trailing split
+    const SplitK sk = split_k(r.K, p.splits);
+    const uint32_t splits = sk.splits, kps = sk.kps;
 
     GemmArgs a{};
     a.x = (const uint16_t *)r.x; a.w = (const uint16_t *)r.w; a.z = (uint16_t *)r.z;

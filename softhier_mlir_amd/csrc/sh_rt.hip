@@ -8,6 +8,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <map>
 #include <vector>
 
 namespace {
@@ -20,8 +21,11 @@ struct ShState {
     void *arena = nullptr;
     size_t arena_bytes = 0;
     std::vector<void *> mallocs;
-    void *ws = nullptr;
-    size_t ws_bytes = 0;
+    // split-K partial workspaces, one per stream (calls on different streams never share partials); an outgrown
+    // buffer is retired, not freed, because a HIP graph captured earlier may still address it
+    struct Ws { void *p = nullptr; size_t bytes = 0; };
+    std::map<hipStream_t, Ws> ws;
+    std::vector<void *> ws_retired;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     bool timer_running = false;
     double last_ns = 0.0;
@@ -66,16 +70,24 @@ int sh_num_xcds() { sh_ensure_init(); return g.xcds; }
 
 void *sh_workspace(size_t bytes) {
     sh_ensure_init();
-    if (bytes <= g.ws_bytes) return g.ws;
-    if (g.ws) {
-        if (!sh_hip_ok(hipStreamSynchronize(g.stream), "workspace sync")) return nullptr;
-        (void)hipFree(g.ws);
-        g.ws = nullptr; g.ws_bytes = 0;
+    ShState::Ws &w = g.ws[g.stream];
+    if (bytes <= w.bytes) return w.p;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(g.stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+        (void)hipGetLastError();
+        sh_set_error(SH_EHIP, "[softhier-ops] split-K workspace of %zu B needed under stream capture (this stream holds %zu B): "
+                     "run the call once on this stream before capturing it", bytes, w.bytes);
+        return nullptr;
     }
+    // geometric growth keeps the retired buffers below the live one in total
     size_t want = bytes < (size_t(64) << 20) ? (size_t(64) << 20) : bytes;
-    if (!sh_hip_ok(hipMalloc(&g.ws, want), "workspace hipMalloc")) { g.ws = nullptr; return nullptr; }
-    g.ws_bytes = want;
-    return g.ws;
+    if (want < 2 * w.bytes) want = 2 * w.bytes;
+    void *p = nullptr;
+    if (!sh_hip_ok(hipMalloc(&p, want), "workspace hipMalloc")) return nullptr;
+    if (w.p) g.ws_retired.push_back(w.p);
+    w.p = p;
+    w.bytes = want;
+    return w.p;
 }
 
 extern "C" {

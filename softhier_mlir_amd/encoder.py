@@ -58,6 +58,7 @@ class Encoder:
         self.lib = shops.load()
         self.lib.sh_init()
         self._bufs: dict = {}
+        self._pingpong: torch.Tensor | None = None   # the stack's second activation buffer (outside _bufs)
         self._plans: dict = {}               # fused-layer call lists by argument set (a stack has one per layer)
         self.gemm_cfg = shops.cfg()          # tile hints 256^3 (library default), as the reference's default policy
         self.tap = None                      # optional tap(name) -> context manager around each op (timing)
@@ -142,24 +143,27 @@ class Encoder:
                 _check(rc, what)
         return out
 
-    def capture(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int) -> "torch.cuda.CUDAGraph":
+    def capture(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int) -> "CapturedLayer":
         """Record one fused layer into a HIP graph (replay with `.replay()` on any stream). The layer runs once
-        eagerly first, so buffers exist and every GEMM shape has its tile configuration settled; during capture
-        the library enqueues on the capture stream, then returns to the stream it had."""
-        self.layer_fused(x, out, p, B, S)
-        torch.cuda.synchronize()
+        eagerly on the capture stream first, so buffers exist, every GEMM shape has its tile configuration settled
+        and the stream's split-K workspace has its size; during capture the library enqueues on the capture
+        stream, then returns to the stream it had. The returned object holds every buffer the graph addresses
+        (the scratch set of this row count, x, out and the weights), so later calls with another row count,
+        which replace the encoder's scratch set, cannot free memory the graph writes."""
         g = torch.cuda.CUDAGraph()
         s = torch.cuda.Stream()
         prev = self.lib.sh_get_stream()
         try:
             with torch.cuda.stream(s):
                 self.lib.sh_set_stream(s.cuda_stream)
+                self.layer_fused(x, out, p, B, S)
+                s.synchronize()
                 with torch.cuda.graph(g, stream=s):
                     self.layer_fused(x, out, p, B, S)
         finally:
             self.lib.sh_set_stream(prev)
         torch.cuda.synchronize()
-        return g
+        return CapturedLayer(g, (dict(self.buffers(B * S)), x, out, p))
 
     @staticmethod
     def op_costs(B: int, S: int, D: int = 768, F: int = 3072, H: int = 12) -> dict:
@@ -184,16 +188,27 @@ class Encoder:
         out = out if out is not None else torch.empty_like(x)
         tmp = None
         if n > 1:                               # the ping-pong buffer persists, so the call plans stay valid
-            tmp = self._bufs.get("pingpong")
-            if tmp is None or tmp.shape != x.shape or tmp.dtype != x.dtype:
+            tmp = self._pingpong
+            if tmp is None or tmp.shape != x.shape or tmp.dtype != x.dtype or tmp.device != x.device:
                 tmp = torch.empty_like(x)
-                self._bufs["pingpong"] = tmp
+                self._pingpong = tmp
         cur = x
         for i, p in enumerate(params):          # ping-pong so that the last layer writes `out`
             dst = out if (n - 1 - i) % 2 == 0 else tmp
             step(cur, dst, p, B, S)
             cur = dst
         return out
+
+
+class CapturedLayer:
+    """A HIP graph of one fused layer and every buffer it addresses, kept alive together."""
+
+    def __init__(self, graph: "torch.cuda.CUDAGraph", keep: tuple):
+        self.graph = graph
+        self._keep = keep
+
+    def replay(self) -> None:
+        self.graph.replay()
 
 
 def flops_per_layer(B: int, S: int, D: int = 768, F: int = 3072) -> int:

@@ -167,3 +167,27 @@ def test_gemm_tile_plan_without_gpu(lib):
     assert plan(8192, 3072, 768)[3] == 1
     out = (C.c_uint32 * 4)()
     assert lib.sh_gemm_plan(0, 8, 8, 0, out) == -1
+
+
+def test_gemm_plan_reports_the_launched_split_count(lib):
+    """sh_gemm_plan reports the split count the launch runs: each K range is a whole number of 64-k slices
+    (kps = 64 ceil(ceil(K / s) / 64)) and no trailing range is empty, so a request for more splits than K has
+    64-k slices, or one that would leave an empty range, reports cdiv(K, kps)."""
+    import ctypes as C
+
+    def plan(M, N, K, splits):
+        out = (C.c_uint32 * 4)()
+        assert lib.sh_gemm_plan(M, N, K, splits, out) == 0
+        return out[3]
+
+    def launched(K, s):
+        slices = -(-K // 64)
+        s = max(1, min(s, slices))
+        kps = 64 * -(-(-(-K // s)) // 64)
+        return -(-K // kps)
+    assert plan(256, 256, 256, 16) == 4            # 4 slices of 64: at most 4 ranges
+    assert plan(256, 768, 768, 5) == 4             # kps = 192: ranges of 192, 192, 192, 192
+    assert plan(256, 768, 768, 7) == 6             # kps = 128
+    for K in (64, 192, 256, 720, 768, 3072):
+        for s in range(1, 20):
+            assert plan(256, 768, K, s) == launched(K, s), (K, s)

@@ -48,6 +48,22 @@ def test_twelve_layer_stack(lib, gpu):
     assert bad == 0, err
 
 
+def test_baseline_config5_twelve_layer_stack_b32(lib, gpu):
+    """BASELINE config 5 as configured: the 12-layer stack at B = 32, S = 256 (layer l seeded 100 + l, input
+    seed 7: the workload bench.py measures), every element of the last layer's output against the oracle's
+    12-layer stack (siglip.py:133-168 per layer, the layer loop of siglip.py:168)."""
+    B, S, D, F, H = 32, 256, 768, 3072, 12
+    ps = [data.encoder_params(D, F, seed=100 + i) for i in range(12)]
+    x = data.normal((B * S, D), 7)
+    enc = encoder.Encoder(D, F, H)
+    out = enc.forward(to_dev(x), [encoder.LayerParams.from_host(p) for p in ps], B=B, S=S, sequence="fused")
+    got = to_np(out)
+    want = refs.encoder_stack(x, ps, H, B=B)
+    bad, err, _ = refs.close(got, want)
+    assert bad == 0, err
+    assert np.isfinite(got).all()
+
+
 def test_captured_layer_graph_replays_match_eager(lib, gpu):
     """The fused layer recorded into a HIP graph: every replay (with eager library work and synchronisations
     between replays, and a new input copied into the captured buffer) stores exactly what the eager call
@@ -71,3 +87,28 @@ def test_captured_layer_graph_replays_match_eager(lib, gpu):
     want = refs.encoder_layer(data.normal((B * S, D), 9), {k: v.cpu().numpy() for k, v in p.t.items()}, H, B=B)
     bad, err, _ = refs.close(to_np(out), want)
     assert bad == 0, err
+
+
+def test_captured_layer_survives_a_call_with_another_row_count(lib, gpu):
+    """A captured layer keeps the scratch buffers it addresses: after an eager call with another batch size (which
+    replaces the encoder's scratch set), replaying the graph still stores what the eager layer stores."""
+    import torch
+    B, S, D, F, H = 2, 256, 768, 3072, 12
+    p = encoder.LayerParams.from_host(data.encoder_params(D, F, seed=100))
+    enc = encoder.Encoder(D, F, H)
+    x = to_dev(data.normal((B * S, D), 7))
+    out = torch.empty_like(x)
+    g = enc.capture(x, out, p, B, S)
+    x3 = to_dev(data.normal((3 * S, D), 8))
+    enc.layer_fused(x3, torch.empty_like(x3), p, 3, S)       # another row count: a new scratch set
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    junk = torch.full((64 << 20,), 7, dtype=torch.float16, device="cuda")   # reuse whatever the cache freed
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    eager = torch.empty_like(x)
+    enc.layer_fused(x, eager, p, B, S)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), eager.view(torch.int16))
+    del junk

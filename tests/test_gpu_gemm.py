@@ -325,6 +325,34 @@ def test_baseline_config2_shapes(lib, gpu, M, N, K, epi):
     assert bad == 0, err
 
 
+@pytest.mark.parametrize("M,N,K,act,splits", [(256, 2304, 768, 0, 1), (256, 3072, 768, 1, 1), (256, 768, 3072, 0, 4)])
+def test_baseline_config2_fp32_bias_epilogue(lib, gpu, M, N, K, act, splits):
+    """BASELINE config 2 with its fp32 bias row (uniform [-0.1, 0.1]) applied in the GEMM epilogue: QKV + bias,
+    FFN-up + bias + tanh-GELU, FFN-down split-K 4 + bias. The epilogue rounds where the unfused sequence stores:
+    r16(r16(X W) + b) [then GELU of that fp16 value]."""
+    import torch
+    x = data.uniform(M, K, 61)
+    w = (data.uniform(K, N, 62).astype(np.float32) / np.sqrt(K)).astype(np.float16)
+    b32 = (data.uniform(1, N, 63).astype(np.float32) * np.float32(0.1))
+    X, W, Bf = to_dev(x), to_dev(w), torch.from_numpy(b32).to("cuda")
+    Z = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    e = shops.epi(bias=A(Bf), bias_fmt=shops.SH_BIAS_FP32, act=shops.SH_ACT_GELU if act else shops.SH_ACT_NONE, splits=splits)
+    assert lib.sh_gemm_ex(A(X), A(W), A(Z), M, N, K, K, N, N, None, e) == 0, shops.last_error()
+    want = refs.r16(refs.r16(refs.gemm(x, w)) + b32)
+    if act:
+        want = refs.gelu(want)
+    got = to_np(Z)
+    bad, err, _ = refs.close(got, want)
+    assert bad == 0, err
+    # the bias is really applied: the same call without it differs by the bias row (within fp16 rounding)
+    Z0 = torch.empty_like(Z)
+    e0 = shops.epi(splits=splits)
+    assert lib.sh_gemm_ex(A(X), A(W), A(Z0), M, N, K, K, N, N, None, e0) == 0, shops.last_error()
+    if not act:
+        d = got.astype(np.float32) - to_np(Z0).astype(np.float32)
+        assert np.abs(d - b32).max() <= 2e-3 * (1 + np.abs(got.astype(np.float32)).max())
+
+
 def test_config1_single_gemm(lib, gpu):
     x = data.uniform(256, 256, 1)
     w = data.uniform(256, 256, 2)
@@ -334,8 +362,9 @@ def test_config1_single_gemm(lib, gpu):
 
 
 def test_large_encoder_shape_property(lib, gpu):
-    """M = 8192 (B = 32 rows of the encoder): a known-answer check at full size. W = I (identity blocks)
-    reproduces X exactly; a row-sum W gives each row's fp32 sum."""
+    """M = 8192 (B = 32 rows of the encoder): known answers at full size. W = I (identity blocks) reproduces X
+    exactly; a W whose column j holds the constant j + 1 (a row-sum W) gives (j + 1) times each row's sum,
+    checked against the float64 row sums within the fp16 tolerance (sums of up to 768 fp32 products)."""
     import torch
     M, K = 8192, 768
     x = data.normal((M, K), 71)
@@ -344,6 +373,14 @@ def test_large_encoder_shape_property(lib, gpu):
     Z = torch.empty((M, K), dtype=torch.float16, device="cuda")
     assert lib.sh_gemm(A(X), A(I), A(Z), M, K, K, K, K, K, None, shops.SH_ALL) == 0
     assert np.array_equal(codes(Z), x.view(np.uint16))
+    N = 64
+    Ws = torch.arange(1, N + 1, dtype=torch.float16, device="cuda").repeat(K, 1).contiguous()
+    Zs = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    assert lib.sh_gemm(A(X), A(Ws), A(Zs), M, N, K, K, N, N, None, shops.SH_ALL) == 0
+    rs = x.astype(np.float64).sum(axis=1)
+    want = rs[:, None] * np.arange(1, N + 1, dtype=np.float64)[None, :]
+    bad, err, _ = refs.close(to_np(Zs), want.astype(np.float32))
+    assert bad == 0, err
 
 
 @pytest.mark.parametrize("M,N,K,mode,tm,acc", [(50, 1600, 720, 0, 0, 0), (200, 720, 960, 1, 0, 0), (241, 960, 960, 0, 0, 0),

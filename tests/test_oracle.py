@@ -256,6 +256,55 @@ def test_encoder_lcg_layer_shapes_and_composition():
     assert np.array_equal(two, refs.encoder_layer(r["OUT"], refs.siglip_params_lcg(D, F, 1), H))
 
 
+# (lo, hi, scale) of every tensor of the reference's LCG layer (siglip_ref.py:12-18, main.c fills)
+SIGLIP_LCG_TABLE = {
+    "wq": (-8, 8, 1 / 128), "wk": (-8, 8, 1 / 128), "wv": (-8, 8, 1 / 128), "wo": (-8, 8, 1 / 128),
+    "w1": (-8, 8, 1 / 128), "w2": (-8, 8, 1 / 256),
+    "bq": (-4, 4, 1 / 16), "bk": (-4, 4, 1 / 16), "bv": (-4, 4, 1 / 16), "bo": (-4, 4, 1 / 16),
+    "b1": (-4, 4, 1 / 16), "b2": (-4, 4, 1 / 16),
+    "g1": (2, 6, 1 / 4), "be1": (-4, 4, 1 / 8), "g2": (2, 6, 1 / 4), "be2": (-4, 4, 1 / 8),
+}
+
+
+@pytest.mark.parametrize("layer", [0, 1])
+def test_siglip_lcg_params_value_sets(layer):
+    """Every tensor of the LCG layer holds exactly the integers lo..hi times its scale (all of them, at the
+    reference's D = 768, F = 3072), in the reference's shapes; the 16 tensors come from 16 different streams, and
+    layer 1 from streams other than layer 0's. The input is {-16..16} / 8."""
+    D, F = 768, 3072
+    p = refs.siglip_params_lcg(D, F, layer=layer)
+    shapes = {"wq": (D, D), "wk": (D, D), "wv": (D, D), "wo": (D, D), "w1": (D, F), "w2": (F, D), "b1": (1, F)}
+    for nm, (lo, hi, sc) in SIGLIP_LCG_TABLE.items():
+        t = p[nm]
+        assert t.dtype == np.float16 and t.shape == shapes.get(nm, (1, D)), nm
+        want = {np.float16(np.float32(v) * np.float32(sc)) for v in range(lo, hi + 1)}
+        assert set(np.unique(t).tolist()) == {float(v) for v in want}, nm
+    heads = {nm: p[nm].ravel()[:64].tobytes() for nm in SIGLIP_LCG_TABLE}
+    assert len(set(heads.values())) == len(heads)                  # no two tensors share a stream prefix
+    if layer:
+        p0 = refs.siglip_params_lcg(D, F, layer=0)
+        assert all(not np.array_equal(p0[nm], p[nm]) for nm in SIGLIP_LCG_TABLE)
+    x = refs.siglip_input_lcg(256, D)
+    assert set(np.unique(x).tolist()) == {v / 8 for v in range(-16, 17)}
+
+
+def test_llm_prefix_tokens_rule():
+    """The prefix token classes of the reference's llmops driver (llmops/main.c tok_prefix): image tokens and the
+    first 5 language tokens class 0, the state token (img + 48) class 1, every other token PAD, with
+    img = S - 64; causal tokens are their own positions."""
+    for S in (64, 128, 256, 1024):
+        tok = refs.llm_tokens(S, "prefix")
+        img = S - 64
+        assert tok.shape == (S,) and tok.dtype == np.uint32
+        assert (tok[:img + 5] == 0).all()
+        assert tok[img + 48] == 1
+        rest = np.ones(S, bool)
+        rest[:img + 5] = False
+        rest[img + 48] = False
+        assert (tok[rest] == refs.LLM_PAD).all() and rest.sum() == 58
+        assert np.array_equal(refs.llm_tokens(S, "causal"), np.arange(S))
+
+
 def test_close_helper():
     bad, err, _ = refs.close(np.array([1.0, 2.0]), np.array([1.015, 2.05]))
     assert bad == 1 and abs(err - 0.05) < 1e-6
