@@ -46,6 +46,9 @@ def parse():
                          "one JSON line each")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the 12-layer stack and the S=1024 attention measurements")
+    ap.add_argument("--library-gemm", action="store_true",
+                    help="instead of the layer line: the four encoder GEMM shapes through sh_gemm_ex (plain and with the "
+                         "layer's epilogue) next to torch.matmul (hipBLASLt), one JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 3 plain device copies of 512 MiB (a known-size kernel for scaling HBM counters)")
     return ap.parse_args()
@@ -382,6 +385,55 @@ def config_table(lib, torch) -> list:
     return rows
 
 
+def library_gemm_table(lib, torch, B: int = 32, S: int = 256, D: int = 768, F: int = 3072) -> dict:
+    """The layer's four GEMM shapes (M = B*S) timed three ways on the same operands: sh_gemm_ex with no epilogue,
+    sh_gemm_ex with the layer's epilogue, and torch.matmul (hipBLASLt, no epilogue). Average of 50 launches back to
+    back with HIP events around them, after 10 warm-up launches; the order of the three is interleaved per shape."""
+    from softhier_mlir_amd import shops
+    A = shops.addr
+    M = B * S
+    shapes = {"qkv": (3 * D, D, "bias"), "out_proj": (D, D, "bias_res"), "ffn_up": (F, D, "bias_gelu"),
+              "ffn_down": (D, F, "bias_res")}
+    out = {}
+    for name, (N, K, epi) in shapes.items():
+        g = torch.Generator(device="cuda").manual_seed(11)
+        x = torch.randn((M, K), dtype=torch.float16, device="cuda", generator=g)
+        w = (torch.randn((K, N), dtype=torch.float16, device="cuda", generator=g) * 0.02).contiguous()
+        b = torch.zeros((1, N), dtype=torch.float16, device="cuda")
+        r = torch.randn((M, N), dtype=torch.float16, device="cuda", generator=g)
+        z = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        zt = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        e_plain = shops.epi()
+        e_layer = shops.epi(bias=A(b), act=shops.SH_ACT_GELU if epi == "bias_gelu" else shops.SH_ACT_NONE,
+                            residual=A(r) if epi == "bias_res" else 0, ldr=N if epi == "bias_res" else 0)
+        runs = {
+            "sh_gemm_ex_plain_us": lambda: lib.sh_gemm_ex(A(x), A(w), A(z), M, N, K, K, N, N, None, e_plain),
+            "sh_gemm_ex_layer_epilogue_us": lambda: lib.sh_gemm_ex(A(x), A(w), A(z), M, N, K, K, N, N, None, e_layer),
+            "torch_matmul_hipblaslt_us": lambda: torch.matmul(x, w, out=zt),
+        }
+        res = {}
+        for key, fn in runs.items():
+            for _ in range(10):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(50):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            res[key] = round(e0.elapsed_time(e1) * 1e3 / 50, 2)
+        flop = 2 * M * N * K
+        res["TFLOP/s_plain"] = round(flop / (res["sh_gemm_ex_plain_us"] * 1e-6) / 1e12, 1)
+        res["TFLOP/s_hipblaslt"] = round(flop / (res["torch_matmul_hipblaslt_us"] * 1e-6) / 1e12, 1)
+        res["shape_MNK"] = [M, N, K]
+        lib.sh_gemm_ex(A(x), A(w), A(z), M, N, K, K, N, N, None, e_plain)
+        torch.cuda.synchronize()
+        res["max_abs_diff_plain_vs_torch"] = round(float((z.float() - zt.float()).abs().max()), 5)
+        out[name] = res
+    return out
+
+
 def cpu_baseline(B: int, S: int, D: int, F: int, H: int, p: dict, x) -> dict:
     """The oracle's numpy restatement of one encoder layer, timed on this host's cores (median of 5)."""
     import numpy as np
@@ -424,6 +476,9 @@ def main() -> int:
     lib.sh_init()
     if args.configs:
         config_table(lib, torch)
+        return 0
+    if args.library_gemm:
+        print(json.dumps({"library_gemm": library_gemm_table(lib, torch, args.batch, args.seq)}), flush=True)
         return 0
     B, S, D, F, H = args.batch, args.seq, 768, 3072, 12
     p = data.encoder_params(D, F, seed=100)

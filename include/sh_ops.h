@@ -189,6 +189,7 @@ uint64_t    sh_captured(char *buf, uint64_t cap);
 int sh_gemm_splitk(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
                    uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg, uint32_t splits, uint32_t cluster);
 
+
 /* Fused GEMM epilogue: z = act(X.W [+ z_old if cfg->accumulate] + bias) rounded to fp16, then
  * [+ residual, rounded again]. bias: 0 or an fp16 (SH_BIAS_FP16) / fp32 (SH_BIAS_FP32) row of N values.
  * residual: 0 or an fp16 [M,N] tensor with leading dim ldr (may alias z). No tile-divisibility rule and no

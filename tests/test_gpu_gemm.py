@@ -373,7 +373,7 @@ def test_large_encoder_shape_property(lib, gpu):
     Z = torch.empty((M, K), dtype=torch.float16, device="cuda")
     assert lib.sh_gemm(A(X), A(I), A(Z), M, K, K, K, K, K, None, shops.SH_ALL) == 0
     assert np.array_equal(codes(Z), x.view(np.uint16))
-    N = 64
+    N = 256
     Ws = torch.arange(1, N + 1, dtype=torch.float16, device="cuda").repeat(K, 1).contiguous()
     Zs = torch.empty((M, N), dtype=torch.float16, device="cuda")
     assert lib.sh_gemm(A(X), A(Ws), A(Zs), M, N, K, K, N, N, None, shops.SH_ALL) == 0
