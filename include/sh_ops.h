@@ -189,6 +189,14 @@ uint64_t    sh_captured(char *buf, uint64_t cap);
 int sh_gemm_splitk(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
                    uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg, uint32_t splits, uint32_t cluster);
 
+/* No counterpart in the reference: sh_gemm_splitk for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments, checks and results
+ * (the same kernels and summation order, so the same bits); the fp32 partials live in a fixed 16 MiB array of
+ * the library's code object on each GPU, so the call makes no hipMalloc / hipFree and skips the one-time tile
+ * timing. Returns -1 (before any GPU work) when the launched split count needs more than 16 MiB of partials
+ * (splits x M x N x 4 bytes). All calls on one GPU share that array: calls that overlap on one GPU race. */
+int sh_gemm_splitk_noalloc(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
+                           uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg, uint32_t splits, uint32_t cluster);
 
 /* Fused GEMM epilogue: z = act(X.W [+ z_old if cfg->accumulate] + bias) rounded to fp16, then
  * [+ residual, rounded again]. bias: 0 or an fp16 (SH_BIAS_FP16) / fp32 (SH_BIAS_FP32) row of N values.

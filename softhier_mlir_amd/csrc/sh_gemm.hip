@@ -1389,8 +1389,27 @@ int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st) {
 struct GemmReq {
     uint64_t x, w, z; uint32_t M, N, K; uint32_t ldx, ldw, ldz;
     uint32_t accumulate; const sh_gemm_epi *epi; uint32_t splits; bool mesh;
+    float *part = nullptr;       // non-null: split-K partials go here (no workspace, no one-time tile timing)
 };
 
+// Split-K partials of sh_gemm_splitk_noalloc: a fixed array in every GPU's copy of the code object, so that entry
+// point allocates nothing. Its device address is looked up once per device (hipGetSymbolAddress with that device
+// current); host code uses that address, never the array's name (which is only a host-side stand-in).
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+__device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+std::map<int, float *> g_scratch_ptr;
+
+float *scratch_ptr() {
+    int dev = -1;
+    if (!sh_hip_ok(hipGetDevice(&dev), "sh_gemm_splitk_noalloc hipGetDevice")) return nullptr;
+    auto it = g_scratch_ptr.find(dev);
+    if (it != g_scratch_ptr.end()) return it->second;
+    void *p = nullptr;
+    if (!sh_hip_ok(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "sh_gemm_splitk_noalloc hipGetSymbolAddress")) return nullptr;
+    if (!p) { sh_set_error(SH_EHIP, "[sh_gemm_splitk_noalloc] scratch array has no device address"); return nullptr; }
+    g_scratch_ptr[dev] = (float *)p;
+    return (float *)p;
+}
 
 int launch(const GemmReq &r, const char *name) {
     if (r.M == 0 || r.N == 0) return 0;
@@ -1403,7 +1422,7 @@ int launch(const GemmReq &r, const char *name) {
     const bool fast = vec && r.K % BK == 0 && r.K > 0;
     Plan p = choose(r.M, r.N, r.K, vec, fast, r.splits);
     if (r.mesh) p.splits = 1;
-    if (fast && p.splits == 1 && g_cfgs[p.cfg].v2) {
+    if (fast && p.splits == 1 && g_cfgs[p.cfg].v2 && !r.part) {
         GemmArgs t{};
         t.x = (const uint16_t *)r.x; t.w = (const uint16_t *)r.w; t.bias = (const void *)bias;
         t.ldx = r.ldx; t.ldw = r.ldw; t.M = r.M; t.N = r.N; t.K = r.K; t.kps = sh_cdiv(r.K, BK) * BK; t.splits = 1;
@@ -1433,8 +1452,17 @@ int launch(const GemmReq &r, const char *name) {
     set_attrs(c);
     if (split) {
         const size_t ws = (size_t)splits * r.M * r.N * sizeof(float);
-        a.part = (float *)sh_workspace(ws);
-        if (!a.part) return SH_EHIP;
+        if (r.part) {
+            if (ws > kNoAllocScratchBytes) {
+                sh_set_error(-1, "[%s] %u splits of %ux%u fp32 partials need %zu B > the %zu B scratch", name, splits, r.M, r.N,
+                             ws, kNoAllocScratchBytes);
+                return -1;
+            }
+            a.part = r.part;
+        } else {
+            a.part = (float *)sh_workspace(ws);
+            if (!a.part) return SH_EHIP;
+        }
     }
     hipLaunchKernelGGL(fn, dim3(nblk), dim3(c.threads), c.lds, st, a);
     if (!sh_launch_ok(name)) return SH_EHIP;
@@ -1505,6 +1533,28 @@ int sh_gemm_splitk(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, u
     return launch(r, "sh_gemm_splitk");
 }
 
+// sh_gemm_splitk with the partials in the library's fixed scratch array: no hipMalloc / hipFree and no one-time
+// tile timing (that allocates a trial output). The launched split count must need at most 16 MiB of fp32
+// partials (splits x M x N x 4 bytes), else -1 before any GPU work. Every call on one GPU shares its array:
+// calls that overlap on one GPU (different streams, or host threads) race on it. Each call writes every partial
+// it reads, so nothing has to be cleared between calls.
+int sh_gemm_splitk_noalloc(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
+                           uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg, uint32_t splits, uint32_t) {
+    sh_gemm_cfg c;
+    cfg_fill(&c, cfg);
+    if (int rc = check_tiled("sh_gemm_splitk_noalloc", c, x, w, z, M, N, K)) return rc;
+    const SplitK sk = split_k(K, splits);
+    if ((size_t)sk.splits * M * N * sizeof(float) > kNoAllocScratchBytes && sk.splits > 1) {
+        sh_set_error(-1, "[sh_gemm_splitk_noalloc] %u splits of %ux%u fp32 partials exceed the %zu B scratch", sk.splits, M, N,
+                     kNoAllocScratchBytes);
+        return -1;
+    }
+    sh_ensure_init();
+    float *part = scratch_ptr();
+    if (!part) return SH_EHIP;
+    GemmReq r{x, w, z, M, N, K, ldx, ldw, ldz, c.accumulate, nullptr, splits, false, part};
+    return launch(r, "sh_gemm_splitk_noalloc");
+}
 
 // The cost model's plan for 16-byte-aligned operands (what a call would launch before the one-time timing of a
 // large problem): out = {tile configuration, tile rows, tile columns, split count}. No GPU work; 256 CUs are
