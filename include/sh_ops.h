@@ -215,6 +215,13 @@ typedef struct {
 int sh_gemm_ex(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
                uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg, const sh_gemm_epi *epi);
 
+/* No counterpart in the reference: sh_gemm_ex with the weight given transposed, wt = W^T as an [N, K] row-major
+ * tensor with leading dim ldwt >= K (z = X . W, W[k][n] = wt[n * ldwt + k]). For callers that keep their weights
+ * transposed once (the encoder layer): both operands are then rows of k, which lets the GPU use larger tiles and
+ * plain LDS reads. Same epilogue, checks and codes as sh_gemm_ex (-1 also for ldwt < K). */
+int sh_gemm_ex_wt(uint64_t x, uint64_t wt, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
+                  uint32_t ldx, uint32_t ldwt, uint32_t ldz, const sh_gemm_cfg *cfg, const sh_gemm_epi *epi);
+
 /* Additive (no counterpart in the reference): the GEMM cost model's plan for an (M, N, K) problem with
  * 16-byte-aligned operands and a split request (0 = library choice): out[0] tile configuration, out[1] /
  * out[2] its tile rows / columns, out[3] the split count. A large problem's first call may still replace the

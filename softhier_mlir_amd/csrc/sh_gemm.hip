@@ -252,7 +252,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs &a, sh_f16v (&acc)[FM][F
     }
 }
 
-template <int BM, int BN, bool VEC, bool SPLIT>
+template <int BM, int BN, bool VEC, bool SPLIT, bool WT = false>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     using C = Cfg<BM, BN>;
     extern __shared__ uint4 smem[];
@@ -281,6 +281,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     uint4 rb[8];
     const bool bload = t < BN;                    // W: one 8 x 8 block per thread, BN blocks per slice
     const int bkb = t & 7, bnc = t >> 3;
+    constexpr int B_PER_T = BN * 8 / 256;         // WT: 16-byte chunks of W^T rows per thread per slice
 
     auto gload = [&](int kt) {
         const uint32_t k0 = kbeg + (uint32_t)kt * BK;
@@ -289,7 +290,13 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
             const int c = t + 256 * i, row = c >> 3, kc = c & 7;
             ra[i] = load8<VEC>(a.x, a.ldx, m0 + row, k0 + 8 * kc, a.M, kend);
         }
-        if (bload) {
+        if constexpr (WT) {                       // W^T [N, K]: rows of k, loaded like X
+#pragma unroll
+            for (int i = 0; i < B_PER_T; ++i) {
+                const int c = t + 256 * i, n = c >> 3, kc = c & 7;
+                rb[i] = load8<VEC>(a.w, a.ldw, n0 + n, k0 + 8 * kc, a.N, kend);
+            }
+        } else if (bload) {
 #pragma unroll
             for (int r = 0; r < 8; ++r) rb[r] = load8<VEC>(a.w, a.ldw, k0 + 8 * bkb + r, n0 + 8 * bnc, kend, a.N);
         }
@@ -301,7 +308,14 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
             const int c = t + 256 * i, row = c >> 3, kc = c & 7;
             pa[row * 8 + (kc ^ swz(row))] = ra[i];
         }
-        if (bload) {
+        if constexpr (WT) {
+            uint4 *pb = sB + st * BN * 8;
+#pragma unroll
+            for (int i = 0; i < B_PER_T; ++i) {
+                const int c = t + 256 * i, n = c >> 3, kc = c & 7;
+                pb[n * 8 + (kc ^ swz(n))] = rb[i];
+            }
+        } else if (bload) {
             uint4 *pb = sB + st * BN * 8;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {         // W^T row n = 8 bnc + j holds column j of the block
@@ -1065,6 +1079,457 @@ __global__ __launch_bounds__(NT, MINW) void k_gemm4(GemmArgs a) {
     else epilogue8<BM, BN, NT, SPLIT, FM, FN>(a, acc, m0, n0, split, (uint16_t *)smem, (uint32_t)(wm * C::TM), (uint32_t)(wn * C::TN));
 }
 
+// ---- v5: LDS-lean tiles, MFMAs interleaved one by one with the LDS reads and DMAs ---------------------------
+// Four wavefronts (2 x 2, one per SIMD), each owning a (BM/2) x (BN/2) block of Z^T accumulators (MFMA operands
+// swapped as in k_gemm4 REG, epilogue straight from registers). SK-wide k-slices (32 or 64) flow through an
+// NST-stage LDS ring filled by global_load_lds_dwordx4; one barrier per slice. Within a slice the work is cut
+// into one segment per 16-k substep: segment s issues the fragment reads of substep s and its share of the
+// DMAs of slice kt + NST - 1, each placed between two MFMAs of substep s - 1 (the MFMAs of a slice's last
+// substep run in the next slice's first segment, after its barrier). The order is fixed in source with
+// sched_barrier fences: every 32-cycle MFMA has at most a few other instructions between it and the next, so
+// the MFMA pipe never waits on a burst of reads, and each read is issued several MFMAs before its first use.
+// W is read either in the caller's [K, N] layout (LDS transpose reads, as k_gemm4) or, with WT, as W^T [N, K]
+// (rows of k like X: plain 16-byte LDS reads, half the LDS read cost). The k order per lane is k_gemm2's
+// (substep s, lane group g -> 8-k chunk 2 s + g), so every configuration stores the same bits.
+// PRE: the epilogue's bias row and residual are loaded into registers at the start of the last slice, so the
+// epilogue does not wait a memory latency after the last MFMA (register budget permitting).
+template <int BM, int BN, int SK, int NST, bool WT>
+struct Cfg5 {
+    static constexpr int TM = BM / 2, TN = BN / 2, FM = TM / 32, FN = TN / 32, NS = SK / 16;
+    static constexpr int XCPR = SK / 8;                  // 16-byte chunks per k-row (X rows; W^T rows)
+    static constexpr int WCPR = BN / 8;                  // chunks per n-row of W ([K, N] layout)
+    static constexpr int XCH = BM * XCPR, WCH = BN * XCPR;
+    static constexpr int XR = XCH / 256, WR = WCH / 256, LOADS = XR + WR;
+    static constexpr int RD = FM + FN * (WT ? 1 : 2);    // LDS read instructions per substep
+    static constexpr int NM = FM * FN;                   // MFMAs per substep
+    static constexpr size_t STAGE = (size_t)(XCH + WCH) * 16;
+    static constexpr size_t LDS = NST * STAGE;
+    static_assert(BM % 64 == 0 && BN % 64 == 0 && (SK == 32 || SK == 64) && XCH % 256 == 0 && WCH % 256 == 0, "tile");
+    static_assert(NST >= 2 && LOADS * (NST - 2) < 64 && LDS <= 160 * 1024, "resources");
+};
+
+template <int BM, int BN, int SK, int NST, bool WT, int MINW, bool SPLIT, bool PRE>
+__global__ __launch_bounds__(256, MINW) void k_gemm5(GemmArgs a) {
+    using C = Cfg5<BM, BN, SK, NST, WT>;
+    constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, NS = C::NS, XCPR = C::XCPR;
+    extern __shared__ uint4 smem[];
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wm = wave >> 1, wn = wave & 1, g = lane >> 5, r32 = lane & 31;
+
+    const uint32_t nblk = a.tiles_m * a.tiles_n * a.splits;
+    uint32_t tm, tn, split;
+    tile_of(a, blockIdx.x, nblk, tm, tn, split);
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t kbeg = split * a.kps;
+    const uint32_t kend = min(a.K, kbeg + a.kps);
+    const int KT = kend > kbeg ? (int)((kend - kbeg) / SK) : 0;
+
+    // per-lane DMA sources of every round; rows past M (W^T rows past N, W columns past N) read clamped valid
+    // addresses and only feed outputs that are never stored
+    const uint16_t *xs[C::XR];
+    const uint16_t *ws[C::WR];
+#pragma unroll
+    for (int r = 0; r < C::XR; ++r) {
+        const uint32_t p = r * 256 + wave * 64 + lane, m = p / XCPR, c = (p % XCPR) ^ xswz<SK>(m);
+        xs[r] = a.x + (uint64_t)min(m0 + m, a.M - 1) * a.ldx + kbeg + 8 * c;
+    }
+#pragma unroll
+    for (int r = 0; r < C::WR; ++r) {
+        const uint32_t p = r * 256 + wave * 64 + lane;
+        if constexpr (WT) {
+            const uint32_t n = p / XCPR, c = (p % XCPR) ^ xswz<SK>(n);
+            ws[r] = a.w + (uint64_t)min(n0 + n, a.N - 1) * a.ldw + kbeg + 8 * c;
+        } else {
+            const uint32_t k = p / C::WCPR, c = (p % C::WCPR) ^ fw<BN>(k);
+            uint32_t gn = n0 + 8 * c;
+            if (gn >= a.N) gn = a.N - 8;
+            ws[r] = a.w + (uint64_t)(kbeg + k) * a.ldw + gn;
+        }
+    }
+    const uint64_t wadv = WT ? (uint64_t)SK : (uint64_t)SK * a.ldw;
+    const uint32_t lds0 = sh_lds_addr(smem);
+    const uint32_t wave_off = (uint32_t)wave * 1024u;
+    auto dma = [&](int d, int src, int stage) {          // DMA instruction d of slice `src` into `stage`
+        const uint32_t st = lds0 + (uint32_t)stage * (uint32_t)C::STAGE;
+        if (d < C::XR) sh_lds_dma16(xs[d] + (uint64_t)src * SK, st + d * 4096 + wave_off);
+        else sh_lds_dma16(ws[d - C::XR] + (uint64_t)src * wadv, st + C::XCH * 16 + (d - C::XR) * 4096 + wave_off);
+    };
+
+    // fragment reads: instruction r of substep s (X fragments first, then W fragments, one or two each)
+    const int q = lane >> 4, iq = lane & 15;
+    // W fragments: WT -> wf (one 16-byte read); [K, N] layout -> two transpose reads into wl / wh, joined at use
+    sh_h8 xf[2][FM], wf[2][WT ? FN : 1];
+    sh_s4 wl[2][WT ? 1 : FN], wh[2][WT ? 1 : FN];
+    auto wfrag = [&](int buf, int j) -> sh_h8 {
+        if constexpr (WT) return wf[buf][j];
+        else return __builtin_bit_cast(sh_h8, __builtin_shufflevector(wl[buf][j], wh[buf][j], 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    auto read = [&](int stage, int s, int r, int buf) {
+        const uint32_t sb = (uint32_t)stage * (uint32_t)C::STAGE;
+        const uint32_t c = (uint32_t)(2 * s + g);
+        if (r < FM) {
+            const uint4 *X = (const uint4 *)((const char *)smem + sb);
+            const uint32_t m = (uint32_t)(wm * TM + r * 32 + r32);
+            xf[buf][r] = __builtin_bit_cast(sh_h8, X[m * XCPR + (c ^ xswz<SK>(m))]);
+        } else if constexpr (WT) {
+            const int j = r - FM;
+            const uint4 *W = (const uint4 *)((const char *)smem + sb + C::XCH * 16);
+            const uint32_t n = (uint32_t)(wn * TN + j * 32 + r32);
+            wf[buf][j] = __builtin_bit_cast(sh_h8, W[n * XCPR + (c ^ xswz<SK>(n))]);
+        } else {
+            const int j = (r - FM) >> 1, half = (r - FM) & 1;
+            const uint32_t wbase = lds0 + sb + C::XCH * 16;
+            const uint32_t n = (uint32_t)(wn * TN + j * 32 + 16 * (q & 1) + 4 * (iq & 3));
+            const uint32_t k = 16 * s + 8 * g + (iq >> 2) + 4 * half;
+            const sh_s4 v = sh_ds_read_tr(wbase + k * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k)) + 2 * (n & 7));
+            if (!half) wl[buf][j] = v;
+            else wh[buf][j] = v;
+        }
+    };
+
+    sh_f16v acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = sh_f16v{};
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {              // the "previous substep" of slice 0 multiplies zeros: acc stays +0
+#pragma unroll
+        for (int i = 0; i < FM; ++i) xf[b][i] = sh_h8{};
+        if constexpr (WT) {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) wf[b][j] = sh_h8{};
+        } else {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) { wl[b][j] = sh_s4{}; wh[b][j] = sh_s4{}; }
+        }
+    }
+
+    // epilogue operands loaded early (PRE): fp16 bias chunks and residual chunks of this lane's outputs
+    // (the largest tiles keep their registers for the accumulators: no early loads there)
+    constexpr bool PRE_B = PRE && FM * FN <= 12, PRE_RES = PRE && FM * FN <= 6;
+    uint4 bq[PRE_B ? FN : 1][2], rq[PRE_RES ? FM : 1][PRE_RES ? FN : 1][2];
+    const bool pre_ok = PRE_B && !a.accumulate && !(a.bias && a.bias_fp32) && (PRE_RES || !a.res);
+    auto prefetch = [&]() {
+#pragma unroll
+        for (int j = 0; j < (PRE_B ? FN : 0); ++j)
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const uint32_t gc = min(n0 + wn * TN + 32 * j + 16 * p + 8 * g, a.N - 8);
+                bq[j][p] = a.bias ? *(const uint4 *)((const uint16_t *)a.bias + gc) : zero4();
+            }
+        if constexpr (PRE_RES) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const uint64_t rowr = (uint64_t)min(m0 + wm * TM + 32 * i + r32, a.M - 1) * a.ldr;
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int p = 0; p < 2; ++p) {
+                        const uint32_t gc = min(n0 + wn * TN + 32 * j + 16 * p + 8 * g, a.N - 8);
+                        rq[i][j][p] = a.res ? *(const uint4 *)(a.res + rowr + gc) : zero4();
+                    }
+            }
+        }
+    };
+
+    if (KT > 0) {
+#pragma unroll
+        for (int s = 0; s < NST - 1; ++s)
+#pragma unroll
+            for (int d = 0; d < C::LOADS; ++d) dma(d, min(s, KT - 1), s);
+    }
+    for (int kt = 0; kt < KT; ++kt) {
+        sh_wait_vmcnt<(NST - 2) * C::LOADS>();           // slice kt landed (this wave's share) ...
+        sh_wait_lgkm0();                                 // ... and this wave's reads of slice kt - 1 are done
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();                    // every share landed; the stage of slice kt - 1 is free
+        __builtin_amdgcn_sched_barrier(0);
+        if (PRE_B && kt == KT - 1 && pre_ok) prefetch();
+        const int st = kt % NST, nsrc = min(kt + NST - 1, KT - 1), nst = (kt + NST - 1) % NST;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const int cur = s & 1, prv = cur ^ 1;
+            // segment s: MFMA q of the previous substep, then read q (if any), then DMA q (if any)
+#pragma unroll
+            for (int qm = 0; qm < C::NM || qm < C::RD; ++qm) {
+                if (qm < C::NM) {            // column-block major: the first MFMAs need the first reads
+                    const int j = qm / FM, i = qm % FM;
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wfrag(prv, j), xf[prv][i], acc[i][j], 0, 0, 0);
+                }
+                if (qm < C::RD) read(st, s, qm, cur);
+                // this segment's DMAs (s * LOADS / NS .. (s + 1) * LOADS / NS) after the first reads
+#pragma unroll
+                for (int d = s * C::LOADS / NS; d < (s + 1) * C::LOADS / NS; ++d)
+                    if (d - s * C::LOADS / NS == qm) dma(d, nsrc, nst);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wfrag((NS - 1) & 1, j), xf[(NS - 1) & 1][i], acc[i][j], 0, 0, 0);
+    if constexpr (SPLIT) {
+        store_partials_zt<BM, BN, FM, FN>(a, acc, m0, n0, split, wm, wn);
+    } else {
+        uint4 qc[FM][FN][2];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) zt_chunks<FM, FN>(acc, i, j, qc[i][j]);
+        if (PRE_B && pre_ok && KT > 0) {
+            if (a.bias || a.res || a.act != SH_ACT_NONE) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+#pragma unroll
+                        for (int p = 0; p < 2; ++p)
+                            qc[i][j][p] = epi_chain8(a, qc[i][j][p], zero4(), bq[PRE_B ? j : 0][p], zero4(),
+                                                     PRE_RES ? rq[PRE_RES ? i : 0][PRE_RES ? j : 0][p] : zero4());
+            }
+        } else {
+            chain_chunks<BM, BN, FM, FN>(a, qc, m0, n0, wm, wn);
+        }
+        store_all<BM, BN, FM, FN>(a, qc, m0, n0, wm, wn);
+    }
+    sh_wait_vmcnt<0>();      // no DMA may still target this workgroup's LDS when it exits
+}
+
+// ---- v6: W given transposed ([N, K], k contiguous), large tiles, any 2-D wavefront grid -------------------
+// For callers that hold W^T (weights transposed once, as the encoder does): both operands are rows of k, so both
+// MFMA fragments come from plain 16-byte LDS reads (no transpose reads) and both DMA streams fetch whole k-row
+// segments with one swizzle. The tile is BM x BN over a WGM x WGN grid of wavefronts (4, 8 or 12 of them), so a
+// CU can hold a 256 x 384 tile whose operand feed, (BM + BN) x 2 bytes per k, stays within what one CU's
+// vector-memory path delivers at the MFMA rate (a 128 x 192 tile needs 1.7x more per FLOP). Slices of SK k
+// flow through an NST-stage DMA ring with one barrier per slice; as in k_gemm5 each 16-k substep's fragment
+// reads and DMAs sit one by one between the MFMAs of the previous substep. Same k order per lane as every
+// other direct-to-LDS kernel (chunk 2 s + g), so the same bits. Epilogue straight from the Z^T accumulators.
+template <int BM, int BN, int WGM, int WGN, int SK, int NST>
+struct Cfg6 {
+    static constexpr int NT = 64 * WGM * WGN;
+    static constexpr int TM = BM / WGM, TN = BN / WGN, FM = TM / 32, FN = TN / 32, NS = SK / 16;
+    static constexpr int XCPR = SK / 8;                  // 16-byte chunks per k-row segment of a slice
+    static constexpr int XCH = BM * XCPR, WCH = BN * XCPR;
+    static constexpr int XR = XCH / NT, WR = WCH / NT, LOADS = XR + WR;
+    static constexpr int RPR = NT / XCPR;                // rows one DMA round covers
+    static constexpr int RD = FM + FN, NM = FM * FN;
+    static constexpr size_t STAGE = (size_t)(XCH + WCH) * 16;
+    static constexpr size_t LDS = NST * STAGE;
+    static_assert(TM % 32 == 0 && TN % 32 == 0 && (SK == 32 || SK == 64) && XCH % NT == 0 && WCH % NT == 0, "tile");
+    // the row swizzle of a k-row segment is the same in every DMA round (rows advance by a multiple of its period)
+    static_assert(RPR % (SK == 64 ? 64 : 16) == 0, "DMA rounds must keep the row swizzle");
+    static_assert(NST >= 2 && LOADS * (NST - 2) < 64 && LDS <= 160 * 1024 && NT <= 1024, "resources");
+};
+
+// DB: fragments double-buffered and interleaved with the previous substep's MFMAs (one wavefront per SIMD);
+// without DB each substep reads its fragments, then runs its MFMAs, and the second wavefront of the SIMD covers
+// the read latency (eight-wavefront tiles, whose accumulators leave no room for a second fragment set).
+template <int BM, int BN, int WGM, int WGN, int SK, int NST, int MINW, bool SPLIT, bool PRE, bool DB = true>
+__global__ __launch_bounds__(64 * WGM * WGN, MINW) void k_gemm6(GemmArgs a) {
+    using C = Cfg6<BM, BN, WGM, WGN, SK, NST>;
+    constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, NS = C::NS, XCPR = C::XCPR, NT = C::NT;
+    extern __shared__ uint4 smem[];
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wm = wave / WGN, wn = wave % WGN, g = lane >> 5, r32 = lane & 31;
+
+    const uint32_t nblk = a.tiles_m * a.tiles_n * a.splits;
+    uint32_t tm, tn, split;
+    tile_of(a, blockIdx.x, nblk, tm, tn, split);
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t kbeg = split * a.kps;
+    const uint32_t kend = min(a.K, kbeg + a.kps);
+    const int KT = kend > kbeg ? (int)((kend - kbeg) / SK) : 0;
+
+    // DMA: round r, lane chunk p = r NT + 64 wave + lane is row r RPR + p0 / XCPR, 16-byte chunk (p0 % XCPR) ^ swizzle
+    // (the same in every round); rows past M (N) read row M - 1 (N - 1): valid memory feeding unstored outputs
+    const uint32_t p0 = (uint32_t)(wave * 64 + lane), row0 = p0 / XCPR, cg = (p0 % XCPR) ^ xswz<SK>(row0);
+    const uint16_t *xbase = a.x + kbeg + 8 * cg, *wbase = a.w + kbeg + 8 * cg;   // a.w holds W^T [N, K]
+    const uint32_t lds0 = sh_lds_addr(smem);
+    const uint32_t wave_off = (uint32_t)wave * 1024u;
+    auto dma = [&](int d, int src, int stage) {          // DMA instruction d of slice `src` into `stage`
+        const uint32_t st = lds0 + (uint32_t)stage * (uint32_t)C::STAGE;
+        if (d < C::XR) {
+            const uint32_t m = min(m0 + (uint32_t)(d * C::RPR) + row0, a.M - 1);
+            sh_lds_dma16(xbase + (uint64_t)m * a.ldx + (uint32_t)src * SK, st + d * NT * 16 + wave_off);
+        } else {
+            const uint32_t n = min(n0 + (uint32_t)((d - C::XR) * C::RPR) + row0, a.N - 1);
+            sh_lds_dma16(wbase + (uint64_t)n * a.ldw + (uint32_t)src * SK, st + C::XCH * 16 + (d - C::XR) * NT * 16 + wave_off);
+        }
+    };
+    constexpr int NB = DB ? 2 : 1;
+    sh_h8 xf[NB][FM], wf[NB][FN];
+    auto read = [&](int stage, int s, int r, int buf) {  // fragment read r of substep s: X fragments, then W^T
+        const char *sb = (const char *)smem + (uint32_t)stage * (uint32_t)C::STAGE;
+        const uint32_t c = (uint32_t)(2 * s + g);
+        if (r < FM) {
+            const uint32_t m = (uint32_t)(wm * TM + r * 32 + r32);
+            xf[buf][r] = __builtin_bit_cast(sh_h8, ((const uint4 *)sb)[m * XCPR + (c ^ xswz<SK>(m))]);
+        } else {
+            const uint32_t n = (uint32_t)(wn * TN + (r - FM) * 32 + r32);
+            wf[buf][r - FM] = __builtin_bit_cast(sh_h8, ((const uint4 *)(sb + C::XCH * 16))[n * XCPR + (c ^ xswz<SK>(n))]);
+        }
+    };
+
+    sh_f16v acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = sh_f16v{};
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {             // the "previous substep" of slice 0 multiplies zeros: acc stays +0
+#pragma unroll
+        for (int i = 0; i < FM; ++i) xf[b][i] = sh_h8{};
+#pragma unroll
+        for (int j = 0; j < FN; ++j) wf[b][j] = sh_h8{};
+    }
+
+    // PRE: the bias row (and, for small per-wave blocks, the residual) loaded at the start of the last slice
+    constexpr bool PRE_B = PRE, PRE_RES = PRE && FM * FN <= 6;
+    uint4 bq[PRE_B ? FN : 1][2], rq[PRE_RES ? FM : 1][PRE_RES ? FN : 1][2];
+    const bool pre_ok = !SPLIT && PRE_B && !a.accumulate && !(a.bias && a.bias_fp32) && (PRE_RES || !a.res);
+    auto prefetch = [&]() {
+#pragma unroll
+        for (int j = 0; j < (PRE_B ? FN : 0); ++j)
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const uint32_t gc = min(n0 + wn * TN + 32 * j + 16 * p + 8 * g, a.N - 8);
+                bq[j][p] = a.bias ? *(const uint4 *)((const uint16_t *)a.bias + gc) : zero4();
+            }
+        if constexpr (PRE_RES) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const uint64_t rowr = (uint64_t)min(m0 + wm * TM + 32 * i + r32, a.M - 1) * a.ldr;
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int p = 0; p < 2; ++p) {
+                        const uint32_t gc = min(n0 + wn * TN + 32 * j + 16 * p + 8 * g, a.N - 8);
+                        rq[i][j][p] = a.res ? *(const uint4 *)(a.res + rowr + gc) : zero4();
+                    }
+            }
+        }
+    };
+
+    if (KT > 0) {
+#pragma unroll
+        for (int s = 0; s < NST - 1; ++s)
+#pragma unroll
+            for (int d = 0; d < C::LOADS; ++d) dma(d, min(s, KT - 1), s);
+    }
+    for (int kt = 0; kt < KT; ++kt) {
+        sh_wait_vmcnt<(NST - 2) * C::LOADS>();           // slice kt landed (this wave's share) ...
+        sh_wait_lgkm0();                                 // ... and this wave's reads of slice kt - 1 are done
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();                    // every share landed; the stage of slice kt - 1 is free
+        __builtin_amdgcn_sched_barrier(0);
+        if (kt == KT - 1 && pre_ok) prefetch();
+        const int st = kt % NST, nsrc = min(kt + NST - 1, KT - 1), nst = (kt + NST - 1) % NST;
+        if constexpr (DB) {
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const int cur = s & 1, prv = cur ^ 1;
+#pragma unroll
+                for (int qm = 0; qm < C::NM || qm < C::RD; ++qm) {
+                    if (qm < C::NM) {            // column-block major: the first MFMAs need the first reads
+                        const int j = qm / FM, i = qm % FM;
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[prv][j], xf[prv][i], acc[i][j], 0, 0, 0);
+                    }
+                    if (qm < C::RD) read(st, s, qm, cur);
+#pragma unroll
+                    for (int d = s * C::LOADS / NS; d < (s + 1) * C::LOADS / NS; ++d)
+                        if (d - s * C::LOADS / NS == qm) dma(d, nsrc, nst);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int d = 0; d < C::LOADS; ++d) dma(d, nsrc, nst);
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+#pragma unroll
+                for (int r = 0; r < C::RD; ++r) read(st, s, r, 0);
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int i = 0; i < FM; ++i)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[0][j], xf[0][i], acc[i][j], 0, 0, 0);
+            }
+        }
+    }
+    if constexpr (DB) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[(NS - 1) & 1][j], xf[(NS - 1) & 1][i], acc[i][j], 0, 0, 0);
+    }
+
+    // lane chunk (i, j, p): row m0 + wm TM + 32 i + r32, columns n0 + wn TN + 32 j + 16 p + 8 g
+    if constexpr (SPLIT) {
+        float *P = a.part + (uint64_t)split * a.M * a.N;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const uint32_t gm = m0 + wm * TM + 32 * i + r32, gn = n0 + wn * TN + 32 * j + 8 * u + 4 * g;
+                    if (gm < a.M && gn < a.N)
+                        *(float4 *)(P + (uint64_t)gm * a.N + gn) =
+                            make_float4(acc[i][j][4 * u], acc[i][j][4 * u + 1], acc[i][j][4 * u + 2], acc[i][j][4 * u + 3]);
+                }
+    } else {
+        uint4 qc[FM][FN][2];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) zt_chunks<FM, FN>(acc, i, j, qc[i][j]);
+        const bool any = a.accumulate || a.bias || a.res || a.act != SH_ACT_NONE;
+        if (any) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const uint32_t gmc = min(m0 + wm * TM + 32 * i + r32, a.M - 1);
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int p = 0; p < 2; ++p) {
+                        const uint32_t gc = min(n0 + wn * TN + 32 * j + 16 * p + 8 * g, a.N - 8);
+                        uint4 zo = zero4(), b0 = zero4(), b1 = zero4(), rr = zero4();
+                        if (pre_ok && KT > 0) {
+                            b0 = bq[PRE_B ? j : 0][p];
+                            if constexpr (PRE_RES) rr = rq[i][j][p];
+                            else if (a.res) rr = *(const uint4 *)(a.res + (uint64_t)gmc * a.ldr + gc);
+                        } else {
+                            if (a.accumulate) zo = *(const uint4 *)(a.z + (uint64_t)gmc * a.ldz + gc);
+                            if (a.bias && a.bias_fp32) {
+                                b0 = *(const uint4 *)((const float *)a.bias + gc);
+                                b1 = *(const uint4 *)((const float *)a.bias + gc + 4);
+                            } else if (a.bias) {
+                                b0 = *(const uint4 *)((const uint16_t *)a.bias + gc);
+                            }
+                            if (a.res) rr = *(const uint4 *)(a.res + (uint64_t)gmc * a.ldr + gc);
+                        }
+                        qc[i][j][p] = epi_chain8(a, qc[i][j][p], zo, b0, b1, rr);
+                    }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    const uint32_t gm = m0 + wm * TM + 32 * i + r32, gn = n0 + wn * TN + 32 * j + 16 * p + 8 * g;
+                    if (gm < a.M && gn < a.N) *(uint4 *)(a.z + (uint64_t)gm * a.ldz + gn) = qc[i][j][p];
+                }
+    }
+    sh_wait_vmcnt<0>();      // no DMA may still target this workgroup's LDS when it exits
+}
+
 template <bool VEC>
 // One item per thread in 64-thread workgroups: a split-K output is usually small (M of a few hundred), and
 // single-wave workgroups spread its items over every CU.
@@ -1122,13 +1587,22 @@ __global__ __launch_bounds__(64) void k_splitk_reduce(GemmArgs a, ShDiv div, uin
 typedef void (*KernelFn)(GemmArgs);
 // v2 entries need vec operands and K % 64 == 0; v1 entries take anything (scalar variants for small tiles).
 // ktail: the kernel also takes K % 64 != 0 (vector operands; the last, partial k-slice reads zeros past K).
+// wt: the configuration computes X . W from W^T ([N, K], sh_gemm_ex_wt) and only serves such calls; the
+// register-staged configurations serve both layouts (wt_vec / wt_scalar: their W^T variants).
 struct KCfg {
     int bm, bn, stages; bool v2; KernelFn vec[2], scalar[2]; size_t lds; float eff; bool attr_set; int threads = 256;
     bool ktail = false; KernelFn tail[2] = {nullptr, nullptr};     // the K % 64 != 0 variants (unsplit, split)
+    bool wt = false; KernelFn wt_vec[2] = {nullptr, nullptr}, wt_scalar[2] = {nullptr, nullptr};
 };
 
 #define SH_KCFG(BM, BN, EFF) { BM, BN, 2, false, { k_gemm<BM, BN, true, false>, k_gemm<BM, BN, true, true> }, \
-                               { k_gemm<BM, BN, false, false>, k_gemm<BM, BN, false, true> }, Cfg<BM, BN>::LDS, EFF, false }
+                               { k_gemm<BM, BN, false, false>, k_gemm<BM, BN, false, true> }, Cfg<BM, BN>::LDS, EFF, false, 256, \
+                               false, { nullptr, nullptr }, false, \
+                               { k_gemm<BM, BN, true, false, true>, k_gemm<BM, BN, true, true, true> }, \
+                               { k_gemm<BM, BN, false, false, true>, k_gemm<BM, BN, false, true, true> } }
+#define SH_KCFG6(BM, BN, WGM, WGN, SK, NST, W, PRE, DB, EFF) \
+    { BM, BN, NST, true, { k_gemm6<BM, BN, WGM, WGN, SK, NST, W, false, PRE, DB>, k_gemm6<BM, BN, WGM, WGN, SK, NST, W, true, PRE, DB> }, \
+      { nullptr, nullptr }, Cfg6<BM, BN, WGM, WGN, SK, NST>::LDS, EFF, false, 64 * WGM * WGN, false, { nullptr, nullptr }, true }
 #define SH_KCFG2(BM, BN, ST, EFF) { BM, BN, ST, true, { k_gemm2<BM, BN, ST, false>, k_gemm2<BM, BN, ST, true> }, \
                                     { nullptr, nullptr }, Cfg2<BM, BN, ST>::LDS, EFF, false, 256, true, \
                                     { k_gemm2<BM, BN, ST, false, true>, k_gemm2<BM, BN, ST, true, true> } }
@@ -1138,6 +1612,9 @@ struct KCfg {
                                        { nullptr, nullptr }, (size_t)(ST) * Cfg4<BN, ST, 256, BM>::STAGE, EFF, false, 256 }
 #define SH_KCFG4S(BM, BN, ST, W, EFF) { BM, BN, ST, true, { k_gemm4<BN, ST, false, 256, BM, W, true, 64>, k_gemm4<BN, ST, true, 256, BM, W, true, 64> }, \
                                        { nullptr, nullptr }, (size_t)(ST) * Cfg4<BN, ST, 256, BM, 64>::STAGE, EFF, false, 256 }
+#define SH_KCFG5(BM, BN, SK, NST, W, EFF) { BM, BN, NST, true, { k_gemm5<BM, BN, SK, NST, false, W, false, true>, \
+                                              k_gemm5<BM, BN, SK, NST, false, W, true, true> }, \
+                                            { nullptr, nullptr }, Cfg5<BM, BN, SK, NST, false>::LDS, EFF, false, 256 }
 #define SH_KCFG3(BM, BN, EFF) { BM, BN, 2, true, { k_gemm3<BM, BN, false>, k_gemm3<BM, BN, true> }, \
                                 { nullptr, nullptr }, Cfg3<BM, BN>::LDS, EFF, false, 512 }
 // eff = sustained fraction of the MFMA peak per CU measured for each tile on MI355X (tile-time model of
@@ -1176,6 +1653,30 @@ KCfg g_cfgs[] = {
     SH_KCFG2(64, 64, 3, 0.13f),
     SH_KCFG2(64, 128, 2, 0.16f),
     SH_KCFG2(128, 64, 2, 0.16f),
+    // LDS-lean tiles with MFMA / read / DMA interleaving (k_gemm5)
+    SH_KCFG5(256, 256, 64, 2, 1, 0.40f),
+    SH_KCFG5(256, 256, 32, 4, 1, 0.40f),
+    SH_KCFG5(256, 192, 64, 2, 1, 0.38f),
+    SH_KCFG5(256, 192, 32, 4, 1, 0.38f),
+    SH_KCFG5(128, 192, 64, 3, 1, 0.36f),
+    SH_KCFG5(128, 192, 64, 2, 2, 0.36f),
+    SH_KCFG5(128, 256, 64, 2, 1, 0.36f),
+    SH_KCFG5(256, 128, 64, 2, 1, 0.36f),
+    // W^T operand (sh_gemm_ex_wt): 4 / 8 wavefronts, up to 256 x 384 tiles (k_gemm6)
+    SH_KCFG6(256, 384, 2, 4, 64, 2, 2, false, false, 0.50f),
+    SH_KCFG6(256, 384, 2, 4, 32, 4, 2, false, false, 0.50f),
+    SH_KCFG6(256, 256, 2, 4, 64, 2, 2, false, true, 0.48f),
+    SH_KCFG6(256, 256, 2, 4, 64, 2, 2, false, false, 0.48f),
+    SH_KCFG6(256, 256, 2, 2, 32, 4, 1, true, true, 0.46f),
+    SH_KCFG6(256, 192, 2, 2, 32, 4, 1, true, true, 0.44f),
+    SH_KCFG6(128, 576, 2, 2, 32, 3, 1, false, true, 0.44f),
+    SH_KCFG6(128, 192, 2, 2, 32, 6, 1, true, true, 0.40f),
+    SH_KCFG6(128, 192, 2, 2, 32, 4, 2, true, true, 0.40f),
+    SH_KCFG6(128, 192, 4, 2, 64, 3, 2, true, false, 0.40f),
+    SH_KCFG6(64, 64, 2, 2, 32, 4, 2, false, true, 0.12f),        // small W^T tiles (small problems)
+    SH_KCFG6(128, 64, 2, 2, 32, 4, 2, false, true, 0.16f),
+    SH_KCFG6(64, 128, 2, 2, 32, 4, 2, false, true, 0.16f),
+    SH_KCFG6(128, 128, 2, 2, 32, 4, 2, true, true, 0.25f),
 };
 #undef SH_KCFG
 #undef SH_KCFG2
@@ -1183,6 +1684,8 @@ KCfg g_cfgs[] = {
 #undef SH_KCFG4
 #undef SH_KCFG4R
 #undef SH_KCFG4S
+#undef SH_KCFG5
+#undef SH_KCFG6
 constexpr int kNumCfg = sizeof(g_cfgs) / sizeof(g_cfgs[0]);
 
 int env_int(const char *name, int dflt) {
@@ -1231,12 +1734,16 @@ double est_time(int i, uint32_t M, uint32_t N, uint32_t K, uint32_t want_splits,
 struct Plan { int cfg; uint32_t splits; };
 
 // fast: vector operands and K % 64 == 0; ktail: vector operands with a partial last k-slice
-bool eligible(const KCfg &c, bool vec, bool fast, bool ktail) {
-    if (c.v2) return fast || (ktail && c.ktail);
+// A W^T call with aligned operands and K % 64 == 0 runs only on the W^T direct-to-LDS tiles, which store the bits
+// of the W-layout direct-to-LDS tiles; otherwise it takes the register-staged tiles (the bits of the W-layout
+// register-staged tiles).
+bool eligible(const KCfg &c, bool vec, bool fast, bool ktail, bool wt) {
+    if (c.v2) return c.wt == wt && (fast || (!wt && ktail && c.ktail));
+    if (wt && fast) return false;
     return vec || c.bm * c.bn <= 128 * 128;
 }
 
-Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t want_splits) {
+Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t want_splits, bool wt = false) {
     const bool ktail = vec && K > 0 && K % BK != 0;
     const int cus = sh_num_cus() > 0 ? sh_num_cus() : 256;
     // Every eligible (config, splits) is estimated; among those within 3 % of the fastest estimate the one with
@@ -1247,7 +1754,7 @@ Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t wa
     int n = 0;
     double tmin = 1e300;
     for (int i = 0; i < kNumCfg; ++i) {
-        if (!eligible(g_cfgs[i], vec, fast, ktail)) continue;
+        if (!eligible(g_cfgs[i], vec, fast, ktail, wt)) continue;
         uint32_t lo = 1, hi = 1;
         if (want_splits) lo = hi = want_splits;
         else hi = std::max<uint32_t>(1, std::min<uint32_t>(16, K / 128));
@@ -1269,7 +1776,7 @@ Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t wa
     const int fc = env_int("SH_GEMM_CFG", -1);
     const int fs = env_int("SH_GEMM_SPLITS", 0);
     if (fs > 0 && !want_splits) best.splits = split_k(K, (uint32_t)fs).splits;
-    if (fc >= 0 && fc < kNumCfg && eligible(g_cfgs[fc], vec, fast, ktail)) best.cfg = fc;
+    if (fc >= 0 && fc < kNumCfg && eligible(g_cfgs[fc], vec, fast, ktail, wt)) best.cfg = fc;
     return best;
 }
 
@@ -1279,6 +1786,8 @@ void set_attrs(KCfg &c) {
         if (c.vec[v]) (void)hipFuncSetAttribute((const void *)c.vec[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
         if (c.scalar[v]) (void)hipFuncSetAttribute((const void *)c.scalar[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
         if (c.tail[v]) (void)hipFuncSetAttribute((const void *)c.tail[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
+        if (c.wt_vec[v]) (void)hipFuncSetAttribute((const void *)c.wt_vec[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
+        if (c.wt_scalar[v]) (void)hipFuncSetAttribute((const void *)c.wt_scalar[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
     }
     c.attr_set = true;
 }
@@ -1294,11 +1803,11 @@ void set_grid(GemmArgs &a, const KCfg &c) {
 // accumulates K in the same order with the same MFMA, so they store bit-identical results and the choice only
 // changes speed. Trial runs write a scratch output (no residual, no accumulate; bias and activation as in the
 // call); the winner is cached per shape. Skipped under stream capture, for small problems, or SH_GEMM_TUNE=0.
-typedef std::tuple<uint32_t, uint32_t, uint32_t, uint64_t, uint64_t, uint32_t, uint32_t> TuneKey;
+typedef std::tuple<uint32_t, uint32_t, uint32_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t> TuneKey;   // + wt
 std::map<TuneKey, int> g_tuned;
 
 // SH_GEMM_TUNE_FILE=path: choices are read from that file at the first tuning decision and every new choice is
-// appended to it ("M N K ldx ldw bias act cfg" per line), so a later process (a counter run, under which the
+// appended to it ("M N K ldx ldw bias act wt cfg" per line), so a later process (a counter run, under which the
 // timing itself would be distorted) launches exactly the tiles an earlier timed run chose.
 void tune_file_load() {
     static bool done = false;
@@ -1308,9 +1817,9 @@ void tune_file_load() {
     if (!path || !*path) return;
     FILE *f = fopen(path, "r");
     if (!f) return;
-    unsigned M, N, K, b, act; unsigned long long ldx, ldw; int cfg;
-    while (fscanf(f, "%u %u %u %llu %llu %u %u %d", &M, &N, &K, &ldx, &ldw, &b, &act, &cfg) == 8)
-        if (cfg >= 0 && cfg < kNumCfg && g_cfgs[cfg].v2) g_tuned[TuneKey{M, N, K, ldx, ldw, b, act}] = cfg;
+    unsigned M, N, K, b, act, wt; unsigned long long ldx, ldw; int cfg;
+    while (fscanf(f, "%u %u %u %llu %llu %u %u %u %d", &M, &N, &K, &ldx, &ldw, &b, &act, &wt, &cfg) == 9)
+        if (cfg >= 0 && cfg < kNumCfg && g_cfgs[cfg].v2 && g_cfgs[cfg].wt == (wt != 0)) g_tuned[TuneKey{M, N, K, ldx, ldw, b, act, wt}] = cfg;
     fclose(f);
 }
 
@@ -1319,12 +1828,12 @@ void tune_file_append(const TuneKey &k, int cfg) {
     if (!path || !*path) return;
     FILE *f = fopen(path, "a");
     if (!f) return;
-    fprintf(f, "%u %u %u %llu %llu %u %u %d\n", std::get<0>(k), std::get<1>(k), std::get<2>(k), (unsigned long long)std::get<3>(k),
-            (unsigned long long)std::get<4>(k), std::get<5>(k), std::get<6>(k), cfg);
+    fprintf(f, "%u %u %u %llu %llu %u %u %u %d\n", std::get<0>(k), std::get<1>(k), std::get<2>(k), (unsigned long long)std::get<3>(k),
+            (unsigned long long)std::get<4>(k), std::get<5>(k), std::get<6>(k), std::get<7>(k), cfg);
     fclose(f);
 }
 
-int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st) {
+int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st, bool wt) {
     static const int enabled = env_int("SH_GEMM_TUNE", 1);
     if (!enabled || env_int("SH_GEMM_CFG", -1) >= 0) return heur;
     const int cus = sh_num_cus() > 0 ? sh_num_cus() : 256;
@@ -1332,7 +1841,7 @@ int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st) {
     (void)est_time(heur, call.M, call.N, call.K, 1, cus, &thr);
     if (thr < 12e-6) return heur;                    // the throughput estimate: small problems keep the model's tile
     tune_file_load();
-    const TuneKey key{call.M, call.N, call.K, call.ldx, call.ldw, call.bias ? 1u + call.bias_fp32 : 0u, call.act};
+    const TuneKey key{call.M, call.N, call.K, call.ldx, call.ldw, call.bias ? 1u + call.bias_fp32 : 0u, call.act, wt ? 1u : 0u};
     auto it = g_tuned.find(key);
     if (it != g_tuned.end()) return it->second;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -1351,7 +1860,7 @@ int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st) {
         for (int round = 0; round < 3 && ok; ++round)
             for (int i = 0; i < kNumCfg && ok; ++i) {
                 KCfg &c = g_cfgs[i];
-                if (!c.v2) continue;
+                if (!c.v2 || c.wt != wt) continue;
                 set_attrs(c);
                 set_grid(a, c);
                 const dim3 grid(a.tiles_m * a.tiles_n);
@@ -1366,12 +1875,12 @@ int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st) {
         if (ok) {
             float best_ms = 1e30f;
             for (int i = 0; i < kNumCfg; ++i)
-                if (g_cfgs[i].v2 && mins[i] < best_ms) { best_ms = mins[i]; best = i; }
+                if (g_cfgs[i].v2 && g_cfgs[i].wt == wt && mins[i] < best_ms) { best_ms = mins[i]; best = i; }
             if (env_int("SH_GEMM_VERBOSE", 0)) {      // the one-time choice on stderr: model pick, winner, all times
                 fprintf(stderr, "[sh_gemm] tuned %ux%ux%u: model cfg %d (%.2f us), chose cfg %d (%.2f us);", call.M, call.N, call.K,
                         heur, 500.f * mins[heur], best, 500.f * best_ms);
                 for (int i = 0; i < kNumCfg; ++i)
-                    if (g_cfgs[i].v2) fprintf(stderr, " %d:%.2f", i, 500.f * mins[i]);
+                    if (g_cfgs[i].v2 && g_cfgs[i].wt == wt) fprintf(stderr, " %d:%.2f", i, 500.f * mins[i]);
                 fprintf(stderr, "\n");
             }
         }
@@ -1390,6 +1899,7 @@ struct GemmReq {
     uint64_t x, w, z; uint32_t M, N, K; uint32_t ldx, ldw, ldz;
     uint32_t accumulate; const sh_gemm_epi *epi; uint32_t splits; bool mesh;
     float *part = nullptr;       // non-null: split-K partials go here (no workspace, no one-time tile timing)
+    bool wt = false;             // w holds W^T ([N, K], leading dim ldw)
 };
 
 // Split-K partials of sh_gemm_splitk_noalloc: a fixed array in every GPU's copy of the code object, so that entry
@@ -1420,14 +1930,14 @@ int launch(const GemmReq &r, const char *name) {
                      sh_aligned16(r.x) && sh_aligned16(r.w) && sh_aligned16(r.z) &&
                      (!res || (ldr % 8 == 0 && sh_aligned16(res))) && (!bias || sh_aligned16(bias));
     const bool fast = vec && r.K % BK == 0 && r.K > 0;
-    Plan p = choose(r.M, r.N, r.K, vec, fast, r.splits);
+    Plan p = choose(r.M, r.N, r.K, vec, fast, r.splits, r.wt);
     if (r.mesh) p.splits = 1;
     if (fast && p.splits == 1 && g_cfgs[p.cfg].v2 && !r.part) {
         GemmArgs t{};
         t.x = (const uint16_t *)r.x; t.w = (const uint16_t *)r.w; t.bias = (const void *)bias;
         t.ldx = r.ldx; t.ldw = r.ldw; t.M = r.M; t.N = r.N; t.K = r.K; t.kps = sh_cdiv(r.K, BK) * BK; t.splits = 1;
         t.bias_fp32 = (e && e->bias_fmt == SH_BIAS_FP32) ? 1 : 0; t.act = e ? e->act : 0;
-        p.cfg = tuned_cfg(t, p.cfg, sh_stream());
+        p.cfg = tuned_cfg(t, p.cfg, sh_stream(), r.wt);
     }
     KCfg &c = g_cfgs[p.cfg];
     const SplitK sk = split_k(r.K, p.splits);
@@ -1448,7 +1958,8 @@ int launch(const GemmReq &r, const char *name) {
 
     hipStream_t st = sh_stream();
     const bool split = splits > 1;
-    KernelFn fn = (c.v2 && !fast) ? c.tail[split] : (vec || c.v2) ? c.vec[split] : c.scalar[split];   // !fast: K % 64 != 0
+    KernelFn fn = r.wt ? (c.v2 ? c.vec[split] : vec ? c.wt_vec[split] : c.wt_scalar[split])
+                       : (c.v2 && !fast) ? c.tail[split] : (vec || c.v2) ? c.vec[split] : c.scalar[split];   // !fast: K % 64 != 0
     set_attrs(c);
     if (split) {
         const size_t ws = (size_t)splits * r.M * r.N * sizeof(float);
@@ -1580,6 +2091,20 @@ int sh_gemm_ex(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint3
     if (epi && epi->act > SH_ACT_GELU) { sh_set_error(-1, "[sh_gemm_ex] unknown act %u", epi->act); return -1; }
     GemmReq r{x, w, z, M, N, K, ldx, ldw, ldz, c.accumulate, epi, epi ? epi->splits : 1u, false};
     return launch(r, "sh_gemm_ex");
+}
+
+int sh_gemm_ex_wt(uint64_t x, uint64_t wt, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
+                  uint32_t ldx, uint32_t ldwt, uint32_t ldz, const sh_gemm_cfg *cfg, const sh_gemm_epi *epi) {
+    sh_gemm_cfg c;
+    cfg_fill(&c, cfg);
+    if (!x || !wt || !z) { sh_set_error(-1, "[sh_gemm_ex_wt] NULL tensor address"); return -1; }
+    if (c.fmt != SH_FP16) { sh_set_error(-1, "[sh_gemm_ex_wt] fmt %u: only SH_FP16 is implemented", c.fmt); return -1; }
+    if (ldwt < K) { sh_set_error(-1, "[sh_gemm_ex_wt] ldwt %u < K %u", ldwt, K); return -1; }
+    if (epi && epi->residual && epi->ldr < N) { sh_set_error(-1, "[sh_gemm_ex_wt] ldr %u < N %u", epi->ldr, N); return -1; }
+    if (epi && epi->act > SH_ACT_GELU) { sh_set_error(-1, "[sh_gemm_ex_wt] unknown act %u", epi->act); return -1; }
+    GemmReq r{x, wt, z, M, N, K, ldx, ldwt, ldz, c.accumulate, epi, epi ? epi->splits : 1u, false};
+    r.wt = true;
+    return launch(r, "sh_gemm_ex_wt");
 }
 
 int sh_gemm_mesh(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,

@@ -66,6 +66,7 @@ _SIGS: dict[str, tuple] = {
     "sh_gemm_splitk": (i32, [u64, u64, u64, u32, u32, u32, u32, u32, u32, C.POINTER(sh_gemm_cfg), u32, u32]),
     "sh_gemm_splitk_noalloc": (i32, [u64, u64, u64, u32, u32, u32, u32, u32, u32, C.POINTER(sh_gemm_cfg), u32, u32]),
     "sh_gemm_ex": (i32, [u64, u64, u64, u32, u32, u32, u32, u32, u32, C.POINTER(sh_gemm_cfg), C.POINTER(sh_gemm_epi)]),
+    "sh_gemm_ex_wt": (i32, [u64, u64, u64, u32, u32, u32, u32, u32, u32, C.POINTER(sh_gemm_cfg), C.POINTER(sh_gemm_epi)]),
     "sh_gemm_plan": (i32, [u32, u32, u32, u32, C.POINTER(C.c_uint32)]),
     # row ops
     "sh_layernorm": (None, [u64, u64, u64, u64, u32, u32, u32, f32, u32]),

@@ -17,7 +17,7 @@ from oracle import lcg, refs
 from softhier_mlir_amd import data, shops
 
 pytestmark = pytest.mark.gpu
-NUM_TILE_CFGS = 33      # entries of the GEMM tile table (g_cfgs in sh_gemm.hip)
+NUM_TILE_CFGS = 55      # entries of the GEMM tile table (g_cfgs in sh_gemm.hip)
 A = shops.addr
 
 
@@ -105,7 +105,7 @@ def test_unsplit_tile_configs_store_identical_bits(lib, gpu, monkeypatch):
         Z = torch.zeros((M, N), dtype=torch.float16, device="cuda")
         assert lib.sh_gemm_ex(A(X), A(W), A(Z), M, N, K, K, N, N, None, None) == 0, shops.last_error()
         outs.append(to_np(Z).view(np.uint16))
-    # the direct-to-LDS kernels the cost model and the one-time timing choose between (configurations 6-32:
+    # the direct-to-LDS kernels the cost model and the one-time timing choose between (configurations 6-40:
     # 64-row to 256-row tiles, 64-k and 32-k slices, 4 and 8 wavefronts, LDS-staged or register epilogue) agree
     # bit for bit; so do the register-staged fallbacks (0-5) among themselves
     for lo, hi in ((6, NUM_TILE_CFGS), (0, 6)):
