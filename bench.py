@@ -64,12 +64,14 @@ def counted_traffic(op: str):
     return None
 
 
-def rowops_bandwidth(lib, torch, B: int, S: int, D: int, F: int, H: int, reps: int = 3) -> dict:
-    """Row ops at the batched shapes, cold: buffer sets rotated so that >= 512 MiB is touched between reuses
-    (MI355X Infinity Cache = 256 MiB). Algorithmic bytes: each input read once, the output written once."""
+def rowops_bandwidth(lib, torch, B: int, S: int, D: int, F: int, H: int, reps: int = 3, scale: int = 1) -> dict:
+    """Row ops at the batched shapes (scale = 1) or at `scale` times as many rows (the large-size table), cold:
+    buffer sets rotated so that >= 512 MiB is touched between reuses (MI355X Infinity Cache = 256 MiB).
+    Algorithmic bytes: each input read once, the output written once. The ceiling next to each op is the
+    library's own streaming copy (sh_dma_copy) of the output's bytes."""
     from softhier_mlir_amd import shops
     A = shops.addr
-    M = B * S
+    M = B * S * scale
     ops = {
         "layernorm": ((M, D), 2 * (2 * M * D + 2 * D)),
         "softmax": ((H * M, S), 2 * 2 * H * M * S),
@@ -106,7 +108,7 @@ def rowops_bandwidth(lib, torch, B: int, S: int, D: int, F: int, H: int, reps: i
                 lib.sh_transpose(A(y), A(x), r, c, c, r, shops.SH_ALL)
 
         def copy(x, y, b):
-            y.view(-1).copy_(x.view(-1))
+            lib.sh_dma_copy(A(y), A(x), 2 * r * c)
 
         def timed(fn):
             """(median us of single launches with events around each, us per launch of all sets back to back)"""
@@ -600,6 +602,7 @@ def main() -> int:
 
     extra = {} if args.no_extra else extra_configs(lib, torch, enc, x, lp, p, B, S, D, F, H)
     rowops = None if args.no_rowops else rowops_bandwidth(lib, torch, B, S, D, F, H)
+    rowops_large = None if args.no_rowops else rowops_bandwidth(lib, torch, B, S, D, F, H, reps=2, scale=16)
     cpu = None if args.no_cpu else cpu_baseline(B, S, D, F, H, p, xh)
 
     line = {
@@ -611,7 +614,8 @@ def main() -> int:
                    "seq_len": S, "d_model": D, "ffn": F, "heads": H, "layers": 1, "parallelism": "single GPU"},
         "mfma_frac_of_peak": round(value / PEAK_TFLOPS, 4),
         "eager_ms_per_step": round(eager_ms, 4) if eager_ms is not None else None,
-        "roofline": roofline, "breakdown": breakdown, **extra, "rowops": rowops, "cpu_baseline": cpu,
+        "roofline": roofline, "breakdown": breakdown, **extra, "rowops": rowops, "rowops_x16_rows": rowops_large,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     return 0

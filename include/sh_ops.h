@@ -111,6 +111,9 @@ void sh_add(uint64_t y, uint64_t a, uint64_t b, uint32_t rows, uint32_t cols, ui
 void sh_add_bias(uint64_t y, uint64_t x, uint64_t bias_row, uint32_t rows, uint32_t cols, uint32_t ld, uint32_t cluster); /* sh_ops.h:98 */
 void sh_scale(uint64_t y, uint64_t x, uint32_t rows, uint32_t cols, uint32_t ld, float s, uint32_t cluster);           /* sh_ops.h:99 */
 void sh_transpose(uint64_t dst, uint64_t src, uint32_t rows, uint32_t cols, uint32_t ld_src, uint32_t ld_dst, uint32_t cluster); /* sh_ops.h:100 bit-exact */
+/* sh_ops.h:218 (sh_l1.inc.c:58-61): 1-D copy of `bytes` from src to dst in HBM (non-overlapping), enqueued on the
+ * library stream (the reference's call is synchronous on its DM core; here it is ordered like every other op). */
+void sh_dma_copy(uint64_t dst, uint64_t src, uint32_t bytes);
 
 /* ---- fused attention (sh_ops.h:102-127, runtime/sh_attention.inc.c:55-243) ----------------------------
  * o = softmax(scale * q k^T) v per head; head h = columns [h*dh, (h+1)*dh). Flash-style on the GPU (online

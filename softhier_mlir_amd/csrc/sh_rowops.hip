@@ -43,6 +43,15 @@ __device__ __forceinline__ uint32_t slot_col(int lane, int u, int i) {
 // Makes q's value available at this point (an empty asm that reads and writes it), so its load is not moved later.
 __device__ __forceinline__ void pin4(uint4 &q) { __asm__ volatile("" : "+v"(q.x), "+v"(q.y), "+v"(q.z), "+v"(q.w)); }
 
+// 16-byte store; nt: nontemporal (streaming), used when the output is larger than the Infinity Cache, where no
+// consumer could find it cached anyway and plain stores only evict what it could use.
+typedef uint32_t sh_u4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void st16(void *p, uint4 v, bool nt) {
+    if (nt) __builtin_nontemporal_store((sh_u4v){v.x, v.y, v.z, v.w}, (sh_u4v *)p);
+    else *(uint4 *)p = v;
+}
+constexpr uint64_t kNtBytes = uint64_t(256) << 20;     // MI355X Infinity Cache
+
 template <int NCH>
 __device__ __forceinline__ void load_raw(const uint16_t *__restrict__ p, uint32_t cols, int lane, uint4 (&raw)[NCH]) {
 #pragma unroll
@@ -150,6 +159,96 @@ __global__ __launch_bounds__(256) void k_layernorm(uint16_t *y, const uint16_t *
     store_row<NCH, VEC>(y + row * ldy, cols, lane, v);
 }
 
+// LayerNorm with rows spread over LPR-lane groups (LPR = 32: two rows per wavefront; 64: one), NCH 16-byte
+// chunks per lane, each group walking rows row0, row0 + groups, ...: the next row's loads are issued before the
+// current row's statistics, so every group keeps two rows in flight; gamma and beta are loaded once per group.
+// Same two-pass statistics as k_layernorm (mean, then the mean of squared deviations, fp32).
+template <int LPR, int NCH>
+__global__ __launch_bounds__(256) void k_layernorm_p(uint16_t *y, const uint16_t *x, const uint16_t *gamma, const uint16_t *beta,
+                                                     uint32_t rows, uint32_t cols, uint64_t ldy, uint64_t ldx, float eps, uint32_t nt) {
+    constexpr int GPW = 64 / LPR;                         // row groups per wavefront
+    const int lane = threadIdx.x & 63, gl = lane % LPR;
+    const uint32_t group = (blockIdx.x * 4 + (threadIdx.x >> 6)) * GPW + lane / LPR;
+    const uint32_t ngroups = gridDim.x * 4 * GPW;
+    auto col = [&](int u) { return 8u * (uint32_t)(gl + LPR * u); };
+    float g[NCH][8], b[NCH][8];
+#pragma unroll
+    for (int u = 0; u < NCH; ++u) {
+        const bool ok = col(u) < cols;
+        float fg[8], fb[8];
+        unpack8(*(const uint4 *)(gamma + (ok ? col(u) : 0u)), fg);
+        unpack8(*(const uint4 *)(beta + (ok ? col(u) : 0u)), fb);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { g[u][i] = fg[i]; b[u][i] = fb[i]; }
+    }
+    uint32_t row = group;
+    uint4 cur[NCH];
+    const uint32_t r0 = row < rows ? row : 0u;
+#pragma unroll
+    for (int u = 0; u < NCH; ++u) cur[u] = *(const uint4 *)(x + r0 * ldx + (col(u) < cols ? col(u) : 0u));
+    const float inv_n = 1.f / (float)cols;
+    for (; row < rows; row += ngroups) {                  // the trip count differs between the groups of a wave
+        const uint32_t nrow = row + ngroups < rows ? row + ngroups : row;
+        uint4 nxt[NCH];
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) nxt[u] = *(const uint4 *)(x + nrow * ldx + (col(u) < cols ? col(u) : 0u));
+        float v[NCH][8];
+        float s = 0.f;
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) {
+            unpack8(cur[u], v[u]);
+            const bool ok = col(u) < cols;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { v[u][i] = ok ? v[u][i] : 0.f; s += v[u][i]; }
+        }
+#pragma unroll
+        for (int o = LPR / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+        const float mean = s * inv_n;
+        float q = 0.f;
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) {
+            const bool ok = col(u) < cols;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { const float d = ok ? v[u][i] - mean : 0.f; q += d * d; }
+        }
+#pragma unroll
+        for (int o = LPR / 2; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
+        const float rs = sh_fast_rsq(q * inv_n + eps);
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) {
+            if (col(u) >= cols) continue;
+            float o8[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o8[i] = (v[u][i] - mean) * rs * g[u][i] + b[u][i];
+            st16(y + row * ldy + col(u), pack8(o8), nt);
+        }
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) cur[u] = nxt[u];
+    }
+}
+
+// Streaming 1-D copy of n16 16-byte chunks: U chunks per thread, all loaded before any is stored, one pass per
+// thread (no grid-stride loop: a thread's next loads would queue behind its stores in the memory counter).
+template <int U>
+__global__ __launch_bounds__(256) void k_copy16(uint4 *__restrict__ dst, const uint4 *__restrict__ src, uint64_t n16, uint32_t nt) {
+    const uint64_t base = (uint64_t)blockIdx.x * 256u * U + threadIdx.x;
+    uint4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint64_t i = base + (uint64_t)u * 256u;
+        v[u] = src[i < n16 ? i : 0];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint64_t i = base + (uint64_t)u * 256u;
+        if (i < n16) st16(dst + i, v[u], nt);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_copy1(uint8_t *dst, const uint8_t *src, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256u) dst[i] = src[i];
+}
+
 // y = softmax(scale x) per row: exp(scale x - max) = 2^(c x - m), c = scale log2(e), m = max(c x).
 template <int NCH, bool VEC>
 __global__ __launch_bounds__(256) void k_softmax(uint16_t *y, const uint16_t *x, uint32_t rows, uint32_t cols, uint64_t ld, float c) {
@@ -201,7 +300,8 @@ __device__ __forceinline__ float group_sum(float v) {
 }
 
 template <int LPR, int RIT>
-__global__ __launch_bounds__(256) void k_softmax_narrow(uint16_t *y, const uint16_t *x, uint32_t rows, uint32_t cols, uint64_t ld, float c) {
+__global__ __launch_bounds__(256) void k_softmax_narrow(uint16_t *y, const uint16_t *x, uint32_t rows, uint32_t cols, uint64_t ld, float c,
+                                                        uint32_t nt) {
     constexpr int RPW = 64 / LPR;                     // rows per wavefront per group
     const int lane = threadIdx.x & 63, sub = lane / LPR, l = lane % LPR;
     const uint32_t row0 = (blockIdx.x * kRowWaves + (threadIdx.x >> 6)) * (uint32_t)(RPW * RIT) + (uint32_t)sub;
@@ -236,7 +336,7 @@ __global__ __launch_bounds__(256) void k_softmax_narrow(uint16_t *y, const uint1
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] *= inv;
         const uint32_t row = row0 + (uint32_t)(r * RPW);
-        if (row < rows && colok) *(uint4 *)(y + row * ld + c0) = pack8(v);
+        if (row < rows && colok) st16(y + row * ld + c0, pack8(v), nt);
     }
 }
 
@@ -295,7 +395,7 @@ __device__ __forceinline__ float ew(float a, float b, float s) {
 
 template <int OP, bool VEC>
 __global__ __launch_bounds__(256) void k_elementwise(uint16_t *y, const uint16_t *a, const uint16_t *b, uint32_t rows,
-                                                     uint32_t per_row, ShDiv div, uint64_t ld, float s, uint32_t items) {
+                                                     uint32_t per_row, ShDiv div, uint64_t ld, float s, uint32_t items, uint32_t nt) {
     constexpr int U = 4;   // items per thread, issued together
     const uint32_t base = blockIdx.x * (256u * U) + threadIdx.x;
     (void)rows;
@@ -322,7 +422,7 @@ __global__ __launch_bounds__(256) void k_elementwise(uint16_t *y, const uint16_t
             if (!ok[u]) continue;
             if (OP == OP_GELU) {                      // on fp16 pairs, as the GEMM epilogue does
                 const uint4 q = ra[u];
-                *(uint4 *)(y + off[u]) = make_uint4(sh_gelu_u32(q.x), sh_gelu_u32(q.y), sh_gelu_u32(q.z), sh_gelu_u32(q.w));
+                st16(y + off[u], make_uint4(sh_gelu_u32(q.x), sh_gelu_u32(q.y), sh_gelu_u32(q.z), sh_gelu_u32(q.w)), nt);
                 continue;
             }
             float fa[8], fb[8];
@@ -330,7 +430,7 @@ __global__ __launch_bounds__(256) void k_elementwise(uint16_t *y, const uint16_t
             unpack8(rb[u], fb);
 #pragma unroll
             for (int i = 0; i < 8; ++i) fa[i] = ew<OP>(fa[i], fb[i], s);
-            *(uint4 *)(y + off[u]) = pack8(fa);
+            st16(y + off[u], pack8(fa), nt);
         }
         return;
     }
@@ -354,7 +454,7 @@ __global__ __launch_bounds__(256) void k_elementwise(uint16_t *y, const uint16_t
 
 // dst[cols, rows] = src[rows, cols]^T, 128 x 128 tile per block, 8 x 8 blocks per thread.
 __global__ __launch_bounds__(256) void k_transpose8(uint16_t *dst, const uint16_t *src, uint32_t rows, uint32_t cols,
-                                                    uint64_t lds, uint64_t ldd) {
+                                                    uint64_t lds, uint64_t ldd, uint32_t nt) {
     __shared__ uint4 tile[128 * 16];                      // [dst row local][16-byte chunk ^ swizzle]
     const int t = threadIdx.x;
     const uint32_t tr = blockIdx.y * 128u, tc = blockIdx.x * 128u;
@@ -385,7 +485,7 @@ __global__ __launch_bounds__(256) void k_transpose8(uint16_t *dst, const uint16_
     for (int k = 0; k < 8; ++k) {
         const int R = (t >> 4) + 16 * k;
         const uint32_t drow = tc + R, dcol = tr + 8u * C;
-        if (drow < cols && dcol < rows) *(uint4 *)(dst + (uint64_t)drow * ldd + dcol) = tile[R * 16 + (C ^ ((R >> 3) & 15))];
+        if (drow < cols && dcol < rows) st16(dst + (uint64_t)drow * ldd + dcol, tile[R * 16 + (C ^ ((R >> 3) & 15))], nt);
     }
 }
 
@@ -431,8 +531,22 @@ void launch_layernorm(uint64_t y, uint64_t x, uint64_t g, uint64_t b, uint32_t r
         sh_launch_ok("sh_layernorm");
         return;
     }
-    const dim3 grid(sh_cdiv(rows, kRowWaves)), block(256);
     const bool vec = vec_ok(cols, {y, x, g, b}, {ldy, ldx});
+    if (vec && cols <= 4096) {
+        // row groups of 32 lanes up to 1024 columns (two rows per wavefront), else 64; one row per group while
+        // that keeps up to 16 blocks per CU, beyond it rows are walked in turn (two in flight per group)
+        const uint32_t lpr = cols <= 1024 ? 32 : 64, gpb = 4 * (64 / lpr);
+        const uint32_t cap = (uint32_t)(sh_num_cus() > 0 ? sh_num_cus() : 256) * 16;
+        const dim3 g(std::max<uint32_t>(1, std::min<uint32_t>(sh_cdiv(rows, gpb), cap)));
+        const uint32_t nt = (uint64_t)rows * cols * 2 >= kNtBytes;
+#define SH_LNP(L, N) hipLaunchKernelGGL((k_layernorm_p<L, N>), g, dim3(256), 0, st, Y, X, G, B, rows, cols, (uint64_t)ldy, (uint64_t)ldx, eps, nt)
+        if (lpr == 32) { if (cols <= 256) SH_LNP(32, 1); else if (cols <= 512) SH_LNP(32, 2); else if (cols <= 768) SH_LNP(32, 3); else SH_LNP(32, 4); }
+        else { if (cols <= 2048) SH_LNP(64, 4); else if (cols <= 3072) SH_LNP(64, 6); else SH_LNP(64, 8); }
+#undef SH_LNP
+        sh_launch_ok("sh_layernorm");
+        return;
+    }
+    const dim3 grid(sh_cdiv(rows, kRowWaves)), block(256);
 #define SH_LN(N) do { if (vec) hipLaunchKernelGGL((k_layernorm<N, true>), grid, block, 0, st, Y, X, G, B, rows, cols, (uint64_t)ldy, (uint64_t)ldx, eps); \
                       else hipLaunchKernelGGL((k_layernorm<N, false>), grid, block, 0, st, Y, X, G, B, rows, cols, (uint64_t)ldy, (uint64_t)ldx, eps); } while (0)
     if (cols <= 512) SH_LN(1); else if (cols <= 1024) SH_LN(2); else if (cols <= 2048) SH_LN(4); else if (cols <= 4096) SH_LN(8); else SH_LN(16);
@@ -450,8 +564,9 @@ void launch_elementwise(int op, uint64_t y, uint64_t a, uint64_t b, uint32_t row
     const ShDiv div = sh_make_div(per_row);
     const dim3 grid(sh_cdiv(items, 256u * 4u)), block(256);
     uint16_t *Y = (uint16_t *)y; const uint16_t *A = (const uint16_t *)a, *B = (const uint16_t *)b;
-#define SH_EW(OP) do { if (vec) hipLaunchKernelGGL((k_elementwise<OP, true>), grid, block, 0, st, Y, A, B, rows, per_row, div, (uint64_t)ld, s, items); \
-                       else hipLaunchKernelGGL((k_elementwise<OP, false>), grid, block, 0, st, Y, A, B, rows, per_row, div, (uint64_t)ld, s, items); } while (0)
+    const uint32_t nt = (uint64_t)rows * cols * 2 >= kNtBytes;
+#define SH_EW(OP) do { if (vec) hipLaunchKernelGGL((k_elementwise<OP, true>), grid, block, 0, st, Y, A, B, rows, per_row, div, (uint64_t)ld, s, items, nt); \
+                       else hipLaunchKernelGGL((k_elementwise<OP, false>), grid, block, 0, st, Y, A, B, rows, per_row, div, (uint64_t)ld, s, items, nt); } while (0)
     switch (op) {
         case OP_GELU: SH_EW(OP_GELU); break;
         case OP_ADD: SH_EW(OP_ADD); break;
@@ -607,6 +722,26 @@ void sh_layernorm_ld(uint64_t y, uint64_t x, uint64_t gamma, uint64_t beta, uint
     launch_layernorm(y, x, gamma, beta, rows, cols, ldy, ldx, eps);
 }
 
+// HBM -> HBM 1-D copy of `bytes` (reference sh_l1.inc.c:58-61, an iDMA 1-D transfer), stream-ordered on the
+// library stream. 16-byte-aligned ends take the streaming chunk kernel; anything else a byte loop.
+void sh_dma_copy(uint64_t dst, uint64_t src, uint32_t bytes) {
+    if (bytes == 0) return;
+    if (!dst || !src) { sh_set_error(-1, "[sh_dma_copy] NULL address"); return; }
+    sh_ensure_init();
+    hipStream_t st = sh_stream();
+    const uint32_t cap = (uint32_t)(sh_num_cus() > 0 ? sh_num_cus() : 256) * 8;
+    if ((dst | src | bytes) % 16 == 0) {
+        constexpr int U = 8;
+        const uint64_t n16 = bytes / 16;
+        const uint32_t blocks = (uint32_t)((n16 + 256 * U - 1) / (256 * U));
+        hipLaunchKernelGGL(k_copy16<U>, dim3(blocks), dim3(256), 0, st, (uint4 *)dst, (const uint4 *)src, n16, (uint32_t)(bytes >= kNtBytes));
+    } else {
+        const uint32_t blocks = (uint32_t)std::min<uint64_t>((bytes + 255) / 256, cap);
+        hipLaunchKernelGGL(k_copy1, dim3(blocks), dim3(256), 0, st, (uint8_t *)dst, (const uint8_t *)src, (uint64_t)bytes);
+    }
+    sh_launch_ok("sh_dma_copy");
+}
+
 void sh_softmax_rows(uint64_t y, uint64_t x, uint32_t rows, uint32_t cols, uint32_t ld, float scale, uint32_t) {
     if (!check_args("sh_softmax_rows", y, x, rows, cols, ld)) return;
     hipStream_t st = sh_stream();
@@ -622,9 +757,10 @@ void sh_softmax_rows(uint64_t y, uint64_t x, uint32_t rows, uint32_t cols, uint3
         constexpr int RIT = 4;
         const uint32_t lpr = cols <= 64 ? 8 : cols <= 128 ? 16 : 32;
         const dim3 g(sh_cdiv(rows, kRowWaves * (64 / lpr) * RIT));
-        if (lpr == 8) hipLaunchKernelGGL((k_softmax_narrow<8, RIT>), g, dim3(256), 0, st, Y, X, rows, cols, (uint64_t)ld, c);
-        else if (lpr == 16) hipLaunchKernelGGL((k_softmax_narrow<16, RIT>), g, dim3(256), 0, st, Y, X, rows, cols, (uint64_t)ld, c);
-        else hipLaunchKernelGGL((k_softmax_narrow<32, RIT>), g, dim3(256), 0, st, Y, X, rows, cols, (uint64_t)ld, c);
+        const uint32_t nt = (uint64_t)rows * cols * 2 >= kNtBytes;
+        if (lpr == 8) hipLaunchKernelGGL((k_softmax_narrow<8, RIT>), g, dim3(256), 0, st, Y, X, rows, cols, (uint64_t)ld, c, nt);
+        else if (lpr == 16) hipLaunchKernelGGL((k_softmax_narrow<16, RIT>), g, dim3(256), 0, st, Y, X, rows, cols, (uint64_t)ld, c, nt);
+        else hipLaunchKernelGGL((k_softmax_narrow<32, RIT>), g, dim3(256), 0, st, Y, X, rows, cols, (uint64_t)ld, c, nt);
         sh_launch_ok("sh_softmax_rows");
         return;
     }
@@ -666,7 +802,8 @@ void sh_transpose(uint64_t dst, uint64_t src, uint32_t rows, uint32_t cols, uint
     const bool vec = rows % 8 == 0 && vec_ok(cols, {dst, src}, {ld_src, ld_dst});
     if (vec) {
         const dim3 grid(sh_cdiv(cols, 128), sh_cdiv(rows, 128));
-        hipLaunchKernelGGL(k_transpose8, grid, dim3(256), 0, st, D, S, rows, cols, (uint64_t)ld_src, (uint64_t)ld_dst);
+        hipLaunchKernelGGL(k_transpose8, grid, dim3(256), 0, st, D, S, rows, cols, (uint64_t)ld_src, (uint64_t)ld_dst,
+                           (uint32_t)((uint64_t)rows * cols * 2 >= kNtBytes));
     } else {
         const dim3 grid(sh_cdiv(cols, 32), sh_cdiv(rows, 32));
         hipLaunchKernelGGL(k_transpose1, grid, dim3(256), 0, st, D, S, rows, cols, (uint64_t)ld_src, (uint64_t)ld_dst);

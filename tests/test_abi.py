@@ -191,3 +191,11 @@ def test_gemm_plan_reports_the_launched_split_count(lib):
     for K in (64, 192, 256, 720, 768, 3072):
         for s in range(1, 20):
             assert plan(256, 768, K, s) == launched(K, s), (K, s)
+
+
+def test_dma_copy_argument_errors_without_gpu(lib):
+    lib.sh_last_error()
+    lib.sh_dma_copy(0, 1 << 20, 64)                    # NULL destination: refused before any HIP call
+    assert lib.sh_last_error() == -1
+    lib.sh_dma_copy(0, 0, 0)                           # nothing to copy: no error
+    assert lib.sh_last_error() == 0

@@ -204,3 +204,17 @@ def test_softmax_short_rows(lib, gpu, cols, scale):
     xi = to_np(X)
     assert (xi[:, :cols].view(np.uint16) == y[:, :cols].view(np.uint16)).all()
     assert (xi[:, cols:].view(np.uint16) == x[:, cols:].view(np.uint16)).all()
+
+
+@pytest.mark.parametrize("nbytes,so,do", [(16 << 20, 0, 0), (4096 + 48, 16, 32), (1000003, 3, 5), (1, 0, 7)])
+def test_dma_copy_moves_every_byte(lib, gpu, nbytes, so, do):
+    """sh_dma_copy (sh_ops.h:218): a 1-D copy of exactly `bytes`, aligned (streaming 16-byte path) or not (byte
+    path), leaving the bytes around the destination range untouched."""
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(5)
+    src = torch.randint(0, 256, (nbytes + so + 64,), dtype=torch.uint8, device="cuda", generator=g)
+    dst = torch.full((nbytes + do + 64,), 0xA5, dtype=torch.uint8, device="cuda")
+    lib.sh_dma_copy(shops.addr(dst, do), shops.addr(src, so), nbytes)
+    torch.cuda.synchronize()
+    assert torch.equal(dst[do:do + nbytes], src[so:so + nbytes])
+    assert (dst[:do] == 0xA5).all() and (dst[do + nbytes:] == 0xA5).all()
