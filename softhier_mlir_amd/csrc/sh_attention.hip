@@ -36,7 +36,22 @@ struct AttnArgs {
     float c;                        // scale * log2(e)
     const uint16_t *tok;            // token classes of the S positions (sh_ops.h:277-282), or null: no mask
     uint32_t grp;                   // query heads per key/value head (GQA); 1 for plain multi-head attention
+    uint32_t xcds;                  // > 1: the query blocks of one head run on one XCD (see attn_item)
 };
+
+// Work item of a workgroup: (query block, head, sequence). Dispatch deals workgroups round-robin over the XCDs,
+// and every query block of a head reads the same K / V, so with `xcds` > 1 the flat block id L is remapped to
+// keep a head's query blocks on one XCD, back to back (L % X picks the XCD, L / X the position in its queue),
+// and the second block's K / V reads hit that XCD's L2. Needs (heads x sequences) % X == 0.
+__device__ __forceinline__ void attn_item(const AttnArgs &a, uint32_t &qb, uint32_t &h, uint32_t &b) {
+    qb = blockIdx.x; h = blockIdx.y; b = blockIdx.z;
+    if (a.xcds > 1) {
+        const uint32_t gx = gridDim.x, gy = gridDim.y;
+        const uint32_t L = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+        const uint32_t j = L / a.xcds, hb = (j / gx) * a.xcds + L % a.xcds;
+        qb = j % gx; h = hb % gy; b = hb / gy;
+    }
+}
 constexpr uint32_t kLlmPad = 0xFFFFu;   // SH_LLM_PAD: a padding position
 
 template <int DH>
@@ -406,6 +421,14 @@ __global__ __launch_bounds__(256) void k_flash_dma(AttnArgs a) {
     }
 }
 
+// Profiling stamp: the 100 MHz real-time counter into slot i of the stamp buffer (a vector store).
+__device__ __forceinline__ void attn_stamp(uint64_t *stamp, bool on, int i) {
+    if (on) {
+        const uint64_t t = __builtin_amdgcn_s_memrealtime();
+        __builtin_nontemporal_store(t, stamp + i);
+    }
+}
+
 // Two-pass variant of k_flash_dma for dh 64 / 128 (the default for aligned heads). On CDNA the softmax
 // VALU work, not the MFMA work, bounds attention, so the row maximum is found first in a cheap pass over the
 // keys (S^T = K . Q^T on MFMA, then max3 only); the second pass recomputes the scores and, with the final
@@ -422,7 +445,7 @@ __global__ __launch_bounds__(256) void k_flash_dma(AttnArgs a) {
 // Occupancy: with a 2-stage ring (32 KB of LDS) a dh = 64 workgroup fits in 168 registers per lane, so three
 // workgroups share a CU (12 waves); the encoder's 768 (sequence, head, query block) workgroups then run in one round.
 template <int DH, int NST, bool MASK, bool FOLD>
-__global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a) {
+__global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a, uint64_t *stamp) {
     constexpr int DC = DH / 8, NS = DH / 16, DT = DH / 32;
     constexpr int KCH = KB * DC;                     // 16-byte chunks per K (or V) block
     constexpr int KR = KCH / 256;                    // DMA rounds per thread per block, per operand
@@ -432,15 +455,22 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a) {
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = lane >> 5, r32 = lane & 31;
     const int q4 = lane >> 4, iq = lane & 15;
-    const uint32_t b = blockIdx.z, h = blockIdx.y;
+    uint32_t qb, h, b;
+    attn_item(a, qb, h, b);
     const uint32_t S = a.S;
     const uint16_t *Q = a.q + b * a.bsq + (uint64_t)h * DH;
     const uint16_t *Kp = a.k + b * a.bsk + (uint64_t)(h / a.grp) * DH;
     const uint16_t *Vp = a.v + b * a.bsv + (uint64_t)(h / a.grp) * DH;
     uint16_t *O = a.o + b * a.bso + (uint64_t)h * DH;
-    const uint32_t qw0 = blockIdx.x * QPB + wave * QPW, myq = qw0 + r32;
+    const uint32_t qw0 = qb * QPB + wave * QPW, myq = qw0 + r32;
     const uint32_t nkb = (S + KB - 1) / KB;
     const bool ragged = S % KB != 0;                 // the last key block is partial
+    // stamps (profile): 0-2 start, 3-4 pass 1 done (maximum known), 5 pass 2 done, 6 stored; 7 first workgroup
+    const bool last = stamp && t == 0 && qb == gridDim.x - 1 && h == gridDim.y - 1 && b == gridDim.z - 1;
+    attn_stamp(stamp, stamp && t == 0 && qb == 0 && h == 0 && b == 0, 7);
+    attn_stamp(stamp, last, 0);
+    attn_stamp(stamp, last, 1);
+    attn_stamp(stamp, last, 2);
     // token mask (MASK): key j is allowed for this lane's query iff tok[j] <= tok[query]; a padding query (or
     // one with no allowed key, found in pass 1) averages V uniformly over the S keys
     const uint32_t tq = MASK ? (myq < S ? (uint32_t)a.tok[myq] : kLlmPad) : 0u;
@@ -546,6 +576,8 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a) {
     }
     sh_wait_vmcnt<0>();                            // the ring is idle before pass 2 refills it
     __syncthreads();
+    attn_stamp(stamp, last, 3);
+    attn_stamp(stamp, last, 4);
 
     // ---- pass 2: p = 2^(c s - m); O^T += V^T P^T; l += 1^T P^T ----
     sh_f16v oacc[DT];
@@ -597,9 +629,10 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a) {
     }
     sh_wait_vmcnt<0>();      // clamped tail loads land before the LDS is reused below
     __syncthreads();
+    attn_stamp(stamp, last, 5);
 
     const float inv = 1.f / lacc[0];                 // every row of the ones product holds this query's l
-    uint16_t *so = (uint16_t *)smem + wave * (QPW * DH);
+    uint16_t *so = (uint16_t *)(smem + 2 * KCH) + wave * (QPW * DH);     // this wave's query rows, now free
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -610,13 +643,15 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a) {
             const int ch = (d0 >> 3) ^ (r32 & 7);
             *(uint2 *)(so + r32 * DH + ch * 8 + (d0 & 7)) = make_uint2(lo, hi);
         }
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0xC07F);              // lgkmcnt(0): the wave's own staging is complete
+    __builtin_amdgcn_wave_barrier();
     for (int c = lane; c < QPW * DC; c += 64) {
         const int row = c / DC, ch = c % DC;
         const uint32_t qq = qw0 + row;
         if (qq >= S) continue;
         *(uint4 *)(O + (uint64_t)qq * a.ldo + 8 * ch) = ((const uint4 *)so)[row * DC + (ch ^ (row & 7))];
     }
+    attn_stamp(stamp, last, 6);
 }
 
 // Any dh: one 256-thread block per (query, head, sequence); scores of the row in LDS (S <= 16384).
@@ -665,7 +700,11 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
 }
 
 // ---- host side ---------------------------------------------------------------------------------------
-struct AttnProfile { hipEvent_t e0 = nullptr, e1 = nullptr; bool valid = false; uint32_t entry_ns = 0; };
+// stamps: device buffer of 8 s_memrealtime values written by the last stamped launch (see attn_stamp)
+struct AttnProfile {
+    hipEvent_t e0 = nullptr, e1 = nullptr; bool valid = false; uint32_t entry_ns = 0;
+    uint64_t *stamps = nullptr; bool stamped = false;       // stamped: the last launch's kernel wrote the stamps
+};
 AttnProfile g_prof;
 
 uint32_t l1_bytes_q(uint32_t S, uint32_t dh, uint32_t sq) {     // sh_attention.inc.c:43-51 (uint32 arithmetic)
@@ -691,10 +730,20 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
     if (B == 0 || S == 0 || H == 0 || dh == 0) return 0;
     if (H > 65535 || B > 65535) { sh_set_error(-1, "[sh_attention] H=%u or B=%u above 65535", H, B); return -1; }
     AttnArgs a{(const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)v, (uint16_t *)o,
-               ldq, ldk, ldv, ldo, bsq, bsk, bsv, bso, S, dh, scale * 1.4426950408889634f, (const uint16_t *)tok, grp};
+               ldq, ldk, ldv, ldo, bsq, bsk, bsv, bso, S, dh, scale * 1.4426950408889634f, (const uint16_t *)tok, grp, 1};
+    {
+        static const int remap = [] { const char *e = getenv("SH_ATTN_XCD"); return (e && *e) ? atoi(e) : 1; }();
+        const uint32_t X = (uint32_t)sh_num_xcds();
+        if (remap && X > 1 && sh_cdiv(S, QPB) > 1 && ((uint64_t)H * B) % X == 0) a.xcds = X;
+    }
     hipStream_t st = sh_stream();
     if (!g_prof.e0) {
         if (!sh_hip_ok(hipEventCreate(&g_prof.e0), "hipEventCreate") || !sh_hip_ok(hipEventCreate(&g_prof.e1), "hipEventCreate")) return SH_EHIP;
+    }
+    if (stamp && !g_prof.stamps) {
+        hipStreamCaptureStatus cs0 = hipStreamCaptureStatusNone;
+        const bool cap0 = hipStreamIsCapturing(st, &cs0) == hipSuccess && cs0 != hipStreamCaptureStatusNone;
+        if (!cap0 && !sh_hip_ok(hipMalloc(&g_prof.stamps, 8 * sizeof(uint64_t)), "attention stamps hipMalloc")) return SH_EHIP;
     }
     g_prof.entry_ns = 0;
     // The kernel's start / end timestamps come with its dispatch (no separate event packets on the stream).
@@ -702,9 +751,17 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     const bool capturing = hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
     const bool events = stamp && !capturing;
+    g_prof.stamped = false;
     auto go = [&](auto kern, dim3 grid, size_t shm) {
         if (!events) hipLaunchKernelGGL(kern, grid, dim3(256), (uint32_t)shm, st, a);
         else hipExtLaunchKernelGGL(kern, grid, dim3(256), (uint32_t)shm, st, g_prof.e0, g_prof.e1, 0u, a);
+    };
+    // kernels that also write the phase stamps of their last workgroup (only on a stamped, uncaptured call)
+    uint64_t *sp = events ? g_prof.stamps : nullptr;
+    auto go2 = [&](auto kern, dim3 grid, size_t shm) {
+        g_prof.stamped = sp != nullptr;
+        if (!events) hipLaunchKernelGGL(kern, grid, dim3(256), (uint32_t)shm, st, a, sp);
+        else hipExtLaunchKernelGGL(kern, grid, dim3(256), (uint32_t)shm, st, g_prof.e0, g_prof.e1, 0u, a, sp);
     };
     const bool vec = dh % 8 == 0 && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 8 == 0 &&
                      bsq % 8 == 0 && bsk % 8 == 0 && bsv % 8 == 0 && bso % 8 == 0 &&
@@ -713,16 +770,16 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
     const dim3 grid(sh_cdiv(S, QPB), H, B);
     const bool fold = fabsf(a.c) <= 1.f;            // c q stays in fp16 range
     if (tok && (dh == 64 || dh == 128) && vec) {
-        if (dh == 64) fold ? go(k_flash2<64, 2, true, true>, grid, 0) : go(k_flash2<64, 2, true, false>, grid, 0);
-        else fold ? go(k_flash2<128, 2, true, true>, grid, 0) : go(k_flash2<128, 2, true, false>, grid, 0);
+        if (dh == 64) fold ? go2(k_flash2<64, 2, true, true>, grid, 0) : go2(k_flash2<64, 2, true, false>, grid, 0);
+        else fold ? go2(k_flash2<128, 2, true, true>, grid, 0) : go2(k_flash2<128, 2, true, false>, grid, 0);
     } else if (tok) {
         if (S > 16384) { sh_set_error(-1, "[sh_attention] masked heads with dh=%u support S <= 16384", dh); return -1; }
         static bool attr_m = false;
         if (!attr_m) { (void)hipFuncSetAttribute((const void *)k_attn_rows, hipFuncAttributeMaxDynamicSharedMemorySize, 16384 * 4); attr_m = true; }
         go(k_attn_rows, dim3(S, H, B), S * sizeof(float));
     } else if ((dh == 64 || dh == 128) && vec && impl == 0) {
-        if (dh == 64) fold ? go(k_flash2<64, 2, false, true>, grid, 0) : go(k_flash2<64, 2, false, false>, grid, 0);
-        else fold ? go(k_flash2<128, 2, false, true>, grid, 0) : go(k_flash2<128, 2, false, false>, grid, 0);
+        if (dh == 64) fold ? go2(k_flash2<64, 2, false, true>, grid, 0) : go2(k_flash2<64, 2, false, false>, grid, 0);
+        else fold ? go2(k_flash2<128, 2, false, true>, grid, 0) : go2(k_flash2<128, 2, false, false>, grid, 0);
     } else if ((dh == 64 || dh == 128) && vec && impl == 1) {
         if (dh == 64) go(k_flash_dma<64, 4>, grid, 0);
         else go(k_flash_dma<128, 2>, grid, 0);
@@ -826,11 +883,18 @@ int sh_attention_gqa(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t S,
     return run(q, k, v, o, 1, S, dh, H, ldq, ldk, ldv, ldo, 0, 0, 0, 0, scale, tok, H / Hkv);
 }
 
+// ns since the first workgroup of the last stamped launch started (phase 7 = 0): 0 the last workgroup's start,
+// 1-2 its operands staged, 3 scores (two-pass kernel: pass 1, the maximum), 4 softmax, 5 P.V, 6 stored. Kernels
+// without stamps report only 6, as the launch's event time.
 uint32_t sh_attention_profile(uint32_t, uint32_t, uint32_t phase) {
     if (!g_prof.valid) return 0;
     phase &= 7;
-    if (phase != 6) return 0;      // entry (7), start (0) and the unsplit phases 1..5 read 0
     if (hipEventSynchronize(g_prof.e1) != hipSuccess) return 0;
+    uint64_t st[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (g_prof.stamped && hipMemcpy(st, g_prof.stamps, sizeof st, hipMemcpyDeviceToHost) == hipSuccess && st[7] && st[6] >= st[7]) {
+        return phase == 7 ? 0u : (uint32_t)((st[phase] >= st[7] ? st[phase] - st[7] : 0) * 10u);   // 100 MHz counter
+    }
+    if (phase != 6) return 0;
     float ms = 0.f;
     if (hipEventElapsedTime(&ms, g_prof.e0, g_prof.e1) != hipSuccess) return 0;
     return (uint32_t)((double)ms * 1e6 + 0.5);

@@ -121,3 +121,23 @@ def test_profile_reports_the_kernel_time(lib, gpu):
     assert lib.sh_attention(A(q), A(q), A(q), A(O), S, D, H, D, D, D, D, 0.125, ALL) == 0
     lib.sh_barrier_global()
     assert lib.sh_attention_profile(S, 64, 6) > lib.sh_attention_profile(S, 64, 7) == 0
+
+
+@pytest.mark.parametrize("S", [256, 1024])
+def test_profile_phase_stamps_are_monotone(lib, gpu, S):
+    """sh_attention_profile (reference sh_attention.inc.c:67-76, sh_ops.h:124-127): the last workgroup's stamps in
+    ns from the first workgroup's start (phase 7 = 0): start (0) <= operands staged (1, 2) <= scores (3; the
+    two-pass kernel of S = 1024: pass 1) <= softmax (4) <= P.V (5; pass 2) <= stored (6). A batched call leaves no
+    stamps (every phase reads 0)."""
+    D, H = 768, 12
+    q = to_dev(data.normal((S, D), 3))
+    O = _zeros(S, D)
+    assert lib.sh_attention(A(q), A(q), A(q), A(O), S, D, H, D, D, D, D, 0.125, ALL) == 0
+    lib.sh_barrier_global()
+    ph = [lib.sh_attention_profile(S, 64, p) for p in range(8)]
+    assert ph[7] == 0
+    assert ph[0] <= ph[1] <= ph[2] <= ph[3] <= ph[4] <= ph[5] <= ph[6], ph
+    assert 0 < ph[6] < 10_000_000 and ph[6] > ph[0], ph
+    assert lib.sh_attention_batched(A(q), A(q), A(q), A(O), 1, S, D, H, D, D, D, D, 0, 0, 0, 0, 0.125, 0) == 0
+    lib.sh_barrier_global()
+    assert all(lib.sh_attention_profile(S, 64, p) == 0 for p in range(8))
