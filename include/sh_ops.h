@@ -111,6 +111,15 @@ void sh_add(uint64_t y, uint64_t a, uint64_t b, uint32_t rows, uint32_t cols, ui
 void sh_add_bias(uint64_t y, uint64_t x, uint64_t bias_row, uint32_t rows, uint32_t cols, uint32_t ld, uint32_t cluster); /* sh_ops.h:98 */
 void sh_scale(uint64_t y, uint64_t x, uint32_t rows, uint32_t cols, uint32_t ld, float s, uint32_t cluster);           /* sh_ops.h:99 */
 void sh_transpose(uint64_t dst, uint64_t src, uint32_t rows, uint32_t cols, uint32_t ld_src, uint32_t ld_dst, uint32_t cluster); /* sh_ops.h:100 bit-exact */
+/* No counterpart in the reference (LayerNorm folded into the next GEMM, sh_gemm_epi.ln_stats): per row of x, the
+ * mean and 1 / sqrt(biased variance + eps) as fp32 pairs into stats [rows][2], the statistics sh_layernorm
+ * computes (two passes over the row in fp32). */
+void sh_row_stats(uint64_t stats, uint64_t x, uint32_t rows, uint32_t cols, uint32_t ld, float eps);
+/* No counterpart in the reference: the weight side of the fold for z = LN(x) . W + b, W [K, N] (ldw):
+ * wp = r16(gamma_k W[k][n]) (fp16, leading dim ldwp), c[n] = sum_k wp[k][n] (fp32), d[n] = sum_k beta_k W[k][n]
+ * + b[n] (fp32; bias = 0: none). gamma, beta, bias: fp16 rows. Run once per weight. */
+void sh_ln_fold(uint64_t wp, uint64_t c, uint64_t d, uint64_t w, uint64_t gamma, uint64_t beta, uint64_t bias,
+                uint32_t K, uint32_t N, uint32_t ldw, uint32_t ldwp);
 /* sh_ops.h:218 (sh_l1.inc.c:58-61): 1-D copy of `bytes` from src to dst in HBM (non-overlapping), enqueued on the
  * library stream (the reference's call is synchronous on its DM core; here it is ordered like every other op). */
 void sh_dma_copy(uint64_t dst, uint64_t src, uint32_t bytes);
@@ -214,6 +223,12 @@ typedef struct {
     uint64_t residual;    /* 0: none */
     uint32_t ldr;         /* leading dim of residual (elements) */
     uint32_t splits;      /* 1: none; 0: library choice */
+    /* LayerNorm folded into the GEMM (0: off). With X the raw rows and W' = diag(gamma) W, c = 1^T W' and
+     * d = beta^T W + b from sh_ln_fold, the product p = X . W' becomes z = r p - r mu c + d before the rest of the
+     * chain (act, residual), which is LN(X) . W + b; ln_stats: fp32 [M][2] (mu, r) rows from sh_row_stats, ln_c:
+     * fp32 row of N, and the bias must then be the fp32 row d (SH_BIAS_FP32). Rounded once to fp16. */
+    uint64_t ln_stats;
+    uint64_t ln_c;
 } sh_gemm_epi;
 int sh_gemm_ex(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
                uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg, const sh_gemm_epi *epi);

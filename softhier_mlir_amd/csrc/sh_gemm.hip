@@ -52,7 +52,16 @@ struct GemmArgs {
     uint32_t tiles_m, tiles_n, splits;
     uint32_t accumulate, bias_fp32, act;
     uint32_t xcd_groups;         // > 1: XCD-aware block remap with this many XCDs (requires divisibility)
+    const float *ln_stats;       // LayerNorm fold (or null): (mu, r) per row, fp32 [M][2] ...
+    const float *ln_c;           // ... and c per column (fp32 [N]); the fp32 bias row is then d
 };
+
+// LayerNorm folded into the product (sh_gemm_epi.ln_stats): p -> r p - (r mu) c + d in fp32, before the fp16
+// rounding; the bias (d) is part of this step, so the chain below skips it.
+__device__ __forceinline__ float ln_apply(const GemmArgs &a, float p, uint32_t gm, uint32_t gn) {
+    const float2 st = ((const float2 *)a.ln_stats)[gm];
+    return fmaf(st.y, p, fmaf(-(st.x * st.y), a.ln_c[gn], ((const float *)a.bias)[gn]));
+}
 
 // Logical tile of block b -> (split, tile row, tile column). Dispatch deals workgroups round-robin over the
 // XCDs, so block b becomes logical index (b % X) (T / X) + b / X: each XCD walks a contiguous run of the
@@ -106,7 +115,7 @@ __device__ __forceinline__ uint32_t comp(const uint4 &q, int i) { return i == 0 
 __device__ __forceinline__ uint16_t epi_chain(const GemmArgs &a, uint16_t p, uint32_t gm, uint32_t gn) {
     float v = sh_dev_h2f(p);
     if (a.accumulate) v = sh_dev_h2f(sh_dev_f2h(v + sh_dev_h2f(a.z[(uint64_t)gm * a.ldz + gn])));
-    if (a.bias) {
+    if (a.bias && !a.ln_stats) {
         const float b = a.bias_fp32 ? ((const float *)a.bias)[gn] : sh_dev_h2f(((const uint16_t *)a.bias)[gn]);
         v = sh_dev_h2f(sh_dev_f2h(v + b));
     }
@@ -124,7 +133,7 @@ __device__ __forceinline__ uint4 epi_chain8(const GemmArgs &a, uint4 q, const ui
 #pragma unroll
         for (int p = 0; p < 4; ++p) w[p] = sh_hadd2(comp(zo, p), w[p]);
     }
-    if (a.bias) {
+    if (a.bias && !a.ln_stats) {
         if (a.bias_fp32) {
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
@@ -779,6 +788,36 @@ __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
     return (uint32_t)sh_dev_f2h(lo) | ((uint32_t)sh_dev_f2h(hi) << 16);
 }
 
+// The LayerNorm fold on a wavefront's Z^T accumulators (block (i, j) of lane l: row mrow + 32 i + l % 32,
+// columns ncol + 32 j + 8 q + 4 g + e in register 4 q + e), in place, before they are rounded.
+template <int FM, int FN>
+__device__ __forceinline__ void ln_fold_zt(const GemmArgs &a, sh_f16v (&acc)[FM][FN], uint32_t mrow, uint32_t ncol) {
+    const int lane = threadIdx.x & 63, g = lane >> 5, r32 = lane & 31;
+    float rr[FM], rm[FM];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const float2 st = ((const float2 *)a.ln_stats)[min(mrow + 32 * i + r32, a.M - 1)];
+        rr[i] = st.y;
+        rm[i] = st.x * st.y;
+    }
+    const float *d = (const float *)a.bias;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        float cj[16], dj[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t n = min(ncol + 32 * j + 8 * q + 4 * g, a.N - 4);
+            const float4 c4 = *(const float4 *)(a.ln_c + n), d4 = *(const float4 *)(d + n);
+            cj[4 * q] = c4.x; cj[4 * q + 1] = c4.y; cj[4 * q + 2] = c4.z; cj[4 * q + 3] = c4.w;
+            dj[4 * q] = d4.x; dj[4 * q + 1] = d4.y; dj[4 * q + 2] = d4.z; dj[4 * q + 3] = d4.w;
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(rr[i], acc[i][j][r], fmaf(-rm[i], cj[r], dj[r]));
+    }
+}
+
 // 8 consecutive fp16 products of row block i, column block j, half p of one lane, in the Z^T layout above.
 // Both 16-byte chunks (p = 0, 1) of the 32 x 32 block come out of the same four swaps.
 template <int FM, int FN>
@@ -805,15 +844,15 @@ template <int BM, int BN, int FM, int FN>
 __device__ __forceinline__ void chain_chunks(const GemmArgs &a, uint4 (&q)[FM][FN][2], uint32_t m0, uint32_t n0, int wm, int wn) {
     constexpr int TM = BM / 2, TN = BN / 2;
     const int lane = threadIdx.x & 63, g = lane >> 5, r32 = lane & 31;
-    if (!a.accumulate && !a.bias && !a.res && a.act == SH_ACT_NONE) return;
-    if (!a.accumulate && !(a.bias && a.bias_fp32)) {
+    if (!a.accumulate && (!a.bias || a.ln_stats) && !a.res && a.act == SH_ACT_NONE) return;
+    if (!a.accumulate && (!(a.bias && a.bias_fp32) || a.ln_stats)) {
         uint4 bq[FN][2];
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
                 const uint32_t gn = n0 + wn * TN + 32 * j + 16 * p + 8 * g, gc = min(gn, a.N - 8);
-                bq[j][p] = a.bias ? *(const uint4 *)((const uint16_t *)a.bias + gc) : zero4();
+                bq[j][p] = (a.bias && !a.ln_stats) ? *(const uint4 *)((const uint16_t *)a.bias + gc) : zero4();
             }
         uint4 rq[FM][FN][2];
 #pragma unroll
@@ -865,8 +904,9 @@ __device__ __forceinline__ void chain_chunks(const GemmArgs &a, uint4 (&q)[FM][F
 
 // Accumulators (Z^T layout) -> fp16 chunks with the epilogue chain applied.
 template <int BM, int BN, int FM, int FN>
-__device__ __forceinline__ void finish_chunks(const GemmArgs &a, const sh_f16v (&acc)[FM][FN], uint32_t m0, uint32_t n0,
+__device__ __forceinline__ void finish_chunks(const GemmArgs &a, sh_f16v (&acc)[FM][FN], uint32_t m0, uint32_t n0,
                                               uint4 (&q)[FM][FN][2], int wm, int wn) {
+    if (a.ln_stats) ln_fold_zt<FM, FN>(a, acc, m0 + wm * (BM / 2), n0 + wn * (BN / 2));
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -1274,6 +1314,7 @@ __global__ __launch_bounds__(256, MINW) void k_gemm5(GemmArgs a) {
     if constexpr (SPLIT) {
         store_partials_zt<BM, BN, FM, FN>(a, acc, m0, n0, split, wm, wn);
     } else {
+        if (a.ln_stats) ln_fold_zt<FM, FN>(a, acc, m0 + wm * TM, n0 + wn * TN);
         uint4 qc[FM][FN][2];
 #pragma unroll
         for (int i = 0; i < FM; ++i)
@@ -1483,12 +1524,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void k_gemm6(GemmArgs a) {
                             make_float4(acc[i][j][4 * u], acc[i][j][4 * u + 1], acc[i][j][4 * u + 2], acc[i][j][4 * u + 3]);
                 }
     } else {
+        if (a.ln_stats) ln_fold_zt<FM, FN>(a, acc, m0 + wm * TM, n0 + wn * TN);
         uint4 qc[FM][FN][2];
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j) zt_chunks<FM, FN>(acc, i, j, qc[i][j]);
-        const bool any = a.accumulate || a.bias || a.res || a.act != SH_ACT_NONE;
+        const bool any = a.accumulate || (a.bias && !a.ln_stats) || a.res || a.act != SH_ACT_NONE;
         if (any) {
 #pragma unroll
             for (int i = 0; i < FM; ++i) {
@@ -1571,6 +1613,10 @@ __global__ __launch_bounds__(64) void k_splitk_reduce(GemmArgs a, ShDiv div, uin
             for (int e = 0; e < W; ++e) v[e] += u[q][e];
     }
     uint16_t out[W];
+    if (a.ln_stats) {
+#pragma unroll
+        for (int e = 0; e < W; ++e) v[e] = ln_apply(a, v[e], gm, gn + e);
+    }
 #pragma unroll
     for (int e = 0; e < W; ++e) out[e] = epi_chain(a, sh_dev_f2h(v[e]), gm, gn + e);
     if (VEC) {
@@ -1593,6 +1639,7 @@ struct KCfg {
     int bm, bn, stages; bool v2; KernelFn vec[2], scalar[2]; size_t lds; float eff; bool attr_set; int threads = 256;
     bool ktail = false; KernelFn tail[2] = {nullptr, nullptr};     // the K % 64 != 0 variants (unsplit, split)
     bool wt = false; KernelFn wt_vec[2] = {nullptr, nullptr}, wt_scalar[2] = {nullptr, nullptr};
+    bool reg = false;            // the unsplit kernel's epilogue works on the fp32 accumulators (the LayerNorm fold)
 };
 
 #define SH_KCFG(BM, BN, EFF) { BM, BN, 2, false, { k_gemm<BM, BN, true, false>, k_gemm<BM, BN, true, true> }, \
@@ -1602,19 +1649,23 @@ struct KCfg {
                                { k_gemm<BM, BN, false, false, true>, k_gemm<BM, BN, false, true, true> } }
 #define SH_KCFG6(BM, BN, WGM, WGN, SK, NST, W, PRE, DB, EFF) \
     { BM, BN, NST, true, { k_gemm6<BM, BN, WGM, WGN, SK, NST, W, false, PRE, DB>, k_gemm6<BM, BN, WGM, WGN, SK, NST, W, true, PRE, DB> }, \
-      { nullptr, nullptr }, Cfg6<BM, BN, WGM, WGN, SK, NST>::LDS, EFF, false, 64 * WGM * WGN, false, { nullptr, nullptr }, true }
+      { nullptr, nullptr }, Cfg6<BM, BN, WGM, WGN, SK, NST>::LDS, EFF, false, 64 * WGM * WGN, false, { nullptr, nullptr }, true, \
+      { nullptr, nullptr }, { nullptr, nullptr }, true }
 #define SH_KCFG2(BM, BN, ST, EFF) { BM, BN, ST, true, { k_gemm2<BM, BN, ST, false>, k_gemm2<BM, BN, ST, true> }, \
                                     { nullptr, nullptr }, Cfg2<BM, BN, ST>::LDS, EFF, false, 256, true, \
                                     { k_gemm2<BM, BN, ST, false, true>, k_gemm2<BM, BN, ST, true, true> } }
 #define SH_KCFG4(BM, BN, ST, NT, W, EFF) { BM, BN, ST, true, { k_gemm4<BN, ST, false, NT, BM, W>, k_gemm4<BN, ST, true, NT, BM, W> }, \
                                            { nullptr, nullptr }, Cfg4<BN, ST, NT, BM>::LDS, EFF, false, NT }
 #define SH_KCFG4R(BM, BN, ST, W, EFF) { BM, BN, ST, true, { k_gemm4<BN, ST, false, 256, BM, W, true>, k_gemm4<BN, ST, true, 256, BM, W, true> }, \
-                                       { nullptr, nullptr }, (size_t)(ST) * Cfg4<BN, ST, 256, BM>::STAGE, EFF, false, 256 }
+                                       { nullptr, nullptr }, (size_t)(ST) * Cfg4<BN, ST, 256, BM>::STAGE, EFF, false, 256, \
+                                       false, { nullptr, nullptr }, false, { nullptr, nullptr }, { nullptr, nullptr }, true }
 #define SH_KCFG4S(BM, BN, ST, W, EFF) { BM, BN, ST, true, { k_gemm4<BN, ST, false, 256, BM, W, true, 64>, k_gemm4<BN, ST, true, 256, BM, W, true, 64> }, \
-                                       { nullptr, nullptr }, (size_t)(ST) * Cfg4<BN, ST, 256, BM, 64>::STAGE, EFF, false, 256 }
+                                       { nullptr, nullptr }, (size_t)(ST) * Cfg4<BN, ST, 256, BM, 64>::STAGE, EFF, false, 256, \
+                                       false, { nullptr, nullptr }, false, { nullptr, nullptr }, { nullptr, nullptr }, true }
 #define SH_KCFG5(BM, BN, SK, NST, W, EFF) { BM, BN, NST, true, { k_gemm5<BM, BN, SK, NST, false, W, false, true>, \
                                               k_gemm5<BM, BN, SK, NST, false, W, true, true> }, \
-                                            { nullptr, nullptr }, Cfg5<BM, BN, SK, NST, false>::LDS, EFF, false, 256 }
+                                            { nullptr, nullptr }, Cfg5<BM, BN, SK, NST, false>::LDS, EFF, false, 256, \
+                                            false, { nullptr, nullptr }, false, { nullptr, nullptr }, { nullptr, nullptr }, true }
 #define SH_KCFG3(BM, BN, EFF) { BM, BN, 2, true, { k_gemm3<BM, BN, false>, k_gemm3<BM, BN, true> }, \
                                 { nullptr, nullptr }, Cfg3<BM, BN>::LDS, EFF, false, 512 }
 // eff = sustained fraction of the MFMA peak per CU measured for each tile on MI355X (tile-time model of
@@ -1737,13 +1788,16 @@ struct Plan { int cfg; uint32_t splits; };
 // A W^T call with aligned operands and K % 64 == 0 runs only on the W^T direct-to-LDS tiles, which store the bits
 // of the W-layout direct-to-LDS tiles; otherwise it takes the register-staged tiles (the bits of the W-layout
 // register-staged tiles).
-bool eligible(const KCfg &c, bool vec, bool fast, bool ktail, bool wt) {
+bool eligible(const KCfg &c, bool vec, bool fast, bool ktail, bool wt, bool reg_only = false) {
+    if (reg_only && !c.reg) return false;
     if (c.v2) return c.wt == wt && (fast || (!wt && ktail && c.ktail));
     if (wt && fast) return false;
     return vec || c.bm * c.bn <= 128 * 128;
 }
 
-Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t want_splits, bool wt = false) {
+// reg_only: only configurations whose unsplit epilogue works on fp32 accumulators (a LayerNorm fold); if none is
+// eligible the plan falls back to the unrestricted choice and the launch goes through the partials path.
+Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t want_splits, bool wt = false, bool reg_only = false) {
     const bool ktail = vec && K > 0 && K % BK != 0;
     const int cus = sh_num_cus() > 0 ? sh_num_cus() : 256;
     // Every eligible (config, splits) is estimated; among those within 3 % of the fastest estimate the one with
@@ -1754,7 +1808,7 @@ Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t wa
     int n = 0;
     double tmin = 1e300;
     for (int i = 0; i < kNumCfg; ++i) {
-        if (!eligible(g_cfgs[i], vec, fast, ktail, wt)) continue;
+        if (!eligible(g_cfgs[i], vec, fast, ktail, wt, reg_only)) continue;
         uint32_t lo = 1, hi = 1;
         if (want_splits) lo = hi = want_splits;
         else hi = std::max<uint32_t>(1, std::min<uint32_t>(16, K / 128));
@@ -1776,7 +1830,8 @@ Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t wa
     const int fc = env_int("SH_GEMM_CFG", -1);
     const int fs = env_int("SH_GEMM_SPLITS", 0);
     if (fs > 0 && !want_splits) best.splits = split_k(K, (uint32_t)fs).splits;
-    if (fc >= 0 && fc < kNumCfg && eligible(g_cfgs[fc], vec, fast, ktail, wt)) best.cfg = fc;
+    if (fc >= 0 && fc < kNumCfg && eligible(g_cfgs[fc], vec, fast, ktail, wt, reg_only)) best.cfg = fc;
+    if (reg_only && n == 0) return choose(M, N, K, vec, fast, want_splits, wt, false);
     return best;
 }
 
@@ -1819,7 +1874,8 @@ void tune_file_load() {
     if (!f) return;
     unsigned M, N, K, b, act, wt; unsigned long long ldx, ldw; int cfg;
     while (fscanf(f, "%u %u %u %llu %llu %u %u %u %d", &M, &N, &K, &ldx, &ldw, &b, &act, &wt, &cfg) == 9)
-        if (cfg >= 0 && cfg < kNumCfg && g_cfgs[cfg].v2 && g_cfgs[cfg].wt == (wt != 0)) g_tuned[TuneKey{M, N, K, ldx, ldw, b, act, wt}] = cfg;
+        if (cfg >= 0 && cfg < kNumCfg && g_cfgs[cfg].v2 && g_cfgs[cfg].wt == ((wt & 1u) != 0) && (!(wt & 2u) || g_cfgs[cfg].reg))
+            g_tuned[TuneKey{M, N, K, ldx, ldw, b, act, wt}] = cfg;
     fclose(f);
 }
 
@@ -1834,6 +1890,7 @@ void tune_file_append(const TuneKey &k, int cfg) {
 }
 
 int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st, bool wt) {
+    const bool reg_only = call.ln_stats != nullptr;
     static const int enabled = env_int("SH_GEMM_TUNE", 1);
     if (!enabled || env_int("SH_GEMM_CFG", -1) >= 0) return heur;
     const int cus = sh_num_cus() > 0 ? sh_num_cus() : 256;
@@ -1841,7 +1898,8 @@ int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st, bool wt) {
     (void)est_time(heur, call.M, call.N, call.K, 1, cus, &thr);
     if (thr < 12e-6) return heur;                    // the throughput estimate: small problems keep the model's tile
     tune_file_load();
-    const TuneKey key{call.M, call.N, call.K, call.ldx, call.ldw, call.bias ? 1u + call.bias_fp32 : 0u, call.act, wt ? 1u : 0u};
+    const TuneKey key{call.M, call.N, call.K, call.ldx, call.ldw, call.bias ? 1u + call.bias_fp32 : 0u, call.act,
+                      (wt ? 1u : 0u) | (reg_only ? 2u : 0u)};
     auto it = g_tuned.find(key);
     if (it != g_tuned.end()) return it->second;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -1860,7 +1918,7 @@ int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st, bool wt) {
         for (int round = 0; round < 3 && ok; ++round)
             for (int i = 0; i < kNumCfg && ok; ++i) {
                 KCfg &c = g_cfgs[i];
-                if (!c.v2 || c.wt != wt) continue;
+                if (!c.v2 || c.wt != wt || (reg_only && !c.reg)) continue;
                 set_attrs(c);
                 set_grid(a, c);
                 const dim3 grid(a.tiles_m * a.tiles_n);
@@ -1875,12 +1933,12 @@ int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st, bool wt) {
         if (ok) {
             float best_ms = 1e30f;
             for (int i = 0; i < kNumCfg; ++i)
-                if (g_cfgs[i].v2 && g_cfgs[i].wt == wt && mins[i] < best_ms) { best_ms = mins[i]; best = i; }
+                if (g_cfgs[i].v2 && g_cfgs[i].wt == wt && (!reg_only || g_cfgs[i].reg) && mins[i] < best_ms) { best_ms = mins[i]; best = i; }
             if (env_int("SH_GEMM_VERBOSE", 0)) {      // the one-time choice on stderr: model pick, winner, all times
                 fprintf(stderr, "[sh_gemm] tuned %ux%ux%u: model cfg %d (%.2f us), chose cfg %d (%.2f us);", call.M, call.N, call.K,
                         heur, 500.f * mins[heur], best, 500.f * best_ms);
                 for (int i = 0; i < kNumCfg; ++i)
-                    if (g_cfgs[i].v2 && g_cfgs[i].wt == wt) fprintf(stderr, " %d:%.2f", i, 500.f * mins[i]);
+                    if (g_cfgs[i].v2 && g_cfgs[i].wt == wt && (!reg_only || g_cfgs[i].reg)) fprintf(stderr, " %d:%.2f", i, 500.f * mins[i]);
                 fprintf(stderr, "\n");
             }
         }
@@ -1930,18 +1988,24 @@ int launch(const GemmReq &r, const char *name) {
                      sh_aligned16(r.x) && sh_aligned16(r.w) && sh_aligned16(r.z) &&
                      (!res || (ldr % 8 == 0 && sh_aligned16(res))) && (!bias || sh_aligned16(bias));
     const bool fast = vec && r.K % BK == 0 && r.K > 0;
-    Plan p = choose(r.M, r.N, r.K, vec, fast, r.splits, r.wt);
+    // LayerNorm fold: the unsplit kernels that apply it on their fp32 accumulators need 16-byte aligned c / d rows;
+    // every other case goes through the fp32 partials (one K range or more) and the reduction applies it
+    const bool ln = e && e->ln_stats;
+    const bool ln_reg = ln && fast && sh_aligned16(e->ln_c) && sh_aligned16(bias);
+    Plan p = choose(r.M, r.N, r.K, vec, fast, r.splits, r.wt, ln_reg);
     if (r.mesh) p.splits = 1;
-    if (fast && p.splits == 1 && g_cfgs[p.cfg].v2 && !r.part) {
+    if (fast && p.splits == 1 && g_cfgs[p.cfg].v2 && !r.part && (!ln || (ln_reg && g_cfgs[p.cfg].reg))) {
         GemmArgs t{};
         t.x = (const uint16_t *)r.x; t.w = (const uint16_t *)r.w; t.bias = (const void *)bias;
         t.ldx = r.ldx; t.ldw = r.ldw; t.M = r.M; t.N = r.N; t.K = r.K; t.kps = sh_cdiv(r.K, BK) * BK; t.splits = 1;
         t.bias_fp32 = (e && e->bias_fmt == SH_BIAS_FP32) ? 1 : 0; t.act = e ? e->act : 0;
+        t.ln_stats = ln ? (const float *)e->ln_stats : nullptr; t.ln_c = ln ? (const float *)e->ln_c : nullptr;
         p.cfg = tuned_cfg(t, p.cfg, sh_stream(), r.wt);
     }
     KCfg &c = g_cfgs[p.cfg];
     const SplitK sk = split_k(r.K, p.splits);
     const uint32_t splits = sk.splits, kps = sk.kps;
+    const bool partials = splits > 1 || (ln && !(ln_reg && c.reg));
 
     GemmArgs a{};
     a.x = (const uint16_t *)r.x; a.w = (const uint16_t *)r.w; a.z = (uint16_t *)r.z;
@@ -1950,6 +2014,7 @@ int launch(const GemmReq &r, const char *name) {
     a.M = r.M; a.N = r.N; a.K = r.K; a.kps = kps;
     a.tiles_m = sh_cdiv(r.M, c.bm); a.tiles_n = sh_cdiv(r.N, c.bn); a.splits = splits;
     a.accumulate = r.accumulate; a.bias_fp32 = (e && e->bias_fmt == SH_BIAS_FP32) ? 1 : 0; a.act = e ? e->act : 0;
+    a.ln_stats = ln ? (const float *)e->ln_stats : nullptr; a.ln_c = ln ? (const float *)e->ln_c : nullptr;
     const uint64_t nblk64 = (uint64_t)a.tiles_m * a.tiles_n * splits;
     if (nblk64 > 0x7FFFFFFFull) { sh_set_error(-1, "[%s] problem too large", name); return -1; }
     const uint32_t nblk = (uint32_t)nblk64;
@@ -1957,7 +2022,7 @@ int launch(const GemmReq &r, const char *name) {
     a.xcd_groups = (X > 1 && nblk % (uint32_t)X == 0) ? (uint32_t)X : 1;
 
     hipStream_t st = sh_stream();
-    const bool split = splits > 1;
+    const bool split = partials;
     KernelFn fn = r.wt ? (c.v2 ? c.vec[split] : vec ? c.wt_vec[split] : c.wt_scalar[split])
                        : (c.v2 && !fast) ? c.tail[split] : (vec || c.v2) ? c.vec[split] : c.scalar[split];   // !fast: K % 64 != 0
     set_attrs(c);
@@ -1987,6 +2052,18 @@ int launch(const GemmReq &r, const char *name) {
         else hipLaunchKernelGGL(k_splitk_reduce<false>, dim3(sh_cdiv((uint32_t)items, 64)), dim3(64), 0, st, a, div, per_row, (uint32_t)items);
         if (!sh_launch_ok(name)) return SH_EHIP;
     }
+    return 0;
+}
+
+// The LayerNorm fold's arguments: both rows given, the bias is the fp32 row d, and no accumulate (z_old would
+// be added after the fold's rounding point, which no unfused sequence does).
+int check_ln(const char *name, const sh_gemm_epi *e, const sh_gemm_cfg &c) {
+    if (!e || (!e->ln_stats && !e->ln_c)) return 0;
+    if (!e->ln_stats || !e->ln_c || !e->bias || e->bias_fmt != SH_BIAS_FP32 || c.accumulate) {
+        sh_set_error(-1, "[%s] LayerNorm fold needs ln_stats, ln_c and the fp32 bias row d, without accumulate", name);
+        return -1;
+    }
+    if ((e->ln_stats | e->ln_c | e->bias) % 4) { sh_set_error(-1, "[%s] LayerNorm fold rows must be 4-byte aligned", name); return -1; }
     return 0;
 }
 
@@ -2089,6 +2166,7 @@ int sh_gemm_ex(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint3
     if (c.fmt != SH_FP16) { sh_set_error(-1, "[sh_gemm_ex] fmt %u: only SH_FP16 is implemented", c.fmt); return -1; }
     if (epi && epi->residual && epi->ldr < N) { sh_set_error(-1, "[sh_gemm_ex] ldr %u < N %u", epi->ldr, N); return -1; }
     if (epi && epi->act > SH_ACT_GELU) { sh_set_error(-1, "[sh_gemm_ex] unknown act %u", epi->act); return -1; }
+    if (int rc = check_ln("sh_gemm_ex", epi, c)) return rc;
     GemmReq r{x, w, z, M, N, K, ldx, ldw, ldz, c.accumulate, epi, epi ? epi->splits : 1u, false};
     return launch(r, "sh_gemm_ex");
 }
@@ -2102,6 +2180,7 @@ int sh_gemm_ex_wt(uint64_t x, uint64_t wt, uint64_t z, uint32_t M, uint32_t N, u
     if (ldwt < K) { sh_set_error(-1, "[sh_gemm_ex_wt] ldwt %u < K %u", ldwt, K); return -1; }
     if (epi && epi->residual && epi->ldr < N) { sh_set_error(-1, "[sh_gemm_ex_wt] ldr %u < N %u", epi->ldr, N); return -1; }
     if (epi && epi->act > SH_ACT_GELU) { sh_set_error(-1, "[sh_gemm_ex_wt] unknown act %u", epi->act); return -1; }
+    if (int rc = check_ln("sh_gemm_ex_wt", epi, c)) return rc;
     GemmReq r{x, wt, z, M, N, K, ldx, ldwt, ldz, c.accumulate, epi, epi ? epi->splits : 1u, false};
     r.wt = true;
     return launch(r, "sh_gemm_ex_wt");

@@ -227,6 +227,72 @@ __global__ __launch_bounds__(256) void k_layernorm_p(uint16_t *y, const uint16_t
     }
 }
 
+// Row statistics of k_layernorm_p's rows (the same two passes in fp32), as (mean, 1 / sqrt(var + eps)) pairs.
+template <int LPR, int NCH>
+__global__ __launch_bounds__(256) void k_row_stats(float2 *stats, const uint16_t *x, uint32_t rows, uint32_t cols, uint64_t ldx,
+                                                   float eps) {
+    constexpr int GPW = 64 / LPR;
+    const int lane = threadIdx.x & 63, gl = lane % LPR;
+    const uint32_t group = (blockIdx.x * 4 + (threadIdx.x >> 6)) * GPW + lane / LPR;
+    const uint32_t ngroups = gridDim.x * 4 * GPW;
+    auto col = [&](int u) { return 8u * (uint32_t)(gl + LPR * u); };
+    const float inv_n = 1.f / (float)cols;
+    uint32_t row = group;
+    uint4 cur[NCH];
+    const uint32_t r0 = row < rows ? row : 0u;
+#pragma unroll
+    for (int u = 0; u < NCH; ++u) cur[u] = *(const uint4 *)(x + r0 * ldx + (col(u) < cols ? col(u) : 0u));
+    for (; row < rows; row += ngroups) {
+        const uint32_t nrow = row + ngroups < rows ? row + ngroups : row;
+        uint4 nxt[NCH];
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) nxt[u] = *(const uint4 *)(x + nrow * ldx + (col(u) < cols ? col(u) : 0u));
+        float v[NCH][8];
+        float s = 0.f;
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) {
+            unpack8(cur[u], v[u]);
+            const bool ok = col(u) < cols;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { v[u][i] = ok ? v[u][i] : 0.f; s += v[u][i]; }
+        }
+#pragma unroll
+        for (int o = LPR / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+        const float mean = s * inv_n;
+        float q = 0.f;
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) {
+            const bool ok = col(u) < cols;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { const float d = ok ? v[u][i] - mean : 0.f; q += d * d; }
+        }
+#pragma unroll
+        for (int o = LPR / 2; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
+        if (gl == 0) stats[row] = make_float2(mean, sh_fast_rsq(q * inv_n + eps));
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) cur[u] = nxt[u];
+    }
+}
+
+// The weight side of a LayerNorm fold, one column n per thread walking k: wp = r16(gamma_k w), c += wp (fp32),
+// d += beta_k w (fp32), then d += bias.
+__global__ __launch_bounds__(256) void k_ln_fold(uint16_t *wp, float *c, float *d, const uint16_t *w, const uint16_t *gamma,
+                                                 const uint16_t *beta, const uint16_t *bias, uint32_t K, uint32_t N,
+                                                 uint64_t ldw, uint64_t ldwp) {
+    const uint32_t n = blockIdx.x * 256u + threadIdx.x;
+    if (n >= N) return;
+    float cs = 0.f, ds = 0.f;
+    for (uint32_t k = 0; k < K; ++k) {
+        const float wv = sh_dev_h2f(w[(uint64_t)k * ldw + n]);
+        const uint16_t h = sh_dev_f2h(sh_dev_h2f(gamma[k]) * wv);
+        wp[(uint64_t)k * ldwp + n] = h;
+        cs += sh_dev_h2f(h);
+        ds = fmaf(sh_dev_h2f(beta[k]), wv, ds);
+    }
+    c[n] = cs;
+    d[n] = ds + (bias ? sh_dev_h2f(bias[n]) : 0.f);
+}
+
 // Streaming 1-D copy of n16 16-byte chunks: U chunks per thread, all loaded before any is stored, one pass per
 // thread (no grid-stride loop: a thread's next loads would queue behind its stores in the memory counter).
 template <int U>
@@ -720,6 +786,37 @@ void sh_layernorm_ld(uint64_t y, uint64_t x, uint64_t gamma, uint64_t beta, uint
     if (!check_args("sh_layernorm_ld", y, x, rows, cols, ldy < ldx ? ldy : ldx)) return;
     if (!gamma || !beta) { sh_set_error(-1, "[sh_layernorm_ld] NULL gamma/beta"); return; }
     launch_layernorm(y, x, gamma, beta, rows, cols, ldy, ldx, eps);
+}
+
+void sh_row_stats(uint64_t stats, uint64_t x, uint32_t rows, uint32_t cols, uint32_t ld, float eps) {
+    if (!check_args("sh_row_stats", stats, x, rows, cols, ld)) return;
+    if (stats % 8) { sh_set_error(-1, "[sh_row_stats] stats must be 8-byte aligned"); return; }
+    if (!vec_ok(cols, {x}, {ld}) || cols > 4096) {
+        sh_set_error(-1, "[sh_row_stats] needs 16-byte aligned rows (cols, ld %% 8 == 0) of at most 4096 columns");
+        return;
+    }
+    hipStream_t st = sh_stream();
+    const uint32_t lpr = cols <= 1024 ? 32 : 64, gpb = 4 * (64 / lpr);
+    const uint32_t cap = (uint32_t)(sh_num_cus() > 0 ? sh_num_cus() : 256) * 16;
+    const dim3 g(std::max<uint32_t>(1, std::min<uint32_t>(sh_cdiv(rows, gpb), cap)));
+    float2 *S = (float2 *)stats; const uint16_t *X = (const uint16_t *)x;
+#define SH_RS(L, N) hipLaunchKernelGGL((k_row_stats<L, N>), g, dim3(256), 0, st, S, X, rows, cols, (uint64_t)ld, eps)
+    if (lpr == 32) { if (cols <= 256) SH_RS(32, 1); else if (cols <= 512) SH_RS(32, 2); else if (cols <= 768) SH_RS(32, 3); else SH_RS(32, 4); }
+    else { if (cols <= 2048) SH_RS(64, 4); else if (cols <= 3072) SH_RS(64, 6); else SH_RS(64, 8); }
+#undef SH_RS
+    sh_launch_ok("sh_row_stats");
+}
+
+void sh_ln_fold(uint64_t wp, uint64_t c, uint64_t d, uint64_t w, uint64_t gamma, uint64_t beta, uint64_t bias,
+                uint32_t K, uint32_t N, uint32_t ldw, uint32_t ldwp) {
+    if (K == 0 || N == 0) return;
+    if (!wp || !c || !d || !w || !gamma || !beta) { sh_set_error(-1, "[sh_ln_fold] NULL address"); return; }
+    if (ldw < N || ldwp < N) { sh_set_error(-1, "[sh_ln_fold] ldw %u / ldwp %u < N %u", ldw, ldwp, N); return; }
+    sh_ensure_init();
+    hipLaunchKernelGGL(k_ln_fold, dim3(sh_cdiv(N, 256)), dim3(256), 0, sh_stream(), (uint16_t *)wp, (float *)c, (float *)d,
+                       (const uint16_t *)w, (const uint16_t *)gamma, (const uint16_t *)beta, (const uint16_t *)bias, K, N,
+                       (uint64_t)ldw, (uint64_t)ldwp);
+    sh_launch_ok("sh_ln_fold");
 }
 
 // HBM -> HBM 1-D copy of `bytes` (reference sh_l1.inc.c:58-61, an iDMA 1-D transfer), stream-ordered on the

@@ -10,8 +10,12 @@ main.c makes, tests/gvsoc/siglip_layer/main.c:64-127), on B sequences stacked as
 sequence, sh_add, sh_gelu). `sequence="fused"` computes the same layer with the additive entry points:
 one QKV GEMM against the concatenated [D, 3D] weight with the bias in its epilogue, one batched attention
 over q/k/v views of the QKV buffer (ld = 3D), and GEMM epilogues that add the bias, apply GELU or add the
-residual, which removes five row-op round trips through HBM. Both match the numpy oracle within the fp16
-tolerance (the fused epilogue rounds once where the reference rounds twice).
+residual, which removes five row-op round trips through HBM. Each LayerNorm is folded into the GEMM that reads
+it: sh_row_stats writes the rows' (mean, 1/sqrt(var + eps)) (8 bytes a row instead of the normalised row), the
+GEMM multiplies the raw rows by W' = r16(gamma W) and its epilogue forms r (x W') - r mu c + d with c = 1^T W',
+d = beta^T W + b (sh_ln_fold, once per weight), which is LN(x) W + b. Both sequences match the numpy oracle
+within the fp16 tolerance (the fused epilogues round once where the reference rounds twice, and the fold rounds
+gamma W where the reference rounds LN(x)).
 
 Buffers are torch tensors (allocation only); every computation is a libshops.so call.
 """
@@ -49,6 +53,23 @@ class LayerParams:
     def __getitem__(self, k):
         return self.t[k]
 
+    def fold(self, lib) -> None:
+        """The weight side of both LayerNorm folds (sh_ln_fold, enqueued on the library stream), once: `wqkv_ln`,
+        `cqkv`, `dqkv` for LN1 -> QKV and `w1_ln`, `c1`, `d1` for LN2 -> FFN-up (fp16 W', fp32 c and d)."""
+        if "w1_ln" in self.t:
+            return
+        A = shops.addr
+        for w, g, be, b, tag in (("wqkv", "g1", "be1", "bqkv", "qkv"), ("w1", "g2", "be2", "b1", "1")):
+            W = self.t[w]
+            K, N = W.shape
+            wp = torch.empty_like(W)
+            c = torch.empty(N, dtype=torch.float32, device=W.device)
+            d = torch.empty(N, dtype=torch.float32, device=W.device)
+            lib.sh_last_error()                  # reads and clears: the check below sees this call's status only
+            lib.sh_ln_fold(A(wp), A(c), A(d), A(W), A(self.t[g]), A(self.t[be]), A(self.t[b]), K, N, N, N)
+            _check(lib.sh_last_error(), "sh_ln_fold " + w)
+            self.t[w + "_ln"], self.t["c" + tag], self.t["d" + tag] = wp, c, d
+
 
 class Encoder:
     """Runs layers on a [B*S, D] fp16 activation buffer; scratch buffers are allocated once per (B, S)."""
@@ -72,7 +93,9 @@ class Encoder:
             D, F = self.D, self.F
             self._plans = {}
             self._bufs = {"rows": rows, "ln1": z(D), "qkv": z(3 * D), "q": z(D), "k": z(D), "v": z(D), "o": z(D),
-                          "ao": z(D), "h": z(D), "ln2": z(D), "f1": z(F), "g": z(F), "f2": z(D)}
+                          "ao": z(D), "h": z(D), "ln2": z(D), "f1": z(F), "g": z(F), "f2": z(D),
+                          "st1": torch.empty((rows, 2), dtype=torch.float32, device=self.device),
+                          "st2": torch.empty((rows, 2), dtype=torch.float32, device=self.device)}
         return self._bufs
 
     # -- the reference's call sequence (siglip.py:133-168) ------------------------------------------------
@@ -106,6 +129,7 @@ class Encoder:
     # -- fused sequence (additive entry points) ------------------------------------------------------------
     def _fused_plan(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int) -> list:
         """The layer's library calls with every argument converted once: (op name, function, args, what)."""
+        p.fold(self.lib)
         key = (x.data_ptr(), out.data_ptr(), B, S) + tuple(t.data_ptr() for t in p.t.values())
         hit = self._plans.get(key)
         if hit is not None:
@@ -116,17 +140,20 @@ class Encoder:
         cfg = self.gemm_cfg
         D3 = 3 * D
         qkv = b["qkv"]
+        F32 = shops.SH_BIAS_FP32
         calls = [
-            ("ln1", L.sh_layernorm, (A(b["ln1"]), A(x), A(p["g1"]), A(p["be1"]), rows, D, D, self.eps, shops.SH_ALL), None),
-            ("qkv", L.sh_gemm_ex, (A(b["ln1"]), A(p["wqkv"]), A(qkv), rows, D3, D, D, D3, D3, cfg,
-                                   shops.epi(bias=A(p["bqkv"]))), "sh_gemm_ex qkv"),
+            ("ln1", L.sh_row_stats, (A(b["st1"]), A(x), rows, D, D, self.eps), None),
+            ("qkv", L.sh_gemm_ex, (A(x), A(p["wqkv_ln"]), A(qkv), rows, D3, D, D, D3, D3, cfg,
+                                   shops.epi(bias=A(p["dqkv"]), bias_fmt=F32, ln_stats=A(b["st1"]), ln_c=A(p["cqkv"]))),
+             "sh_gemm_ex qkv"),
             ("attention", L.sh_attention_batched, (A(qkv), A(qkv, D), A(qkv, 2 * D), A(b["o"]), B, S, D, H, D3, D3, D3, D,
                                                    S * D3, S * D3, S * D3, S * D, 1.0 / math.sqrt(D // H), 0), "sh_attention_batched"),
             ("out_proj", L.sh_gemm_ex, (A(b["o"]), A(p["wo"]), A(b["h"]), rows, D, D, D, D, D, cfg,
                                         shops.epi(bias=A(p["bo"]), residual=A(x), ldr=D)), "sh_gemm_ex wo"),
-            ("ln2", L.sh_layernorm, (A(b["ln2"]), A(b["h"]), A(p["g2"]), A(p["be2"]), rows, D, D, self.eps, shops.SH_ALL), None),
-            ("ffn_up", L.sh_gemm_ex, (A(b["ln2"]), A(p["w1"]), A(b["g"]), rows, F, D, D, F, F, cfg,
-                                      shops.epi(bias=A(p["b1"]), act=shops.SH_ACT_GELU)), "sh_gemm_ex w1"),
+            ("ln2", L.sh_row_stats, (A(b["st2"]), A(b["h"]), rows, D, D, self.eps), None),
+            ("ffn_up", L.sh_gemm_ex, (A(b["h"]), A(p["w1_ln"]), A(b["g"]), rows, F, D, D, F, F, cfg,
+                                      shops.epi(bias=A(p["d1"]), bias_fmt=F32, act=shops.SH_ACT_GELU, ln_stats=A(b["st2"]),
+                                                ln_c=A(p["c1"]))), "sh_gemm_ex w1"),
             ("ffn_down", L.sh_gemm_ex, (A(b["g"]), A(p["w2"]), A(out), rows, D, F, F, D, D, cfg,
                                         shops.epi(bias=A(p["b2"]), residual=A(b["h"]), ldr=D)), "sh_gemm_ex w2"),
         ]
@@ -167,16 +194,17 @@ class Encoder:
 
     @staticmethod
     def op_costs(B: int, S: int, D: int = 768, F: int = 3072, H: int = 12) -> dict:
-        """Algorithmic FLOP and HBM bytes of each op of layer_fused (fp16 = 2 bytes; weights read once)."""
+        """Algorithmic FLOP and HBM bytes of each op of layer_fused (fp16 = 2 bytes, row statistics and the fold's
+        c / d rows fp32; weights read once)."""
         M = B * S
         g = lambda m, n, k: 2 * m * n * k  # noqa: E731
         return {
-            "ln1": {"flop": 0, "bytes": 2 * (2 * M * D + 2 * D)},
-            "qkv": {"flop": g(M, 3 * D, D), "bytes": 2 * (M * D + D * 3 * D + 3 * D + M * 3 * D)},
+            "ln1": {"flop": 0, "bytes": 2 * M * D + 8 * M},
+            "qkv": {"flop": g(M, 3 * D, D), "bytes": 2 * (M * D + D * 3 * D + M * 3 * D) + 8 * M + 8 * 3 * D},
             "attention": {"flop": 4 * B * H * S * S * (D // H), "bytes": 2 * 4 * M * D},
             "out_proj": {"flop": g(M, D, D), "bytes": 2 * (M * D + D * D + D + 2 * M * D)},
-            "ln2": {"flop": 0, "bytes": 2 * (2 * M * D + 2 * D)},
-            "ffn_up": {"flop": g(M, F, D), "bytes": 2 * (M * D + D * F + F + M * F)},
+            "ln2": {"flop": 0, "bytes": 2 * M * D + 8 * M},
+            "ffn_up": {"flop": g(M, F, D), "bytes": 2 * (M * D + D * F + M * F) + 8 * M + 8 * F},
             "ffn_down": {"flop": g(M, D, F), "bytes": 2 * (M * F + F * D + D + 2 * M * D)},
         }
 
