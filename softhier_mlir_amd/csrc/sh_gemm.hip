@@ -930,6 +930,46 @@ __device__ __forceinline__ void store_all(const GemmArgs &a, const uint4 (&q)[FM
             }
 }
 
+// Store a wavefront's finished block (TM x TN at rbase, cbase) through LDS: 32 rows at a time, its Z^T chunks (chunk
+// (i, j, p) of a lane: row 32 i + r32, columns 32 j + 16 p + 8 g) go to a row-major copy in LDS that only this
+// wavefront writes (`slots`: its NSLOT 1 KB DMA slots, slot s at slots + 4096 s, in a stage no wavefront reads
+// any more), then each store instruction writes 64 consecutive 16-byte chunks of those rows (whole row segments
+// of the block) instead of 32 rows x 32 bytes. The residual of the epilogue chain is added to the row chunks here
+// (the chain up to it was applied to q without it; the same fp16 adds, so the same bits). LDS instructions of
+// one wavefront execute in order, so no barrier is involved.
+template <int TM, int TN, int FM, int FN, int NSLOT>
+__device__ __forceinline__ void store_wave_staged(const GemmArgs &a, const uint4 (&q)[FM][FN][2], uint32_t rbase, uint32_t cbase,
+                                                  char *slots) {
+    constexpr int CPRW = TN / 8, HALF = 32 * CPRW, STEPS = HALF / 64;
+    static_assert(HALF % 64 == 0 && STEPS <= NSLOT, "32 rows of the block fit in the wavefront's slots");
+    const int lane = threadIdx.x & 63, g = lane >> 5, r32 = lane & 31;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        uint4 rq[STEPS];
+#pragma unroll
+        for (int u = 0; u < STEPS; ++u) {                // residual row chunks first: their latency overlaps the staging
+            const int lin = u * 64 + lane, row = lin / CPRW, c = lin % CPRW;
+            const uint32_t gm = min(rbase + 32 * i + row, a.M - 1), gn = min(cbase + 8 * c, a.N - 8);
+            rq[u] = a.res ? *(const uint4 *)(a.res + (uint64_t)gm * a.ldr + gn) : zero4();
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const int lin = r32 * CPRW + 4 * j + 2 * p + g;
+                *(uint4 *)(slots + (lin / 64) * 4096 + (lin % 64) * 16) = q[i][j][p];
+            }
+#pragma unroll
+        for (int u = 0; u < STEPS; ++u) {
+            const int lin = u * 64 + lane, row = lin / CPRW, c = lin % CPRW;
+            uint4 v = *(const uint4 *)(slots + u * 4096 + lane * 16);
+            if (a.res) v = make_uint4(sh_hadd2(v.x, rq[u].x), sh_hadd2(v.y, rq[u].y), sh_hadd2(v.z, rq[u].z), sh_hadd2(v.w, rq[u].w));
+            const uint32_t gm = rbase + 32 * i + row, gn = cbase + 8 * c;
+            if (gm < a.M && gn < a.N) *(uint4 *)(a.z + (uint64_t)gm * a.ldz + gn) = v;
+        }
+    }
+}
+
 // Split-K: the fp32 partial tile straight from the Z^T layout, 4 consecutive columns (16 bytes) per store.
 template <int BM, int BN, int FM, int FN>
 __device__ __forceinline__ void store_partials_zt(const GemmArgs &a, const sh_f16v (&acc)[FM][FN], uint32_t m0, uint32_t n0,
@@ -1248,9 +1288,11 @@ __global__ __launch_bounds__(256, MINW) void k_gemm5(GemmArgs a) {
 
     // epilogue operands loaded early (PRE): fp16 bias chunks and residual chunks of this lane's outputs
     // (the largest tiles keep their registers for the accumulators: no early loads there)
-    constexpr bool PRE_B = PRE && FM * FN <= 12, PRE_RES = PRE && FM * FN <= 6;
+    // (unsplit tiles are stored through each wavefront's DMA slots, and the residual is added there: no early load)
+    constexpr bool STAGED = !SPLIT && 4 * TN <= 64 * C::LOADS;
+    constexpr bool PRE_B = PRE && FM * FN <= 12, PRE_RES = PRE && FM * FN <= 6 && !STAGED;
     uint4 bq[PRE_B ? FN : 1][2], rq[PRE_RES ? FM : 1][PRE_RES ? FN : 1][2];
-    const bool pre_ok = PRE_B && !a.accumulate && !(a.bias && a.bias_fp32) && (PRE_RES || !a.res);
+    const bool pre_ok = PRE_B && !a.accumulate && !(a.bias && a.bias_fp32) && (PRE_RES || STAGED || !a.res);
     auto prefetch = [&]() {
 #pragma unroll
         for (int j = 0; j < (PRE_B ? FN : 0); ++j)
@@ -1320,21 +1362,31 @@ __global__ __launch_bounds__(256, MINW) void k_gemm5(GemmArgs a) {
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j) zt_chunks<FM, FN>(acc, i, j, qc[i][j]);
+        GemmArgs an = a;
+        if (STAGED) an.res = nullptr;                // the residual is added to the staged row chunks
         if (PRE_B && pre_ok && KT > 0) {
-            if (a.bias || a.res || a.act != SH_ACT_NONE) {
+            if (an.bias || an.res || an.act != SH_ACT_NONE) {
 #pragma unroll
                 for (int i = 0; i < FM; ++i)
 #pragma unroll
                     for (int j = 0; j < FN; ++j)
 #pragma unroll
                         for (int p = 0; p < 2; ++p)
-                            qc[i][j][p] = epi_chain8(a, qc[i][j][p], zero4(), bq[PRE_B ? j : 0][p], zero4(),
+                            qc[i][j][p] = epi_chain8(an, qc[i][j][p], zero4(), bq[PRE_B ? j : 0][p], zero4(),
                                                      PRE_RES ? rq[PRE_RES ? i : 0][PRE_RES ? j : 0][p] : zero4());
             }
         } else {
-            chain_chunks<BM, BN, FM, FN>(a, qc, m0, n0, wm, wn);
+            chain_chunks<BM, BN, FM, FN>(an, qc, m0, n0, wm, wn);
         }
-        store_all<BM, BN, FM, FN>(a, qc, m0, n0, wm, wn);
+        if constexpr (STAGED) {
+            // stage KT % NST holds no slice (only the clamped tail DMAs, each wavefront's into its own slots); its
+            // last reads were slice KT - NST's, finished before the barrier of a later slice
+            sh_wait_vmcnt<0>();                      // this wavefront's tail DMAs have landed
+            char *slots = (char *)smem + (size_t)(KT % NST) * C::STAGE + (size_t)wave * 1024;
+            store_wave_staged<TM, TN, FM, FN, C::LOADS>(a, qc, m0 + wm * TM, n0 + wn * TN, slots);
+        } else {
+            store_all<BM, BN, FM, FN>(a, qc, m0, n0, wm, wn);
+        }
     }
     sh_wait_vmcnt<0>();      // no DMA may still target this workgroup's LDS when it exits
 }
@@ -1847,11 +1899,16 @@ void set_attrs(KCfg &c) {
     c.attr_set = true;
 }
 
-void set_grid(GemmArgs &a, const KCfg &c) {
-    a.tiles_m = sh_cdiv(a.M, c.bm); a.tiles_n = sh_cdiv(a.N, c.bn);
+// Workgroups of a launch (tiles_m, tiles_n and splits set): one per tile and K range; sets the XCD remap.
+uint32_t grid_of(GemmArgs &a) {
     const uint32_t nblk = a.tiles_m * a.tiles_n * a.splits;
     const int X = sh_num_xcds();
     a.xcd_groups = (X > 1 && nblk % (uint32_t)X == 0) ? (uint32_t)X : 1;
+    return nblk;
+}
+
+void set_grid(GemmArgs &a, const KCfg &c) {
+    a.tiles_m = sh_cdiv(a.M, c.bm); a.tiles_n = sh_cdiv(a.N, c.bn);
 }
 
 // One-time timing of the tile configurations for a large unsplit problem. Every unsplit configuration
@@ -1921,7 +1978,7 @@ int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st, bool wt) {
                 if (!c.v2 || c.wt != wt || (reg_only && !c.reg)) continue;
                 set_attrs(c);
                 set_grid(a, c);
-                const dim3 grid(a.tiles_m * a.tiles_n);
+                const dim3 grid(grid_of(a));
                 if (round == 0) hipLaunchKernelGGL(c.vec[0], grid, dim3(c.threads), c.lds, st, a);     // warm-up
                 (void)hipEventRecord(e0, st);
                 for (int rep = 0; rep < 2; ++rep) hipLaunchKernelGGL(c.vec[0], grid, dim3(c.threads), c.lds, st, a);
@@ -2017,9 +2074,7 @@ int launch(const GemmReq &r, const char *name) {
     a.ln_stats = ln ? (const float *)e->ln_stats : nullptr; a.ln_c = ln ? (const float *)e->ln_c : nullptr;
     const uint64_t nblk64 = (uint64_t)a.tiles_m * a.tiles_n * splits;
     if (nblk64 > 0x7FFFFFFFull) { sh_set_error(-1, "[%s] problem too large", name); return -1; }
-    const uint32_t nblk = (uint32_t)nblk64;
-    const int X = sh_num_xcds();
-    a.xcd_groups = (X > 1 && nblk % (uint32_t)X == 0) ? (uint32_t)X : 1;
+    const uint32_t nblk = grid_of(a);
 
     hipStream_t st = sh_stream();
     const bool split = partials;

@@ -46,6 +46,9 @@ _KEEP: list = []
 
 @pytest.fixture(autouse=True)
 def _keep_device_tensors_alive():
+    from softhier_mlir_amd import shops
+    if shops._lib is not None:          # sh_last_error reads and clears: no test sees an earlier test's error code
+        shops._lib.sh_last_error()
     yield
     if _KEEP:
         import torch

@@ -115,6 +115,41 @@ def test_unsplit_tile_configs_store_identical_bits(lib, gpu, monkeypatch):
         assert refs.close(outs[i].view(np.float16), refs.gemm(x, w))[0] == 0
 
 
+REG_EPILOGUE_CFGS = (25, 26, 27, 28, 33, 34, 35, 36, 37, 38, 39, 40)   # register-epilogue tiles (W layout)
+
+
+@pytest.mark.parametrize("K", [64, 448])
+def test_register_epilogue_configs_with_residual(lib, gpu, K, monkeypatch):
+    """Register-epilogue tiles (configurations 33-40 store each wavefront's block through its own LDS slots as whole
+    row segments and add the residual there) on partial tiles in M and N with ldz > N, bias + GELU and
+    bias + residual epilogues: bit-identical to configuration 6 (LDS-staged epilogue of the whole tile), rows
+    sampled against the oracle, nothing written outside the view. K = 64 is a single slice."""
+    import torch
+    M, N = 1000, 584
+    x = data.normal((M, K), 61)
+    w = data.normal((K, N), 62, std=1 / np.sqrt(K))
+    b = data.normal((1, N), 63, std=0.3)
+    r = data.normal((M, N), 64)
+    X, W, Bb, R = to_dev(x), to_dev(w), to_dev(b), to_dev(r)
+    rows = np.array([0, 1, 31, 32, 127, 128, 511, 999])
+    for epi in ("gelu", "res"):
+        e = (shops.epi(bias=A(Bb), act=shops.SH_ACT_GELU) if epi == "gelu"
+             else shops.epi(bias=A(Bb), residual=A(R), ldr=N))
+        outs = {}
+        for cfg in (6,) + REG_EPILOGUE_CFGS:
+            monkeypatch.setenv("SH_GEMM_CFG", str(cfg))
+            Z = torch.full((M, N + 8), 7.0, dtype=torch.float16, device="cuda")
+            assert lib.sh_gemm_ex(A(X), A(W), A(Z), M, N, K, K, N, N + 8, None, e) == 0, (cfg, shops.last_error())
+            assert (to_np(Z)[:, N:] == 7.0).all(), cfg
+            outs[cfg] = codes(Z)[:, :N]
+        for cfg in REG_EPILOGUE_CFGS:
+            assert np.array_equal(outs[cfg], outs[6]), (epi, cfg, int((outs[cfg] != outs[6]).sum()))
+        zs = refs.r16(refs.add_bias(refs.r16(refs.gemm(x[rows], w)), b))
+        want = refs.r16(refs.gelu(zs)) if epi == "gelu" else refs.r16(refs.add(zs, r[rows]))
+        bad, err, _ = refs.close(outs[6][rows].view(np.float16), want)
+        assert bad == 0, (epi, err)
+
+
 def test_scalar_path_unaligned_views(lib, gpu):
     """Odd N and K, and operands starting one element into their buffers (no 16-byte alignment)."""
     import torch
