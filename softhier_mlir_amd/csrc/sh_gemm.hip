@@ -932,12 +932,12 @@ __device__ __forceinline__ void store_all(const GemmArgs &a, const uint4 (&q)[FM
 
 // Store a wavefront's finished block (TM x TN at rbase, cbase) through LDS: 32 rows at a time, its Z^T chunks (chunk
 // (i, j, p) of a lane: row 32 i + r32, columns 32 j + 16 p + 8 g) go to a row-major copy in LDS that only this
-// wavefront writes (`slots`: its NSLOT 1 KB DMA slots, slot s at slots + 4096 s, in a stage no wavefront reads
-// any more), then each store instruction writes 64 consecutive 16-byte chunks of those rows (whole row segments
+// wavefront writes (`slots`: its NSLOT 1 KB DMA slots, slot s at slots + SSTRIDE s, in a stage no wavefront
+// reads any more), then each store instruction writes 64 consecutive 16-byte chunks of those rows (whole row segments
 // of the block) instead of 32 rows x 32 bytes. The residual of the epilogue chain is added to the row chunks here
 // (the chain up to it was applied to q without it; the same fp16 adds, so the same bits). LDS instructions of
 // one wavefront execute in order, so no barrier is involved.
-template <int TM, int TN, int FM, int FN, int NSLOT>
+template <int TM, int TN, int FM, int FN, int NSLOT, int SSTRIDE>
 __device__ __forceinline__ void store_wave_staged(const GemmArgs &a, const uint4 (&q)[FM][FN][2], uint32_t rbase, uint32_t cbase,
                                                   char *slots) {
     constexpr int CPRW = TN / 8, HALF = 32 * CPRW, STEPS = HALF / 64;
@@ -957,12 +957,12 @@ __device__ __forceinline__ void store_wave_staged(const GemmArgs &a, const uint4
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
                 const int lin = r32 * CPRW + 4 * j + 2 * p + g;
-                *(uint4 *)(slots + (lin / 64) * 4096 + (lin % 64) * 16) = q[i][j][p];
+                *(uint4 *)(slots + (lin / 64) * SSTRIDE + (lin % 64) * 16) = q[i][j][p];
             }
 #pragma unroll
         for (int u = 0; u < STEPS; ++u) {
             const int lin = u * 64 + lane, row = lin / CPRW, c = lin % CPRW;
-            uint4 v = *(const uint4 *)(slots + u * 4096 + lane * 16);
+            uint4 v = *(const uint4 *)(slots + u * SSTRIDE + lane * 16);
             if (a.res) v = make_uint4(sh_hadd2(v.x, rq[u].x), sh_hadd2(v.y, rq[u].y), sh_hadd2(v.z, rq[u].z), sh_hadd2(v.w, rq[u].w));
             const uint32_t gm = rbase + 32 * i + row, gn = cbase + 8 * c;
             if (gm < a.M && gn < a.N) *(uint4 *)(a.z + (uint64_t)gm * a.ldz + gn) = v;
@@ -1383,7 +1383,7 @@ __global__ __launch_bounds__(256, MINW) void k_gemm5(GemmArgs a) {
             // last reads were slice KT - NST's, finished before the barrier of a later slice
             sh_wait_vmcnt<0>();                      // this wavefront's tail DMAs have landed
             char *slots = (char *)smem + (size_t)(KT % NST) * C::STAGE + (size_t)wave * 1024;
-            store_wave_staged<TM, TN, FM, FN, C::LOADS>(a, qc, m0 + wm * TM, n0 + wn * TN, slots);
+            store_wave_staged<TM, TN, FM, FN, C::LOADS, 4096>(a, qc, m0 + wm * TM, n0 + wn * TN, slots);
         } else {
             store_all<BM, BN, FM, FN>(a, qc, m0, n0, wm, wn);
         }
@@ -1481,9 +1481,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void k_gemm6(GemmArgs a) {
     }
 
     // PRE: the bias row (and, for small per-wave blocks, the residual) loaded at the start of the last slice
-    constexpr bool PRE_B = PRE, PRE_RES = PRE && FM * FN <= 6;
+    // (unsplit tiles of up to 6 blocks per wavefront are stored through each wavefront's DMA slots, and the residual
+    // is added there: no early load; larger blocks leave no registers for the staging)
+    constexpr bool STAGED = !SPLIT && 4 * TN <= 64 * C::LOADS && FM * FN <= 6;
+    constexpr bool PRE_B = PRE, PRE_RES = PRE && FM * FN <= 6 && !STAGED;
     uint4 bq[PRE_B ? FN : 1][2], rq[PRE_RES ? FM : 1][PRE_RES ? FN : 1][2];
-    const bool pre_ok = !SPLIT && PRE_B && !a.accumulate && !(a.bias && a.bias_fp32) && (PRE_RES || !a.res);
+    const bool pre_ok = !SPLIT && PRE_B && !a.accumulate && !(a.bias && a.bias_fp32) && (PRE_RES || STAGED || !a.res);
     auto prefetch = [&]() {
 #pragma unroll
         for (int j = 0; j < (PRE_B ? FN : 0); ++j)
@@ -1582,7 +1585,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void k_gemm6(GemmArgs a) {
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j) zt_chunks<FM, FN>(acc, i, j, qc[i][j]);
-        const bool any = a.accumulate || (a.bias && !a.ln_stats) || a.res || a.act != SH_ACT_NONE;
+        const bool has_res = a.res && !STAGED;           // staged tiles add the residual to their row chunks
+        const bool any = a.accumulate || (a.bias && !a.ln_stats) || has_res || a.act != SH_ACT_NONE;
+        GemmArgs an = a;
+        if (STAGED) an.res = nullptr;
         if (any) {
 #pragma unroll
             for (int i = 0; i < FM; ++i) {
@@ -1596,7 +1602,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void k_gemm6(GemmArgs a) {
                         if (pre_ok && KT > 0) {
                             b0 = bq[PRE_B ? j : 0][p];
                             if constexpr (PRE_RES) rr = rq[i][j][p];
-                            else if (a.res) rr = *(const uint4 *)(a.res + (uint64_t)gmc * a.ldr + gc);
+                            else if (has_res) rr = *(const uint4 *)(a.res + (uint64_t)gmc * a.ldr + gc);
                         } else {
                             if (a.accumulate) zo = *(const uint4 *)(a.z + (uint64_t)gmc * a.ldz + gc);
                             if (a.bias && a.bias_fp32) {
@@ -1605,21 +1611,28 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void k_gemm6(GemmArgs a) {
                             } else if (a.bias) {
                                 b0 = *(const uint4 *)((const uint16_t *)a.bias + gc);
                             }
-                            if (a.res) rr = *(const uint4 *)(a.res + (uint64_t)gmc * a.ldr + gc);
+                            if (has_res) rr = *(const uint4 *)(a.res + (uint64_t)gmc * a.ldr + gc);
                         }
-                        qc[i][j][p] = epi_chain8(a, qc[i][j][p], zo, b0, b1, rr);
+                        qc[i][j][p] = epi_chain8(an, qc[i][j][p], zo, b0, b1, rr);
                     }
             }
         }
+        if constexpr (STAGED) {
+            // stage KT % NST holds no slice (only the clamped tail DMAs, each wavefront's into its own slots)
+            sh_wait_vmcnt<0>();                          // this wavefront's tail DMAs have landed
+            char *slots = (char *)smem + (size_t)(KT % NST) * C::STAGE + (size_t)wave * 1024;
+            store_wave_staged<TM, TN, FM, FN, C::LOADS, NT * 16>(a, qc, m0 + wm * TM, n0 + wn * TN, slots);
+        } else {
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
+            for (int i = 0; i < FM; ++i)
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
+                for (int j = 0; j < FN; ++j)
 #pragma unroll
-                for (int p = 0; p < 2; ++p) {
-                    const uint32_t gm = m0 + wm * TM + 32 * i + r32, gn = n0 + wn * TN + 32 * j + 16 * p + 8 * g;
-                    if (gm < a.M && gn < a.N) *(uint4 *)(a.z + (uint64_t)gm * a.ldz + gn) = qc[i][j][p];
-                }
+                    for (int p = 0; p < 2; ++p) {
+                        const uint32_t gm = m0 + wm * TM + 32 * i + r32, gn = n0 + wn * TN + 32 * j + 16 * p + 8 * g;
+                        if (gm < a.M && gn < a.N) *(uint4 *)(a.z + (uint64_t)gm * a.ldz + gn) = qc[i][j][p];
+                    }
+        }
     }
     sh_wait_vmcnt<0>();      // no DMA may still target this workgroup's LDS when it exits
 }
@@ -1780,6 +1793,9 @@ KCfg g_cfgs[] = {
     SH_KCFG6(128, 64, 2, 2, 32, 4, 2, false, true, 0.16f),
     SH_KCFG6(64, 128, 2, 2, 32, 4, 2, false, true, 0.16f),
     SH_KCFG6(128, 128, 2, 2, 32, 4, 2, true, true, 0.25f),
+    SH_KCFG5(128, 192, 32, 4, 2, 0.36f),        // two workgroups per CU with a deeper ring of 32-k slices
+    SH_KCFG5(128, 128, 64, 2, 2, 0.30f),
+    SH_KCFG5(128, 128, 32, 4, 2, 0.30f),
 };
 #undef SH_KCFG
 #undef SH_KCFG2
