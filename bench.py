@@ -44,6 +44,8 @@ def parse():
     ap.add_argument("--configs", action="store_true",
                     help="instead of the layer line: every BASELINE config on its own (time, parity, CPU oracle time), "
                          "one JSON line each")
+    ap.add_argument("--row-stats", action="store_true",
+                    help="fused layer with sh_row_stats before each folded GEMM (7 launches) instead of row partials")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the 12-layer stack and the S=1024 attention measurements")
     ap.add_argument("--library-gemm", action="store_true",
@@ -488,8 +490,20 @@ def main() -> int:
     x = torch.from_numpy(xh).cuda()
     out = torch.empty_like(x)
     enc = encoder.Encoder(D, F, H)
+    enc.row_partials = not args.row_stats
     lp = encoder.LayerParams.from_host(p)
-    step = enc.layer_fused if args.sequence == "fused" else enc.layer_reference
+    if args.sequence == "fused":
+        # one layer of the 12-layer stack as it runs there: each step reads the rows the previous step stored, and
+        # the row partials its FFN-down wrote (five launches); the first step starts with sh_row_stats
+        bufs, nstep = (x, out), [0]
+
+        def step(*_):
+            i = nstep[0]
+            nstep[0] += 1
+            enc.layer_fused(bufs[i % 2], bufs[(i + 1) % 2], lp, B, S, x_parts=i > 0)
+    else:
+        def step(*_):
+            enc.layer_reference(x, out, lp, B, S)
 
     if args.copy_calibration:
         src = torch.empty(256 << 20, dtype=torch.float16, device="cuda").fill_(1.0)

@@ -229,6 +229,14 @@ typedef struct {
      * fp32 row of N, and the bias must then be the fp32 row d (SH_BIAS_FP32). Rounded once to fp16. */
     uint64_t ln_stats;
     uint64_t ln_c;
+    /* Row partials (0: off): the GEMM also writes, for each stored row of Z and each 32 columns of it, the fp32 pair
+     * (sum s, M2 = sum (z - s / 32)^2) of the stored fp16 values to stats_out [M][N / 32] (N % 32 == 0, 16-byte
+     * aligned operands): the statistics the next GEMM's LayerNorm fold needs, without a pass over Z. That GEMM
+     * takes them with ln_stats = stats_out, ln_parts = N / 32 (its K / 32) and ln_eps, and forms mean and
+     * variance with Chan's pairwise combination; ln_parts = 0: ln_stats holds (mean, r) rows of sh_row_stats. */
+    uint64_t stats_out;
+    uint32_t ln_parts;
+    float ln_eps;
 } sh_gemm_epi;
 int sh_gemm_ex(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
                uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg, const sh_gemm_epi *epi);

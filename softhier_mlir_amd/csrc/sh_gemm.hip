@@ -52,14 +52,84 @@ struct GemmArgs {
     uint32_t tiles_m, tiles_n, splits;
     uint32_t accumulate, bias_fp32, act;
     uint32_t xcd_groups;         // > 1: XCD-aware block remap with this many XCDs (requires divisibility)
-    const float *ln_stats;       // LayerNorm fold (or null): (mu, r) per row, fp32 [M][2] ...
+    const float *ln_stats;       // LayerNorm fold (or null): (mu, r) per row, fp32 [M][2], or ln_parts partials ...
     const float *ln_c;           // ... and c per column (fp32 [N]); the fp32 bias row is then d
+    uint32_t ln_parts;           // > 0: ln_stats holds ln_parts (sum, M2) pairs of 32 columns per row (row_partials)
+    float ln_eps;                // ... and the statistics are formed with this eps
+    float *stats_out;            // or null: the (sum, M2) pairs of every 32 columns of each stored row, [M][N / 32]
 };
 
+// (mu, r = 1 / sqrt(var + eps)) of row gm for the LayerNorm fold: given (ln_parts == 0), or formed from the row's
+// ln_parts partials (s_b, M2_b) of 32 columns each (Chan, Golub and LeVeque, "Algorithms for computing the sample
+// variance", 1983): mu = sum s_b / n, M2 = sum_b (M2_b + 32 (s_b / 32 - mu)^2), var = M2 / n, n = 32 ln_parts,
+// sums in block order. Up to 32 partials (K <= 1024) are loaded at once into registers, 16 bytes per load, and
+// summed twice; more are read twice from memory. Every consumer (register epilogues, split-K reduction) forms the
+// statistics with this one function.
+__device__ __forceinline__ float2 ln_row(const GemmArgs &a, uint32_t gm) {
+    if (a.ln_parts == 0) return ((const float2 *)a.ln_stats)[gm];
+    const uint32_t P = a.ln_parts;
+    const float2 *pp = (const float2 *)a.ln_stats + (uint64_t)gm * P;
+    const float inv_n = 1.f / (32.f * (float)P);
+    float s = 0.f, m2 = 0.f;
+    if (P <= 32 && P % 2 == 0) {                     // no branches: absent blocks re-read the last one, weight 0
+        const uint32_t last = P / 2 - 1;
+        float4 q[16];
+        float wgt[16];
+#pragma unroll
+        for (int h = 0; h < 16; ++h) {
+            q[h] = ((const float4 *)pp)[min((uint32_t)h, last)];
+            wgt[h] = (uint32_t)h <= last ? 1.f : 0.f;
+        }
+#pragma unroll
+        for (int h = 0; h < 16; ++h) s = fmaf(wgt[h], q[h].x + q[h].z, s);
+        const float mu = s * inv_n;
+#pragma unroll
+        for (int h = 0; h < 16; ++h) {
+            const float d0 = fmaf(q[h].x, 1.f / 32.f, -mu), d1 = fmaf(q[h].z, 1.f / 32.f, -mu);
+            m2 = fmaf(wgt[h], fmaf(32.f * d0, d0, q[h].y) + fmaf(32.f * d1, d1, q[h].w), m2);
+        }
+        return make_float2(mu, sh_fast_rsq(fmaf(m2, inv_n, a.ln_eps)));
+    }
+    for (uint32_t b = 0; b < P; b += 2) s += pp[b].x + (b + 1 < P ? pp[b + 1].x : 0.f);
+    const float mu = s * inv_n;
+    for (uint32_t b = 0; b < P; b += 2) {
+        const float2 q0 = pp[b], q1 = b + 1 < P ? pp[b + 1] : make_float2(32.f * mu, 0.f);
+        const float d0 = fmaf(q0.x, 1.f / 32.f, -mu), d1 = fmaf(q1.x, 1.f / 32.f, -mu);
+        m2 += fmaf(32.f * d0, d0, q0.y) + fmaf(32.f * d1, d1, q1.y);
+    }
+    return make_float2(mu, sh_fast_rsq(fmaf(m2, inv_n, a.ln_eps)));
+}
+
+// A wavefront's rows' fold factors (r and r mu of rows mrow + 32 i + r32), formed once at the start of a tile so
+// the loads overlap its first DMAs and the epilogue waits on nothing: lane l forms rows mrow + l + 64 k, and each
+// lane takes its rows' factors from those lanes.
+template <int FM>
+struct LnRows { float r[FM], rm[FM]; };
+template <int FM>
+__device__ __forceinline__ LnRows<FM> ln_rows(const GemmArgs &a, uint32_t mrow) {
+    constexpr int RPL = (FM + 1) / 2;                // rows formed per lane
+    LnRows<FM> l;
+    const int lane = threadIdx.x & 63, r32 = lane & 31;
+    if (!a.ln_stats) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) { l.r[i] = 0.f; l.rm[i] = 0.f; }
+        return l;
+    }
+    float2 st[RPL];
+#pragma unroll
+    for (int k = 0; k < RPL; ++k) st[k] = ln_row(a, min(mrow + 64 * k + lane, a.M - 1));
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {                   // row 32 i + r32 was formed by lane 32 (i % 2) + r32, k = i / 2
+        const float mu = __shfl(st[i / 2].x, 32 * (i % 2) + r32, 64), r = __shfl(st[i / 2].y, 32 * (i % 2) + r32, 64);
+        l.r[i] = r;
+        l.rm[i] = mu * r;
+    }
+    return l;
+}
+
 // LayerNorm folded into the product (sh_gemm_epi.ln_stats): p -> r p - (r mu) c + d in fp32, before the fp16
-// rounding; the bias (d) is part of this step, so the chain below skips it.
-__device__ __forceinline__ float ln_apply(const GemmArgs &a, float p, uint32_t gm, uint32_t gn) {
-    const float2 st = ((const float2 *)a.ln_stats)[gm];
+// rounding; the bias (d) is part of this step, so the chain below skips it. st = ln_row(a, gm).
+__device__ __forceinline__ float ln_apply(const GemmArgs &a, float2 st, float p, uint32_t gn) {
     return fmaf(st.y, p, fmaf(-(st.x * st.y), a.ln_c[gn], ((const float *)a.bias)[gn]));
 }
 
@@ -788,18 +858,12 @@ __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
     return (uint32_t)sh_dev_f2h(lo) | ((uint32_t)sh_dev_f2h(hi) << 16);
 }
 
-// The LayerNorm fold on a wavefront's Z^T accumulators (block (i, j) of lane l: row mrow + 32 i + l % 32,
-// columns ncol + 32 j + 8 q + 4 g + e in register 4 q + e), in place, before they are rounded.
+// The LayerNorm fold on a wavefront's Z^T accumulators (block (i, j) of lane l: the row of ln's entry i, columns
+// ncol + 32 j + 8 q + 4 g + e in register 4 q + e), in place, before they are rounded.
 template <int FM, int FN>
-__device__ __forceinline__ void ln_fold_zt(const GemmArgs &a, sh_f16v (&acc)[FM][FN], uint32_t mrow, uint32_t ncol) {
-    const int lane = threadIdx.x & 63, g = lane >> 5, r32 = lane & 31;
-    float rr[FM], rm[FM];
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-        const float2 st = ((const float2 *)a.ln_stats)[min(mrow + 32 * i + r32, a.M - 1)];
-        rr[i] = st.y;
-        rm[i] = st.x * st.y;
-    }
+__device__ __forceinline__ void ln_fold_zt(const GemmArgs &a, sh_f16v (&acc)[FM][FN], const LnRows<FM> &ln, uint32_t ncol) {
+    const int lane = threadIdx.x & 63, g = lane >> 5;
+    const float *rr = ln.r, *rm = ln.rm;
     const float *d = (const float *)a.bias;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
@@ -815,6 +879,43 @@ __device__ __forceinline__ void ln_fold_zt(const GemmArgs &a, sh_f16v (&acc)[FM]
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(rr[i], acc[i][j][r], fmaf(-rm[i], cj[r], dj[r]));
+    }
+}
+
+// Row partials of a wavefront's finished chunks (Z^T layout: chunk (i, j, p) of a lane is row rbase + 32 i + r32,
+// columns cbase + 32 j + 16 p + 8 g): for each row and each 32-column block, the sum s of its 32 stored fp16 values
+// and M2 = sum (v - s / 32)^2 (two passes in fp32; lanes g = 0, 1 hold 16 values each), written as a float2 to
+// stats_out[row][block] (the consumer combines a row's blocks with ln_row). Stores the same bits in every
+// register-epilogue tile (the same 32 values, the same order).
+template <int FM, int FN>
+__device__ __forceinline__ void stats_zt(const GemmArgs &a, const uint4 (&q)[FM][FN][2], uint32_t rbase, uint32_t cbase) {
+    const int lane = threadIdx.x & 63, g = lane >> 5, r32 = lane & 31;
+    const uint32_t P = a.N / 32;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const uint32_t row = rbase + 32 * i + r32;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            float x[16], sum = 0.f;
+#pragma unroll
+            for (int p = 0; p < 2; ++p)
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const sh_h2 h = __builtin_bit_cast(sh_h2, comp(q[i][j][p], w));
+                    x[8 * p + 2 * w] = (float)h.x;
+                    x[8 * p + 2 * w + 1] = (float)h.y;
+                }
+#pragma unroll
+            for (int e = 0; e < 16; ++e) sum += x[e];
+            sum += __shfl_xor(sum, 32, 64);
+            const float mb = sum * (1.f / 32.f);
+            float m2 = 0.f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) { const float d = x[e] - mb; m2 = fmaf(d, d, m2); }
+            m2 += __shfl_xor(m2, 32, 64);
+            const uint32_t col = cbase + 32 * j;
+            if (g == 0 && row < a.M && col < a.N) ((float2 *)a.stats_out)[(uint64_t)row * P + col / 32] = make_float2(sum, m2);
+        }
     }
 }
 
@@ -905,8 +1006,8 @@ __device__ __forceinline__ void chain_chunks(const GemmArgs &a, uint4 (&q)[FM][F
 // Accumulators (Z^T layout) -> fp16 chunks with the epilogue chain applied.
 template <int BM, int BN, int FM, int FN>
 __device__ __forceinline__ void finish_chunks(const GemmArgs &a, sh_f16v (&acc)[FM][FN], uint32_t m0, uint32_t n0,
-                                              uint4 (&q)[FM][FN][2], int wm, int wn) {
-    if (a.ln_stats) ln_fold_zt<FM, FN>(a, acc, m0 + wm * (BM / 2), n0 + wn * (BN / 2));
+                                              uint4 (&q)[FM][FN][2], int wm, int wn, const LnRows<FM> &ln) {
+    if (a.ln_stats) ln_fold_zt<FM, FN>(a, acc, ln, n0 + wn * (BN / 2));
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -1111,6 +1212,7 @@ __global__ __launch_bounds__(NT, MINW) void k_gemm4(GemmArgs a) {
             }
     };
 
+    const LnRows<FM> lnw = ln_rows<FM>(a, m0 + wm * C::TM);   // (before the first DMAs: no wait on them)
     // prologue: slices 0 .. STAGES-2 (past the end: the last slice again, into stages nobody reads), so every
     // iteration waits for a constant number of outstanding DMAs
     if (KT > 0) {
@@ -1147,7 +1249,8 @@ __global__ __launch_bounds__(NT, MINW) void k_gemm4(GemmArgs a) {
             store_partials_zt<BM, BN, FM, FN>(a, acc, m0, n0, split, wm, wn);
         } else {
             uint4 q[FM][FN][2];
-            finish_chunks<BM, BN, FM, FN>(a, acc, m0, n0, q, wm, wn);
+            finish_chunks<BM, BN, FM, FN>(a, acc, m0, n0, q, wm, wn, lnw);
+            if (a.stats_out) stats_zt<FM, FN>(a, q, m0 + wm * (BM / 2), n0 + wn * (BN / 2));
             store_all<BM, BN, FM, FN>(a, q, m0, n0, wm, wn);
         }
         sh_wait_vmcnt<0>();     // no DMA may still target this workgroup's LDS when it exits
@@ -1292,7 +1395,9 @@ __global__ __launch_bounds__(256, MINW) void k_gemm5(GemmArgs a) {
     constexpr bool STAGED = !SPLIT && 4 * TN <= 64 * C::LOADS;
     constexpr bool PRE_B = PRE && FM * FN <= 12, PRE_RES = PRE && FM * FN <= 6 && !STAGED;
     uint4 bq[PRE_B ? FN : 1][2], rq[PRE_RES ? FM : 1][PRE_RES ? FN : 1][2];
-    const bool pre_ok = PRE_B && !a.accumulate && !(a.bias && a.bias_fp32) && (PRE_RES || STAGED || !a.res);
+    // (a GEMM that also writes row partials adds the residual in the chain, before them)
+    const bool stage_res = STAGED && !a.stats_out;
+    const bool pre_ok = PRE_B && !a.accumulate && !(a.bias && a.bias_fp32) && (PRE_RES || stage_res || !a.res);
     auto prefetch = [&]() {
 #pragma unroll
         for (int j = 0; j < (PRE_B ? FN : 0); ++j)
@@ -1316,6 +1421,7 @@ __global__ __launch_bounds__(256, MINW) void k_gemm5(GemmArgs a) {
         }
     };
 
+    const LnRows<FM> lnw = ln_rows<FM>(a, m0 + wm * TM);      // (before the first DMAs: no wait on them)
     if (KT > 0) {
 #pragma unroll
         for (int s = 0; s < NST - 1; ++s)
@@ -1356,14 +1462,14 @@ __global__ __launch_bounds__(256, MINW) void k_gemm5(GemmArgs a) {
     if constexpr (SPLIT) {
         store_partials_zt<BM, BN, FM, FN>(a, acc, m0, n0, split, wm, wn);
     } else {
-        if (a.ln_stats) ln_fold_zt<FM, FN>(a, acc, m0 + wm * TM, n0 + wn * TN);
+        if (a.ln_stats) ln_fold_zt<FM, FN>(a, acc, lnw, n0 + wn * TN);
         uint4 qc[FM][FN][2];
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j) zt_chunks<FM, FN>(acc, i, j, qc[i][j]);
         GemmArgs an = a;
-        if (STAGED) an.res = nullptr;                // the residual is added to the staged row chunks
+        if (stage_res) an.res = nullptr;             // the residual is added to the staged row chunks
         if (PRE_B && pre_ok && KT > 0) {
             if (an.bias || an.res || an.act != SH_ACT_NONE) {
 #pragma unroll
@@ -1378,12 +1484,15 @@ __global__ __launch_bounds__(256, MINW) void k_gemm5(GemmArgs a) {
         } else {
             chain_chunks<BM, BN, FM, FN>(an, qc, m0, n0, wm, wn);
         }
+        if (a.stats_out) stats_zt<FM, FN>(a, qc, m0 + wm * TM, n0 + wn * TN);
         if constexpr (STAGED) {
             // stage KT % NST holds no slice (only the clamped tail DMAs, each wavefront's into its own slots); its
             // last reads were slice KT - NST's, finished before the barrier of a later slice
             sh_wait_vmcnt<0>();                      // this wavefront's tail DMAs have landed
             char *slots = (char *)smem + (size_t)(KT % NST) * C::STAGE + (size_t)wave * 1024;
-            store_wave_staged<TM, TN, FM, FN, C::LOADS, 4096>(a, qc, m0 + wm * TM, n0 + wn * TN, slots);
+            GemmArgs as = a;
+            if (!stage_res) as.res = nullptr;        // already added in the chain
+            store_wave_staged<TM, TN, FM, FN, C::LOADS, 4096>(as, qc, m0 + wm * TM, n0 + wn * TN, slots);
         } else {
             store_all<BM, BN, FM, FN>(a, qc, m0, n0, wm, wn);
         }
@@ -1486,7 +1595,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void k_gemm6(GemmArgs a) {
     constexpr bool STAGED = !SPLIT && 4 * TN <= 64 * C::LOADS && FM * FN <= 6;
     constexpr bool PRE_B = PRE, PRE_RES = PRE && FM * FN <= 6 && !STAGED;
     uint4 bq[PRE_B ? FN : 1][2], rq[PRE_RES ? FM : 1][PRE_RES ? FN : 1][2];
-    const bool pre_ok = !SPLIT && PRE_B && !a.accumulate && !(a.bias && a.bias_fp32) && (PRE_RES || STAGED || !a.res);
+    const bool stage_res = STAGED && !a.stats_out;       // (row partials need the residual in the chain)
+    const bool pre_ok = !SPLIT && PRE_B && !a.accumulate && !(a.bias && a.bias_fp32) && (PRE_RES || stage_res || !a.res);
     auto prefetch = [&]() {
 #pragma unroll
         for (int j = 0; j < (PRE_B ? FN : 0); ++j)
@@ -1510,6 +1620,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void k_gemm6(GemmArgs a) {
         }
     };
 
+    const LnRows<FM> lnw = ln_rows<FM>(a, m0 + wm * TM);      // (before the first DMAs: no wait on them)
     if (KT > 0) {
 #pragma unroll
         for (int s = 0; s < NST - 1; ++s)
@@ -1579,16 +1690,18 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void k_gemm6(GemmArgs a) {
                             make_float4(acc[i][j][4 * u], acc[i][j][4 * u + 1], acc[i][j][4 * u + 2], acc[i][j][4 * u + 3]);
                 }
     } else {
-        if (a.ln_stats) ln_fold_zt<FM, FN>(a, acc, m0 + wm * TM, n0 + wn * TN);
+        if constexpr (FM * FN <= 6) {                    // (the configurations that apply the fold unsplit)
+            if (a.ln_stats) ln_fold_zt<FM, FN>(a, acc, lnw, n0 + wn * TN);
+        }
         uint4 qc[FM][FN][2];
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j) zt_chunks<FM, FN>(acc, i, j, qc[i][j]);
-        const bool has_res = a.res && !STAGED;           // staged tiles add the residual to their row chunks
+        const bool has_res = a.res && !stage_res;        // staged tiles add the residual to their row chunks
         const bool any = a.accumulate || (a.bias && !a.ln_stats) || has_res || a.act != SH_ACT_NONE;
         GemmArgs an = a;
-        if (STAGED) an.res = nullptr;
+        if (stage_res) an.res = nullptr;
         if (any) {
 #pragma unroll
             for (int i = 0; i < FM; ++i) {
@@ -1617,11 +1730,16 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void k_gemm6(GemmArgs a) {
                     }
             }
         }
+        if constexpr (FM * FN <= 6) {                    // (larger blocks: no registers left; never chosen for them)
+            if (a.stats_out) stats_zt<FM, FN>(a, qc, m0 + wm * TM, n0 + wn * TN);
+        }
         if constexpr (STAGED) {
             // stage KT % NST holds no slice (only the clamped tail DMAs, each wavefront's into its own slots)
             sh_wait_vmcnt<0>();                          // this wavefront's tail DMAs have landed
             char *slots = (char *)smem + (size_t)(KT % NST) * C::STAGE + (size_t)wave * 1024;
-            store_wave_staged<TM, TN, FM, FN, C::LOADS, NT * 16>(a, qc, m0 + wm * TM, n0 + wn * TN, slots);
+            GemmArgs as = a;
+            if (!stage_res) as.res = nullptr;            // already added in the chain
+            store_wave_staged<TM, TN, FM, FN, C::LOADS, NT * 16>(as, qc, m0 + wm * TM, n0 + wn * TN, slots);
         } else {
 #pragma unroll
             for (int i = 0; i < FM; ++i)
@@ -1679,11 +1797,26 @@ __global__ __launch_bounds__(64) void k_splitk_reduce(GemmArgs a, ShDiv div, uin
     }
     uint16_t out[W];
     if (a.ln_stats) {
+        const float2 st = ln_row(a, gm);
 #pragma unroll
-        for (int e = 0; e < W; ++e) v[e] = ln_apply(a, v[e], gm, gn + e);
+        for (int e = 0; e < W; ++e) v[e] = ln_apply(a, st, v[e], gn + e);
     }
 #pragma unroll
     for (int e = 0; e < W; ++e) out[e] = epi_chain(a, sh_dev_f2h(v[e]), gm, gn + e);
+    if (VEC && a.stats_out) {                        // 4 consecutive threads hold the 32 columns of one partial
+        float x[W], sum = 0.f;
+#pragma unroll
+        for (int e = 0; e < W; ++e) { x[e] = sh_dev_h2f(out[e]); sum += x[e]; }
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        const float mb = sum * (1.f / 32.f);
+        float m2 = 0.f;
+#pragma unroll
+        for (int e = 0; e < W; ++e) { const float d = x[e] - mb; m2 = fmaf(d, d, m2); }
+        m2 += __shfl_xor(m2, 1, 64);
+        m2 += __shfl_xor(m2, 2, 64);
+        if ((cc & 3) == 0) ((float2 *)a.stats_out)[(uint64_t)gm * (a.N / 32) + cc / 4] = make_float2(sum, m2);
+    }
     if (VEC) {
         uint32_t w4[4];
 #pragma unroll
@@ -1704,7 +1837,7 @@ struct KCfg {
     int bm, bn, stages; bool v2; KernelFn vec[2], scalar[2]; size_t lds; float eff; bool attr_set; int threads = 256;
     bool ktail = false; KernelFn tail[2] = {nullptr, nullptr};     // the K % 64 != 0 variants (unsplit, split)
     bool wt = false; KernelFn wt_vec[2] = {nullptr, nullptr}, wt_scalar[2] = {nullptr, nullptr};
-    bool reg = false;            // the unsplit kernel's epilogue works on the fp32 accumulators (the LayerNorm fold)
+    bool reg = false;            // the unsplit epilogue applies a LayerNorm fold and writes row partials from registers
 };
 
 #define SH_KCFG(BM, BN, EFF) { BM, BN, 2, false, { k_gemm<BM, BN, true, false>, k_gemm<BM, BN, true, true> }, \
@@ -1715,7 +1848,7 @@ struct KCfg {
 #define SH_KCFG6(BM, BN, WGM, WGN, SK, NST, W, PRE, DB, EFF) \
     { BM, BN, NST, true, { k_gemm6<BM, BN, WGM, WGN, SK, NST, W, false, PRE, DB>, k_gemm6<BM, BN, WGM, WGN, SK, NST, W, true, PRE, DB> }, \
       { nullptr, nullptr }, Cfg6<BM, BN, WGM, WGN, SK, NST>::LDS, EFF, false, 64 * WGM * WGN, false, { nullptr, nullptr }, true, \
-      { nullptr, nullptr }, { nullptr, nullptr }, true }
+      { nullptr, nullptr }, { nullptr, nullptr }, Cfg6<BM, BN, WGM, WGN, SK, NST>::FM * Cfg6<BM, BN, WGM, WGN, SK, NST>::FN <= 6 }
 #define SH_KCFG2(BM, BN, ST, EFF) { BM, BN, ST, true, { k_gemm2<BM, BN, ST, false>, k_gemm2<BM, BN, ST, true> }, \
                                     { nullptr, nullptr }, Cfg2<BM, BN, ST>::LDS, EFF, false, 256, true, \
                                     { k_gemm2<BM, BN, ST, false, true>, k_gemm2<BM, BN, ST, true, true> } }
@@ -1863,7 +1996,7 @@ bool eligible(const KCfg &c, bool vec, bool fast, bool ktail, bool wt, bool reg_
     return vec || c.bm * c.bn <= 128 * 128;
 }
 
-// reg_only: only configurations whose unsplit epilogue works on fp32 accumulators (a LayerNorm fold); if none is
+// reg_only: only configurations whose unsplit epilogue applies a LayerNorm fold and writes row partials; if none is
 // eligible the plan falls back to the unrestricted choice and the launch goes through the partials path.
 Plan choose(uint32_t M, uint32_t N, uint32_t K, bool vec, bool fast, uint32_t want_splits, bool wt = false, bool reg_only = false) {
     const bool ktail = vec && K > 0 && K % BK != 0;
@@ -1963,7 +2096,7 @@ void tune_file_append(const TuneKey &k, int cfg) {
 }
 
 int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st, bool wt) {
-    const bool reg_only = call.ln_stats != nullptr;
+    const bool reg_only = call.ln_stats != nullptr || call.stats_out != nullptr;
     static const int enabled = env_int("SH_GEMM_TUNE", 1);
     if (!enabled || env_int("SH_GEMM_CFG", -1) >= 0) return heur;
     const int cus = sh_num_cus() > 0 ? sh_num_cus() : 256;
@@ -2061,24 +2194,36 @@ int launch(const GemmReq &r, const char *name) {
                      sh_aligned16(r.x) && sh_aligned16(r.w) && sh_aligned16(r.z) &&
                      (!res || (ldr % 8 == 0 && sh_aligned16(res))) && (!bias || sh_aligned16(bias));
     const bool fast = vec && r.K % BK == 0 && r.K > 0;
-    // LayerNorm fold: the unsplit kernels that apply it on their fp32 accumulators need 16-byte aligned c / d rows;
-    // every other case goes through the fp32 partials (one K range or more) and the reduction applies it
+    // LayerNorm fold and row partials: the unsplit kernels that apply the fold on their fp32 accumulators (16-byte
+    // aligned c / d rows) and write the partials from their registers; every other case goes through the fp32
+    // partials (one K range or more) and the reduction does both
     const bool ln = e && e->ln_stats;
+    const bool stats = e && e->stats_out;
+    if (stats && (!vec || r.N % 32 != 0)) {
+        sh_set_error(-1, "[%s] row partials need N %% 32 == 0 and 16-byte aligned operands and leading dims", name);
+        return -1;
+    }
     const bool ln_reg = ln && fast && sh_aligned16(e->ln_c) && sh_aligned16(bias);
-    Plan p = choose(r.M, r.N, r.K, vec, fast, r.splits, r.wt, ln_reg);
+    const bool want_reg = (ln || stats) && fast && (!ln || ln_reg);
+    Plan p = choose(r.M, r.N, r.K, vec, fast, r.splits, r.wt, want_reg);
     if (r.mesh) p.splits = 1;
-    if (fast && p.splits == 1 && g_cfgs[p.cfg].v2 && !r.part && (!ln || (ln_reg && g_cfgs[p.cfg].reg))) {
+    auto set_epi = [&](GemmArgs &t) {
+        t.ln_stats = ln ? (const float *)e->ln_stats : nullptr; t.ln_c = ln ? (const float *)e->ln_c : nullptr;
+        t.ln_parts = ln ? e->ln_parts : 0; t.ln_eps = ln ? e->ln_eps : 0.f;
+        t.stats_out = stats ? (float *)e->stats_out : nullptr;
+    };
+    if (fast && p.splits == 1 && g_cfgs[p.cfg].v2 && !r.part && (!(ln || stats) || (want_reg && g_cfgs[p.cfg].reg))) {
         GemmArgs t{};
         t.x = (const uint16_t *)r.x; t.w = (const uint16_t *)r.w; t.bias = (const void *)bias;
         t.ldx = r.ldx; t.ldw = r.ldw; t.M = r.M; t.N = r.N; t.K = r.K; t.kps = sh_cdiv(r.K, BK) * BK; t.splits = 1;
         t.bias_fp32 = (e && e->bias_fmt == SH_BIAS_FP32) ? 1 : 0; t.act = e ? e->act : 0;
-        t.ln_stats = ln ? (const float *)e->ln_stats : nullptr; t.ln_c = ln ? (const float *)e->ln_c : nullptr;
+        set_epi(t);
         p.cfg = tuned_cfg(t, p.cfg, sh_stream(), r.wt);
     }
     KCfg &c = g_cfgs[p.cfg];
     const SplitK sk = split_k(r.K, p.splits);
     const uint32_t splits = sk.splits, kps = sk.kps;
-    const bool partials = splits > 1 || (ln && !(ln_reg && c.reg));
+    const bool partials = splits > 1 || ((ln || stats) && !(want_reg && c.reg));
 
     GemmArgs a{};
     a.x = (const uint16_t *)r.x; a.w = (const uint16_t *)r.w; a.z = (uint16_t *)r.z;
@@ -2087,7 +2232,7 @@ int launch(const GemmReq &r, const char *name) {
     a.M = r.M; a.N = r.N; a.K = r.K; a.kps = kps;
     a.tiles_m = sh_cdiv(r.M, c.bm); a.tiles_n = sh_cdiv(r.N, c.bn); a.splits = splits;
     a.accumulate = r.accumulate; a.bias_fp32 = (e && e->bias_fmt == SH_BIAS_FP32) ? 1 : 0; a.act = e ? e->act : 0;
-    a.ln_stats = ln ? (const float *)e->ln_stats : nullptr; a.ln_c = ln ? (const float *)e->ln_c : nullptr;
+    set_epi(a);
     const uint64_t nblk64 = (uint64_t)a.tiles_m * a.tiles_n * splits;
     if (nblk64 > 0x7FFFFFFFull) { sh_set_error(-1, "[%s] problem too large", name); return -1; }
     const uint32_t nblk = grid_of(a);
@@ -2127,14 +2272,21 @@ int launch(const GemmReq &r, const char *name) {
 }
 
 // The LayerNorm fold's arguments: both rows given, the bias is the fp32 row d, and no accumulate (z_old would
-// be added after the fold's rounding point, which no unfused sequence does).
-int check_ln(const char *name, const sh_gemm_epi *e, const sh_gemm_cfg &c) {
+// be added after the fold's rounding point, which no unfused sequence does); partial statistics cover the K
+// columns the fold normalises. Row partials go to an 8-byte aligned [M][N / 32] pair array.
+int check_ln(const char *name, const sh_gemm_epi *e, const sh_gemm_cfg &c, uint32_t K) {
+    if (e && e->stats_out % 8) { sh_set_error(-1, "[%s] stats_out must be 8-byte aligned", name); return -1; }
     if (!e || (!e->ln_stats && !e->ln_c)) return 0;
     if (!e->ln_stats || !e->ln_c || !e->bias || e->bias_fmt != SH_BIAS_FP32 || c.accumulate) {
         sh_set_error(-1, "[%s] LayerNorm fold needs ln_stats, ln_c and the fp32 bias row d, without accumulate", name);
         return -1;
     }
     if ((e->ln_stats | e->ln_c | e->bias) % 4) { sh_set_error(-1, "[%s] LayerNorm fold rows must be 4-byte aligned", name); return -1; }
+    if (e->ln_parts && (uint64_t)e->ln_parts * 32 != K) {
+        sh_set_error(-1, "[%s] %u row partials of 32 columns do not cover K = %u", name, e->ln_parts, K);
+        return -1;
+    }
+    if (e->ln_parts && !(e->ln_eps >= 0.f)) { sh_set_error(-1, "[%s] ln_eps must be >= 0", name); return -1; }
     return 0;
 }
 
@@ -2237,7 +2389,7 @@ int sh_gemm_ex(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint3
     if (c.fmt != SH_FP16) { sh_set_error(-1, "[sh_gemm_ex] fmt %u: only SH_FP16 is implemented", c.fmt); return -1; }
     if (epi && epi->residual && epi->ldr < N) { sh_set_error(-1, "[sh_gemm_ex] ldr %u < N %u", epi->ldr, N); return -1; }
     if (epi && epi->act > SH_ACT_GELU) { sh_set_error(-1, "[sh_gemm_ex] unknown act %u", epi->act); return -1; }
-    if (int rc = check_ln("sh_gemm_ex", epi, c)) return rc;
+    if (int rc = check_ln("sh_gemm_ex", epi, c, K)) return rc;
     GemmReq r{x, w, z, M, N, K, ldx, ldw, ldz, c.accumulate, epi, epi ? epi->splits : 1u, false};
     return launch(r, "sh_gemm_ex");
 }
@@ -2251,7 +2403,7 @@ int sh_gemm_ex_wt(uint64_t x, uint64_t wt, uint64_t z, uint32_t M, uint32_t N, u
     if (ldwt < K) { sh_set_error(-1, "[sh_gemm_ex_wt] ldwt %u < K %u", ldwt, K); return -1; }
     if (epi && epi->residual && epi->ldr < N) { sh_set_error(-1, "[sh_gemm_ex_wt] ldr %u < N %u", epi->ldr, N); return -1; }
     if (epi && epi->act > SH_ACT_GELU) { sh_set_error(-1, "[sh_gemm_ex_wt] unknown act %u", epi->act); return -1; }
-    if (int rc = check_ln("sh_gemm_ex_wt", epi, c)) return rc;
+    if (int rc = check_ln("sh_gemm_ex_wt", epi, c, K)) return rc;
     GemmReq r{x, wt, z, M, N, K, ldx, ldwt, ldz, c.accumulate, epi, epi ? epi->splits : 1u, false};
     r.wt = true;
     return launch(r, "sh_gemm_ex_wt");

@@ -11,11 +11,14 @@ sequence, sh_add, sh_gelu). `sequence="fused"` computes the same layer with the 
 one QKV GEMM against the concatenated [D, 3D] weight with the bias in its epilogue, one batched attention
 over q/k/v views of the QKV buffer (ld = 3D), and GEMM epilogues that add the bias, apply GELU or add the
 residual, which removes five row-op round trips through HBM. Each LayerNorm is folded into the GEMM that reads
-it: sh_row_stats writes the rows' (mean, 1/sqrt(var + eps)) (8 bytes a row instead of the normalised row), the
-GEMM multiplies the raw rows by W' = r16(gamma W) and its epilogue forms r (x W') - r mu c + d with c = 1^T W',
-d = beta^T W + b (sh_ln_fold, once per weight), which is LN(x) W + b. Both sequences match the numpy oracle
-within the fp16 tolerance (the fused epilogues round once where the reference rounds twice, and the fold rounds
-gamma W where the reference rounds LN(x)).
+it: the GEMM multiplies the raw rows by W' = r16(gamma W) and its epilogue forms r (x W') - r mu c + d with
+c = 1^T W', d = beta^T W + b (sh_ln_fold, once per weight), which is LN(x) W + b. The row statistics (mu, r) come
+from the GEMM that stored the rows: out-proj and FFN-down write (sum, M2) pairs of every 32 columns of each output
+row from their registers (sh_gemm_epi.stats_out), and the next QKV / FFN-up GEMM combines them. So a layer of
+the stack is five launches (QKV, attention, out-proj, FFN-up, FFN-down); a layer whose input has no such
+partials (the first) starts with sh_row_stats. Both sequences match the numpy oracle within the fp16 tolerance
+(the fused epilogues round once where the reference rounds twice, and the fold rounds gamma W where the reference
+rounds LN(x)).
 
 Buffers are torch tensors (allocation only); every computation is a libshops.so call.
 """
@@ -82,6 +85,7 @@ class Encoder:
         self._pingpong: torch.Tensor | None = None   # the stack's second activation buffer (outside _bufs)
         self._plans: dict = {}               # fused-layer call lists by argument set (a stack has one per layer)
         self.gemm_cfg = shops.cfg()          # tile hints 256^3 (library default), as the reference's default policy
+        self.row_partials = True             # False: sh_row_stats before each folded GEMM (seven launches a layer)
         self.tap = None                      # optional tap(name) -> context manager around each op (timing)
 
     def _op(self, name: str):
@@ -95,7 +99,9 @@ class Encoder:
             self._bufs = {"rows": rows, "ln1": z(D), "qkv": z(3 * D), "q": z(D), "k": z(D), "v": z(D), "o": z(D),
                           "ao": z(D), "h": z(D), "ln2": z(D), "f1": z(F), "g": z(F), "f2": z(D),
                           "st1": torch.empty((rows, 2), dtype=torch.float32, device=self.device),
-                          "st2": torch.empty((rows, 2), dtype=torch.float32, device=self.device)}
+                          "st2": torch.empty((rows, 2), dtype=torch.float32, device=self.device),
+                          "pst_x": torch.empty((rows, D // 32, 2), dtype=torch.float32, device=self.device),
+                          "pst_h": torch.empty((rows, D // 32, 2), dtype=torch.float32, device=self.device)}
         return self._bufs
 
     # -- the reference's call sequence (siglip.py:133-168) ------------------------------------------------
@@ -127,10 +133,12 @@ class Encoder:
         return out
 
     # -- fused sequence (additive entry points) ------------------------------------------------------------
-    def _fused_plan(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int) -> list:
-        """The layer's library calls with every argument converted once: (op name, function, args, what)."""
+    def _fused_plan(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int, x_parts: bool) -> list:
+        """The layer's library calls with every argument converted once: (op name, function, args, what).
+        x_parts: the row partials of x are in the `pst_x` buffer (written by the GEMM that stored x)."""
         p.fold(self.lib)
-        key = (x.data_ptr(), out.data_ptr(), B, S) + tuple(t.data_ptr() for t in p.t.values())
+        x_parts = x_parts and self.row_partials
+        key = (x.data_ptr(), out.data_ptr(), B, S, x_parts, self.row_partials) + tuple(t.data_ptr() for t in p.t.values())
         hit = self._plans.get(key)
         if hit is not None:
             return hit
@@ -141,29 +149,47 @@ class Encoder:
         D3 = 3 * D
         qkv = b["qkv"]
         F32 = shops.SH_BIAS_FP32
-        calls = [
-            ("ln1", L.sh_row_stats, (A(b["st1"]), A(x), rows, D, D, self.eps), None),
+        parts = D // 32
+        sp = (lambda t: A(t)) if self.row_partials else (lambda t: 0)  # noqa: E731  (row partials written or not)
+        calls = []
+        if x_parts:
+            ln1 = dict(ln_stats=A(b["pst_x"]), ln_parts=parts, ln_eps=self.eps)
+        else:
+            calls.append(("ln1", L.sh_row_stats, (A(b["st1"]), A(x), rows, D, D, self.eps), None))
+            ln1 = dict(ln_stats=A(b["st1"]))
+        calls += [
             ("qkv", L.sh_gemm_ex, (A(x), A(p["wqkv_ln"]), A(qkv), rows, D3, D, D, D3, D3, cfg,
-                                   shops.epi(bias=A(p["dqkv"]), bias_fmt=F32, ln_stats=A(b["st1"]), ln_c=A(p["cqkv"]))),
+                                   shops.epi(bias=A(p["dqkv"]), bias_fmt=F32, ln_c=A(p["cqkv"]), **ln1)),
              "sh_gemm_ex qkv"),
             ("attention", L.sh_attention_batched, (A(qkv), A(qkv, D), A(qkv, 2 * D), A(b["o"]), B, S, D, H, D3, D3, D3, D,
                                                    S * D3, S * D3, S * D3, S * D, 1.0 / math.sqrt(D // H), 0), "sh_attention_batched"),
             ("out_proj", L.sh_gemm_ex, (A(b["o"]), A(p["wo"]), A(b["h"]), rows, D, D, D, D, D, cfg,
-                                        shops.epi(bias=A(p["bo"]), residual=A(x), ldr=D)), "sh_gemm_ex wo"),
-            ("ln2", L.sh_row_stats, (A(b["st2"]), A(b["h"]), rows, D, D, self.eps), None),
+                                        shops.epi(bias=A(p["bo"]), residual=A(x), ldr=D, stats_out=sp(b["pst_h"]))),
+             "sh_gemm_ex wo"),
+        ]
+        if self.row_partials:
+            ln2 = dict(ln_stats=A(b["pst_h"]), ln_parts=parts, ln_eps=self.eps)
+        else:
+            calls.append(("ln2", L.sh_row_stats, (A(b["st2"]), A(b["h"]), rows, D, D, self.eps), None))
+            ln2 = dict(ln_stats=A(b["st2"]))
+        calls += [
             ("ffn_up", L.sh_gemm_ex, (A(b["h"]), A(p["w1_ln"]), A(b["g"]), rows, F, D, D, F, F, cfg,
-                                      shops.epi(bias=A(p["d1"]), bias_fmt=F32, act=shops.SH_ACT_GELU, ln_stats=A(b["st2"]),
-                                                ln_c=A(p["c1"]))), "sh_gemm_ex w1"),
+                                      shops.epi(bias=A(p["d1"]), bias_fmt=F32, act=shops.SH_ACT_GELU, ln_c=A(p["c1"]), **ln2)),
+             "sh_gemm_ex w1"),
             ("ffn_down", L.sh_gemm_ex, (A(b["g"]), A(p["w2"]), A(out), rows, D, F, F, D, D, cfg,
-                                        shops.epi(bias=A(p["b2"]), residual=A(b["h"]), ldr=D)), "sh_gemm_ex w2"),
+                                        shops.epi(bias=A(p["b2"]), residual=A(b["h"]), ldr=D, stats_out=sp(b["pst_x"]))),
+             "sh_gemm_ex w2"),
         ]
         if len(self._plans) >= 64:            # bounded: argument sets of retired buffers are dropped
             self._plans.clear()
         self._plans[key] = calls
         return calls
 
-    def layer_fused(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int) -> torch.Tensor:
-        for name, fn, args, what in self._fused_plan(x, out, p, B, S):
+    def layer_fused(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int,
+                    x_parts: bool = False) -> torch.Tensor:
+        """One fused layer. x_parts=True: x was stored by the previous layer's FFN-down, whose row partials are in
+        the encoder's `pst_x` buffer (the layer then skips sh_row_stats); the layer leaves out's in it."""
+        for name, fn, args, what in self._fused_plan(x, out, p, B, S, x_parts):
             with self._op(name):
                 rc = fn(*args)
             if what is not None:
@@ -194,18 +220,20 @@ class Encoder:
 
     @staticmethod
     def op_costs(B: int, S: int, D: int = 768, F: int = 3072, H: int = 12) -> dict:
-        """Algorithmic FLOP and HBM bytes of each op of layer_fused (fp16 = 2 bytes, row statistics and the fold's
-        c / d rows fp32; weights read once)."""
+        """Algorithmic FLOP and HBM bytes of each op of layer_fused (fp16 = 2 bytes; row statistics, row partials
+        (8 bytes per 32 columns of a row) and the fold's c / d rows fp32; weights read once). "ln1" (sh_row_stats
+        of the input) runs only in a layer whose input has no row partials (the first of a stack)."""
         M = B * S
         g = lambda m, n, k: 2 * m * n * k  # noqa: E731
+        pb = 8 * M * (D // 32)              # row partials of one [M, D] activation
         return {
             "ln1": {"flop": 0, "bytes": 2 * M * D + 8 * M},
-            "qkv": {"flop": g(M, 3 * D, D), "bytes": 2 * (M * D + D * 3 * D + M * 3 * D) + 8 * M + 8 * 3 * D},
+            "ln2": {"flop": 0, "bytes": 2 * M * D + 8 * M},   # (only with row_partials = False)
+            "qkv": {"flop": g(M, 3 * D, D), "bytes": 2 * (M * D + D * 3 * D + M * 3 * D) + pb + 8 * 3 * D},
             "attention": {"flop": 4 * B * H * S * S * (D // H), "bytes": 2 * 4 * M * D},
-            "out_proj": {"flop": g(M, D, D), "bytes": 2 * (M * D + D * D + D + 2 * M * D)},
-            "ln2": {"flop": 0, "bytes": 2 * M * D + 8 * M},
-            "ffn_up": {"flop": g(M, F, D), "bytes": 2 * (M * D + D * F + M * F) + 8 * M + 8 * F},
-            "ffn_down": {"flop": g(M, D, F), "bytes": 2 * (M * F + F * D + D + 2 * M * D)},
+            "out_proj": {"flop": g(M, D, D), "bytes": 2 * (M * D + D * D + D + 2 * M * D) + pb},
+            "ffn_up": {"flop": g(M, F, D), "bytes": 2 * (M * D + D * F + M * F) + pb + 8 * F},
+            "ffn_down": {"flop": g(M, D, F), "bytes": 2 * (M * F + F * D + D + 2 * M * D) + pb},
         }
 
     def forward(self, x: torch.Tensor, params: list[LayerParams], B: int, S: int, sequence: str = "fused",
@@ -223,7 +251,10 @@ class Encoder:
         cur = x
         for i, p in enumerate(params):          # ping-pong so that the last layer writes `out`
             dst = out if (n - 1 - i) % 2 == 0 else tmp
-            step(cur, dst, p, B, S)
+            if sequence == "fused":
+                step(cur, dst, p, B, S, x_parts=i > 0)   # layer i > 0 reads the partials layer i - 1 wrote
+            else:
+                step(cur, dst, p, B, S)
             cur = dst
         return out
 

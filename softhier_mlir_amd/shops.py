@@ -38,7 +38,8 @@ class sh_gemm_epi(C.Structure):
     """Fused GEMM epilogue of sh_gemm_ex (additive)."""
     _fields_ = [("bias", C.c_uint64), ("bias_fmt", C.c_uint32), ("act", C.c_uint32),
                 ("residual", C.c_uint64), ("ldr", C.c_uint32), ("splits", C.c_uint32),
-                ("ln_stats", C.c_uint64), ("ln_c", C.c_uint64)]
+                ("ln_stats", C.c_uint64), ("ln_c", C.c_uint64), ("stats_out", C.c_uint64), ("ln_parts", C.c_uint32),
+                ("ln_eps", C.c_float)]
 
 
 u32, u64, i32, f32, i16 = C.c_uint32, C.c_uint64, C.c_int, C.c_float, C.c_uint16
@@ -143,8 +144,9 @@ def cfg(tm: int = 0, tn: int = 0, tk: int = 0, pipeline: int = 1, accumulate: in
 
 
 def epi(bias: int = 0, bias_fmt: int = SH_BIAS_FP16, act: int = SH_ACT_NONE, residual: int = 0, ldr: int = 0,
-        splits: int = 1, ln_stats: int = 0, ln_c: int = 0) -> sh_gemm_epi:
-    return sh_gemm_epi(bias, bias_fmt, act, residual, ldr, splits, ln_stats, ln_c)
+        splits: int = 1, ln_stats: int = 0, ln_c: int = 0, stats_out: int = 0, ln_parts: int = 0,
+        ln_eps: float = 0.0) -> sh_gemm_epi:
+    return sh_gemm_epi(bias, bias_fmt, act, residual, ldr, splits, ln_stats, ln_c, stats_out, ln_parts, ln_eps)
 
 
 def addr(t, elem_offset: int = 0) -> int:

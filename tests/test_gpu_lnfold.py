@@ -214,3 +214,107 @@ def test_fold_argument_errors(lib, gpu):
         assert lib.sh_gemm_ex(A(X), A(W), A(Z), M, N, K, K, N, N, None, e) == -1
     e = shops.epi(bias=A(D), bias_fmt=shops.SH_BIAS_FP32, ln_stats=A(S), ln_c=A(C))
     assert lib.sh_gemm_ex(A(X), A(W), A(Z), M, N, K, K, N, N, shops.cfg(accumulate=1), e) == -1
+
+
+# ---- row partials written by the producing GEMM (sh_gemm_epi.stats_out) and combined by the consumer ----------
+def _partials_f64(z):
+    """(sum, M2) of every 32 columns of each row, float64."""
+    z = np.asarray(z, np.float64)
+    M, N = z.shape
+    b = z.reshape(M, N // 32, 32)
+    s = b.sum(2)
+    return s, ((b - s[..., None] / 32) ** 2).sum(2)
+
+
+def _producer(M, N, K, seed):
+    a = data.normal((M, K), seed)
+    w = data.normal((K, N), seed + 1, std=1 / np.sqrt(K))
+    b = data.normal((1, N), seed + 2, std=0.3)
+    r = (data.normal((M, N), seed + 3, std=2.0) + 0.7).astype(np.float16)
+    return a, w, b, r
+
+
+def test_row_partials_match_float64_and_agree_across_tiles(lib, gpu, monkeypatch):
+    """A GEMM with bias + residual that also writes row partials: the pairs match float64 sums over the stored
+    fp16 output; every register-epilogue tile writes the same pairs and outputs bit for bit (the same 32 values
+    summed in the same order), and the split-K path (the reduction writes them) agrees within fp32 rounding."""
+    import torch
+    M, N, K = 520, 768, 448
+    a, w, b, r = _producer(M, N, K, 130)
+    X, W, Bb, R = to_dev(a), to_dev(w), to_dev(b), to_dev(r)
+    P = N // 32
+    runs = {}
+    for cfg in REG_CFGS + ["split3"]:
+        Z = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        St = _empty32(M, P, 2)
+        if cfg == "split3":
+            monkeypatch.delenv("SH_GEMM_CFG", raising=False)
+            e = shops.epi(bias=A(Bb), residual=A(R), ldr=N, stats_out=A(St), splits=3)
+        else:
+            monkeypatch.setenv("SH_GEMM_CFG", str(cfg))
+            e = shops.epi(bias=A(Bb), residual=A(R), ldr=N, stats_out=A(St))
+        assert lib.sh_gemm_ex(A(X), A(W), A(Z), M, N, K, K, N, N, None, e) == 0, (cfg, shops.last_error())
+        runs[cfg] = (codes(Z), to_np(St))
+    z0, st0 = runs[REG_CFGS[0]]
+    for cfg in REG_CFGS:
+        assert np.array_equal(runs[cfg][0], z0), cfg
+        assert np.array_equal(runs[cfg][1].view(np.uint32), st0.view(np.uint32)), cfg
+    s, m2 = _partials_f64(z0.view(np.float16))
+    u = 2.0 ** -24
+    mag = np.abs(z0.view(np.float16).astype(np.float64)).reshape(M, P, 32).sum(2)
+    assert np.all(np.abs(st0[..., 0] - s) <= 32 * u * mag)
+    assert np.all(np.abs(st0[..., 1] - m2) <= 64 * u * (m2 + mag ** 2 / 32))
+    zs, sts = runs["split3"]
+    assert refs.close(zs.view(np.float16), z0.view(np.float16), atol=2e-2, rtol=1e-2)[0] == 0
+    s3, m23 = _partials_f64(zs.view(np.float16))
+    assert np.all(np.abs(sts[..., 0] - s3) <= 32 * u * mag + 1e-3)
+    assert np.all(np.abs(sts[..., 1] - m23) <= 64 * u * (m23 + mag ** 2 / 32) + 1e-3)
+    want = refs.r16(refs.add(refs.r16(refs.add_bias(refs.r16(refs.gemm(a, w)), b)), r))
+    assert refs.close(z0.view(np.float16), want)[0] == 0
+
+
+@pytest.mark.parametrize("mean,act", [(0.7, 0), (0.7, 1), (60.0, 0)])
+def test_fold_from_row_partials(lib, gpu, mean, act):
+    """The consumer of row partials (ln_parts = K / 32): H from a GEMM that wrote its partials, then the folded
+    GEMM on H against the oracle's LayerNorm -> GEMM -> bias (-> GELU) of the stored H, and against the same
+    folded GEMM given sh_row_stats of H (two-pass statistics), which it matches to a few fp16 ulps. mean = 60:
+    rows far from zero mean (the partials keep M2 about each block's own mean)."""
+    import torch
+    M, D, N = 1000, 768, 1536
+    a, wh, bh, r = _producer(M, D, 256, 150)
+    r = (r.astype(np.float32) + np.float32(mean - 0.7)).astype(np.float16)
+    X, WH, BH, R = to_dev(a), to_dev(wh), to_dev(bh), to_dev(r)
+    H = torch.empty((M, D), dtype=torch.float16, device="cuda")
+    Pst = _empty32(M, D // 32, 2)
+    e = shops.epi(bias=A(BH), residual=A(R), ldr=D, stats_out=A(Pst))
+    assert lib.sh_gemm_ex(A(X), A(WH), A(H), M, D, 256, 256, D, D, None, e) == 0, shops.last_error()
+    h = to_np(H)
+    _, w, g, be, b = _problem(M, N, D, 160)
+    W, G, BE, Bb = to_dev(w), to_dev(g), to_dev(be), to_dev(b)
+    WP, C, Dd, S = _fold(lib, H, W, G, BE, Bb, M, N, D)
+    Z = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    e = shops.epi(bias=A(Dd), bias_fmt=shops.SH_BIAS_FP32, act=act, ln_stats=A(Pst), ln_c=A(C), ln_parts=D // 32,
+                  ln_eps=EPS)
+    assert lib.sh_gemm_ex(A(H), A(WP), A(Z), M, N, D, D, N, N, None, e) == 0, shops.last_error()
+    Z2 = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    e2 = shops.epi(bias=A(Dd), bias_fmt=shops.SH_BIAS_FP32, act=act, ln_stats=A(S), ln_c=A(C))
+    assert lib.sh_gemm_ex(A(H), A(WP), A(Z2), M, N, D, D, N, N, None, e2) == 0, shops.last_error()
+    bad, err, _ = refs.close(to_np(Z), _want(h, w, g, be, b, act))
+    assert bad == 0, err
+    bad, err, _ = refs.close(to_np(Z), to_np(Z2), atol=2e-3, rtol=2e-3)
+    assert bad == 0, err
+
+
+def test_row_partials_argument_errors(lib, gpu):
+    import torch
+    M, N, K = 256, 768, 256
+    X = to_dev(data.normal((M, K), 1))
+    W = to_dev(data.normal((K, N), 2))
+    W584 = to_dev(data.normal((K, 584), 3))
+    Z = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    St = _empty32(M, N // 32 + 1, 2)
+    assert lib.sh_gemm_ex(A(X), A(W), A(Z), M, N, K, K, N, N, None, shops.epi(stats_out=A(St) + 4)) == -1   # alignment
+    assert lib.sh_gemm_ex(A(X), A(W584), A(Z), M, 584, K, K, 584, 584, None, shops.epi(stats_out=A(St))) == -1  # N % 32
+    S, C, D = _empty32(M, 8, 2), _empty32(N), _empty32(N)
+    e = shops.epi(bias=A(D), bias_fmt=shops.SH_BIAS_FP32, ln_stats=A(S), ln_c=A(C), ln_parts=4, ln_eps=EPS)
+    assert lib.sh_gemm_ex(A(X), A(W), A(Z), M, N, K, K, N, N, None, e) == -1                                # 4 x 32 != K
