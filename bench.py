@@ -3,14 +3,16 @@ B=32, S=256, D=768, 12 heads, FFN 3072, fp16, weights N(0, 0.02), biases zero, x
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--sequence fused|reference] [--graph] [--no-cpu] [--no-rowops]
 
-A step is one forward pass of the layer over the batch through libshops.so (inputs resident in HBM), its calls
-launched one by one; `--graph` records the fused layer's seven calls once into a HIP graph and times replays of
-it instead (the same kernels every step; on MI355X this measured no faster: the gaps between kernels are not
-host launch time). Prints ONE JSON line with the whole-job TFLOP/s, the roofline of the dominant kernel (HIP events around its
-launches, on the library stream = the legacy null stream torch also uses), the per-op breakdown, the row-op HBM
-bandwidths at the batched shapes (cold: rotating buffer sets of >= 512 MiB; each next to a plain device copy of
-the same bytes, the practical ceiling at that size) and the numpy CPU baseline (the oracle's restatement, timed
-on this host).
+A step is one forward pass of one layer over the batch through libshops.so (inputs resident in HBM), its calls
+launched one by one, as a layer runs inside the 12-layer stack: the fused layer (five launches) reads the rows
+and the row partials the previous step stored (the first step computes the row statistics of the input itself);
+`--row-stats` times the seven-launch variant with a row-statistics pass before each folded GEMM. `--graph`
+records the fused layer (from the input's own statistics) once into a HIP graph and times replays of it instead.
+Prints ONE JSON line with the whole-job TFLOP/s, the roofline of the dominant kernel (its call of the timed step
+launched K times back to back between one HIP event pair on the library stream = the legacy null stream),
+the per-op breakdown, the row-op HBM bandwidths at the batched shapes (cold: rotating buffer sets of >= 512 MiB;
+each next to the library's streaming copy of the same bytes) and the numpy CPU baseline (the oracle's
+restatement, timed on this host).
 """
 from __future__ import annotations
 
@@ -520,8 +522,11 @@ def main() -> int:
     events: dict = {}
 
     class Tap:
-        """HIP events (torch's current stream = the legacy null stream the library launches on) around one op."""
+        """HIP events (torch's current stream = the legacy null stream the library launches on) around one op.
+        The events are created ahead (`pool`), so recording them costs the host little and the host keeps ahead
+        of the GPU: an event pair then brackets the kernel, not an idle gap before it."""
         only = None
+        pool: list = []
 
         def __init__(self, name):
             self.name = name
@@ -529,8 +534,10 @@ def main() -> int:
 
         def __enter__(self):
             if self.on:
-                self.e0 = torch.cuda.Event(enable_timing=True)
-                self.e1 = torch.cuda.Event(enable_timing=True)
+                if not Tap.pool:
+                    Tap.pool = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                                for _ in range(256)]
+                self.e0, self.e1 = Tap.pool.pop()
                 self.e0.record()
 
         def __exit__(self, *exc):
@@ -560,7 +567,7 @@ def main() -> int:
             entry["GB/s"] = round(c["bytes"] / (us * 1e-6) / 1e9, 1)
             breakdown[name] = entry
         events.clear()
-        Tap.only = max(breakdown, key=lambda k: breakdown[k]["us"])   # only the dominant op is timed below
+        Tap.only = max(breakdown, key=lambda k: breakdown[k]["us"])   # the dominant op (its launches are timed below)
 
     # timed region: K steps, each one replay of the captured layer graph (or the eager op sequence)
     graph = None
@@ -589,19 +596,28 @@ def main() -> int:
     flop = encoder.flops_per_layer(B, S, D, F)
     value = flop / (elapsed / args.steps) / 1e12
 
-    # the dominant op's launches, timed with HIP events in K eager steps right after (same kernels, same shapes)
-    if Tap.only is not None:
-        enc.tap = Tap
-        for _ in range(args.steps):
-            step(x, out, lp, B, S)
+    # the dominant op's average launch duration: its library call of the steady-state step (same kernel, same
+    # operands) launched K times back to back between one HIP event pair on the library stream, so the pair's
+    # own dispatch overhead (a few us per pair, more under a kernel tracer) is spread over K launches
+    dom_us = None
+    if Tap.only is not None and args.sequence == "fused":
+        plan = {nm: (fn, a) for nm, fn, a, _ in enc._fused_plan(bufs[0], bufs[1], lp, B, S, True)}
+        fn, a = plan[Tap.only]
+        fn(*a)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
-        enc.tap = None
+        e0.record()
+        for _ in range(args.steps):
+            fn(*a)
+        e1.record()
+        torch.cuda.synchronize()
+        dom_us = e0.elapsed_time(e1) * 1e3 / args.steps
 
     roofline = None
-    if Tap.only is not None:
+    if dom_us is not None:
         dom = Tap.only
         c = costs[dom]
-        us = avg_us(events[dom])
+        us = dom_us
         if c["flop"]:
             ach = c["flop"] / (us * 1e-6) / 1e12
             roofline = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
