@@ -433,8 +433,9 @@ __device__ __forceinline__ void attn_stamp(uint64_t *stamp, bool on, int i) {
 // VALU work, not the MFMA work, bounds attention, so the row maximum is found first in a cheap pass over the
 // keys (S^T = K . Q^T on MFMA, then max3 only); the second pass recomputes the scores and, with the final
 // maximum known, needs no running rescale of O or l: p = 2^(c s - m), P (fp16) feeds O^T += V^T . P^T, and
-// the row sums l come from one more MFMA with an all-ones A operand (the sums of the fp16 numerators the
-// PV product used). Masking of keys past S happens only in the last, partial key block.
+// the row sums l are the sums of the fp16 numerators the PV product used (v_dot2_f32_f16 with ones, fp32).
+// Masking of keys past S happens only in the last, partial key block. LDS fragment reads are issued ahead of
+// the MFMAs that use them (two ahead for K, one for V), so a read's latency overlaps earlier MFMAs.
 // FOLD (|c| <= 1, so c q stays in fp16 range): the softmax VALU work shrinks by folding c and m into the score
 // MFMAs. The query fragments are scaled once, q' = r16(c q), so the scores come out as c s (pass 1 then takes
 // a plain maximum for either sign of c), and pass 2 adds one more 16-k MFMA step per score tile whose
@@ -514,19 +515,28 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a, ui
     if (FOLD && g == 0) { kbias[0] = (_Float16)1.0f; kbias[1] = (_Float16)1.0f; }
 
     // S^T tile pair of key block in stage st: sacc[tt][r] = s(key 32 tt + 8 (r/4) + 4 g + r%4, query r32)
-    // (FOLD: c s, and with bias, c s - m)
+    // (FOLD: c s, and with bias, c s - m). The 2 NS K fragments are read two MFMAs ahead of their use (the two
+    // tiles' chains interleaved), so each LDS read has two MFMAs to land in.
+    auto kfrag = [&](const uint4 *sk, int i) -> sh_h8 {        // fragment i: substep i / 2 of tile i % 2
+        const uint32_t key = 32 * (i & 1) + r32;
+        return __builtin_bit_cast(sh_h8, sk[key * DC + ((2 * (i >> 1) + g) ^ kswz<DH>(key))]);
+    };
     auto scores = [&](int st, sh_f16v (&sacc)[2], bool bias) {
         const uint4 *sk = smem + st * 2 * KCH;
+        constexpr int NI = 2 * NS;
+        sh_h8 kf[3];
+        kf[0] = kfrag(sk, 0);
+        kf[1] = kfrag(sk, 1);
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
             sacc[tt] = sh_f16v{};
             if (FOLD && bias) sacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kbias, qbias, sacc[tt], 0, 0, 0);
-            const uint32_t key = 32 * tt + r32;
+        }
 #pragma unroll
-            for (int s = 0; s < NS; ++s) {
-                const sh_h8 kf = __builtin_bit_cast(sh_h8, sk[key * DC + ((2 * s + g) ^ kswz<DH>(key))]);
-                sacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], sacc[tt], 0, 0, 0);
-            }
+        for (int i = 0; i < NI; ++i) {
+            if (i + 2 < NI) kf[(i + 2) % 3] = kfrag(sk, i + 2);
+            sacc[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[i % 3], qf[i >> 1], sacc[i & 1], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
     auto key_of = [&](uint32_t kb, int tt, int r) { return kb * KB + 32 * tt + 8 * (r >> 2) + 4 * g + (r & 3); };
@@ -583,10 +593,8 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a, ui
     sh_f16v oacc[DT];
 #pragma unroll
     for (int i = 0; i < DT; ++i) oacc[i] = sh_f16v{};
-    sh_f16v lacc = sh_f16v{};
-    sh_h8 ones;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ones[e] = (_Float16)1.0f;
+    float lsum = 0.f;                                // this lane's keys' fp16 numerators, summed in fp32
+    const sh_h2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
     for (int s = 0; s < NST - 1; ++s) issue(min((uint32_t)s, nkb - 1), s, true);
     for (uint32_t kb = 0; kb < nkb; ++kb) {
@@ -612,26 +620,38 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a, ui
                 pf[2 * tt + (r >> 3)][r & 7] = (_Float16)p;
             }
         const uint32_t vbase = lds0 + (uint32_t)st * STAGE + KCH * 16;
-#pragma unroll
-        for (int sp = 0; sp < 4; ++sp) lacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, pf[sp], lacc, 0, 0, 0);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
+        // V^T fragment j: substep j / DT, d tile j % DT (consecutive MFMAs alternate accumulators); read one ahead
+        auto vfrag = [&](int j) -> sh_h8 {
+            const int sp = j / DT, dt = j % DT;
             const uint32_t d = 32 * dt + 16 * (q4 & 1) + 4 * (iq & 3);
+            const uint32_t k0 = 16 * sp + 4 * g + (iq >> 2), k1 = k0 + 8;
+            const sh_s4 lo = sh_ds_read_tr(vbase + k0 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k0)) + 2 * (d & 7));
+            const sh_s4 hi = sh_ds_read_tr(vbase + k1 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k1)) + 2 * (d & 7));
+            return __builtin_bit_cast(sh_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        };
+        constexpr int NJ = 4 * DT;
+        sh_h8 vq[2];
+        vq[0] = vfrag(0);
 #pragma unroll
-            for (int sp = 0; sp < 4; ++sp) {
-                const uint32_t k0 = 16 * sp + 4 * g + (iq >> 2), k1 = k0 + 8;
-                const sh_s4 lo = sh_ds_read_tr(vbase + k0 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k0)) + 2 * (d & 7));
-                const sh_s4 hi = sh_ds_read_tr(vbase + k1 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k1)) + 2 * (d & 7));
-                const sh_h8 vf = __builtin_bit_cast(sh_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-                oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[sp], oacc[dt], 0, 0, 0);
-            }
+        for (int sp = 0; sp < 4; ++sp) {
+            const uint4 w = __builtin_bit_cast(uint4, pf[sp]);
+            lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(sh_h2, w.x), one2, lsum, false);
+            lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(sh_h2, w.y), one2, lsum, false);
+            lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(sh_h2, w.z), one2, lsum, false);
+            lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(sh_h2, w.w), one2, lsum, false);
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            if (j + 1 < NJ) vq[(j + 1) & 1] = vfrag(j + 1);
+            oacc[j % DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vq[j & 1], pf[j / DT], oacc[j % DT], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     sh_wait_vmcnt<0>();      // clamped tail loads land before the LDS is reused below
     __syncthreads();
     attn_stamp(stamp, last, 5);
 
-    const float inv = 1.f / lacc[0];                 // every row of the ones product holds this query's l
+    const float inv = 1.f / (lsum + __shfl_xor(lsum, 32, 64));   // lanes g = 0, 1 hold complementary keys
     uint16_t *so = (uint16_t *)(smem + 2 * KCH) + wave * (QPW * DH);     // this wave's query rows, now free
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)

@@ -2102,7 +2102,7 @@ int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st, bool wt) {
     const int cus = sh_num_cus() > 0 ? sh_num_cus() : 256;
     double thr = 0.0;
     (void)est_time(heur, call.M, call.N, call.K, 1, cus, &thr);
-    if (thr < 12e-6) return heur;                    // the throughput estimate: small problems keep the model's tile
+    if (thr < 6e-6) return heur;                     // the throughput estimate: small problems keep the model's tile
     tune_file_load();
     const TuneKey key{call.M, call.N, call.K, call.ldx, call.ldw, call.bias ? 1u + call.bias_fp32 : 0u, call.act,
                       (wt ? 1u : 0u) | (reg_only ? 2u : 0u)};
