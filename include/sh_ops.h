@@ -136,8 +136,10 @@ int sh_attention(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t S, uin
 uint32_t sh_attention_l1_bytes_q(uint32_t S, uint32_t dh, uint32_t sq);   /* sh_ops.h:118 */
 uint32_t sh_attention_l1_bytes(uint32_t S, uint32_t dh);                  /* sh_ops.h:119 */
 uint32_t sh_attention_q_block(uint32_t S, uint32_t dh, uint32_t H, uint32_t P);   /* sh_ops.h:123 same rule */
-/* sh_ops.h:127: ns stamps of the last attention call: 7 entry, 0 kernel start, 1..5 = 0, 6 kernel end (all 0
- * when that call was sh_attention_batched or made under stream capture, which carry no stamps). */
+/* sh_ops.h:127: ns stamps of the last attention call's last workgroup, from its first workgroup's start (phase 7
+ * = 0): 0 start, 1-2 operands staged, 3-4 row maximum known, 5 every key block done, 6 stored (the kernels without
+ * stamps report only 6, the launch's event time; all 0 when that call was sh_attention_batched or made under
+ * stream capture, which carry no stamps). */
 uint32_t sh_attention_profile(uint32_t S, uint32_t dh, uint32_t phase);
 
 /* ---- Llama-style decoder ops (sh_ops.h:277-307, runtime/sh_llm.inc.c) -----------------------------------

@@ -429,7 +429,8 @@ __device__ __forceinline__ void attn_stamp(uint64_t *stamp, bool on, int i) {
     }
 }
 
-// Two-pass variant of k_flash_dma for dh 64 / 128 (the default for aligned heads). On CDNA the softmax
+// Two-pass variant of k_flash_dma for dh 64 / 128 (aligned heads with a token mask or a scale that does not
+// fold, |c| > 1; SH_ATTN_IMPL=2 selects it for every aligned head). On CDNA the softmax
 // VALU work, not the MFMA work, bounds attention, so the row maximum is found first in a cheap pass over the
 // keys (S^T = K . Q^T on MFMA, then max3 only); the second pass recomputes the scores and, with the final
 // maximum known, needs no running rescale of O or l: p = 2^(c s - m), P (fp16) feeds O^T += V^T . P^T, and
@@ -674,6 +675,223 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a, ui
     attn_stamp(stamp, last, 6);
 }
 
+// One-pass variant of k_flash2 (the default for aligned dh 64 / 128 heads whose scale folds, |c| <= 1, without a
+// token mask): each key block's scores come out of the MFMAs already shifted by the query's running maximum m (the
+// FOLD bias step: ones x (-m_hi, -m_lo)), so p = 2^acc. The first block sets m to its own maximum; a later block
+// whose maximum exceeds m by more than kTau (log2 units) moves m up to it, and only then are O and l rescaled by
+// 2^-shift and the block's scores computed again with the new bias (a wave-uniform branch, taken for the first
+// block and rarely after). Numerators therefore stay at or below 2^kTau, well inside fp16, and the row sums are the
+// sums of the same fp16 numerators the P.V product uses, so O / l is the softmax with every p rounded once. Against
+// k_flash2 this drops the maximum pass (its score MFMAs, K fragment reads and K DMAs) and the refill of the ring
+// between the passes. Same LDS ring, fragment prefetch and occupancy as k_flash2.
+constexpr float kTau = 8.f;
+template <int DH, int NST>
+__global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, uint64_t *stamp) {
+    constexpr int DC = DH / 8, NS = DH / 16, DT = DH / 32;
+    constexpr int KCH = KB * DC;                     // 16-byte chunks per K (or V) block
+    constexpr int KR = KCH / 256;                    // DMA rounds per thread per block, per operand
+    constexpr uint32_t STAGE = 2u * KCH * 16u;       // K block then V block
+    static_assert(KCH % 256 == 0 && NST >= 2, "attention tiling");
+    __shared__ uint4 smem[NST * 2 * KCH];
+
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = lane >> 5, r32 = lane & 31;
+    const int q4 = lane >> 4, iq = lane & 15;
+    uint32_t qb, h, b;
+    attn_item(a, qb, h, b);
+    const uint32_t S = a.S;
+    const uint16_t *Q = a.q + b * a.bsq + (uint64_t)h * DH;
+    const uint16_t *Kp = a.k + b * a.bsk + (uint64_t)(h / a.grp) * DH;
+    const uint16_t *Vp = a.v + b * a.bsv + (uint64_t)(h / a.grp) * DH;
+    uint16_t *O = a.o + b * a.bso + (uint64_t)h * DH;
+    const uint32_t qw0 = qb * QPB + wave * QPW, myq = qw0 + r32;
+    const uint32_t nkb = (S + KB - 1) / KB;
+    const bool ragged = S % KB != 0;                 // the last key block is partial
+    // stamps (profile): 0-2 start, 3-4 first key block done (its maximum known), 5 all blocks done, 6 stored;
+    // 7 first workgroup
+    const bool last = stamp && t == 0 && qb == gridDim.x - 1 && h == gridDim.y - 1 && b == gridDim.z - 1;
+    attn_stamp(stamp, stamp && t == 0 && qb == 0 && h == 0 && b == 0, 7);
+    attn_stamp(stamp, last, 0);
+    attn_stamp(stamp, last, 1);
+    attn_stamp(stamp, last, 2);
+
+    const uint16_t *kcol[KR];
+    const uint16_t *vcol[KR];
+    uint32_t kkey[KR];
+#pragma unroll
+    for (int r = 0; r < KR; ++r) {
+        const uint32_t p = r * 256 + wave * 64 + lane, key = p / DC, pc = p % DC;
+        kkey[r] = key;
+        kcol[r] = Kp + 8 * (pc ^ kswz<DH>(key));
+        vcol[r] = Vp + 8 * (pc ^ vfw<DH>(key));
+    }
+    const uint32_t lds0 = sh_lds_addr(smem);
+    const uint32_t wave_off = (uint32_t)__builtin_amdgcn_readfirstlane(wave * 64 * 16);
+    auto issue = [&](uint32_t kb, int stage) {
+        const uint32_t st = lds0 + (uint32_t)stage * STAGE;
+        const uint32_t k0 = kb * KB;
+#pragma unroll
+        for (int r = 0; r < KR; ++r) {
+            const uint64_t row = min(k0 + kkey[r], S - 1);                      // rows past S read row S-1
+            sh_lds_dma16(kcol[r] + row * a.ldk, st + r * 4096 + wave_off);
+            sh_lds_dma16(vcol[r] + row * a.ldv, st + KCH * 16 + r * 4096 + wave_off);
+        }
+    };
+#pragma unroll
+    for (int s = 0; s < NST - 1; ++s) issue(min((uint32_t)s, nkb - 1), s);
+
+    // query fragments, scaled once by c: the scores come out as c s
+    sh_h8 qf[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) qf[s] = __builtin_bit_cast(sh_h8, ld8<true>(Q, a.ldq, myq, 16 * s + 8 * g, S, DH));
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qf[s][e] = (_Float16)((float)qf[s][e] * a.c);
+    // operands of the bias step (k elements 0 and 1 of lane group 0): ones for every key, -m_hi, -m_lo of this
+    // lane's query (set from the running maximum)
+    sh_h8 kbias = {}, qbias = {};
+    if (g == 0) { kbias[0] = (_Float16)1.0f; kbias[1] = (_Float16)1.0f; }
+    auto set_bias = [&](float m) {
+        if (g == 0) {
+            const _Float16 mh = (_Float16)m;
+            qbias[0] = -mh;
+            qbias[1] = -(_Float16)(m - (float)mh);
+        }
+    };
+
+    // S^T tile pair of key block in stage st (as k_flash2): sacc[tt][r] = c s(key 32 tt + 8 (r/4) + 4 g + r%4,
+    // query r32) [- m with the bias step]; K fragments read two MFMAs ahead
+    auto kfrag = [&](const uint4 *sk, int i) -> sh_h8 {
+        const uint32_t key = 32 * (i & 1) + r32;
+        return __builtin_bit_cast(sh_h8, sk[key * DC + ((2 * (i >> 1) + g) ^ kswz<DH>(key))]);
+    };
+    auto scores = [&](int st, sh_f16v (&sacc)[2], bool bias) {
+        const uint4 *sk = smem + st * 2 * KCH;
+        constexpr int NI = 2 * NS;
+        sh_h8 kf[3];
+        kf[0] = kfrag(sk, 0);
+        kf[1] = kfrag(sk, 1);
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            sacc[tt] = sh_f16v{};
+            if (bias) sacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kbias, qbias, sacc[tt], 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            if (i + 2 < NI) kf[(i + 2) % 3] = kfrag(sk, i + 2);
+            sacc[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[i % 3], qf[i >> 1], sacc[i & 1], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    sh_f16v oacc[DT];
+#pragma unroll
+    for (int i = 0; i < DT; ++i) oacc[i] = sh_f16v{};
+    float lsum = 0.f;                                // this lane's keys' fp16 numerators, summed in fp32
+    float mrun = 0.f;                                // running maximum of c s for this lane's query
+    const sh_h2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
+    for (uint32_t kb = 0; kb < nkb; ++kb) {
+        sh_wait_vmcnt<(NST - 2) * 2 * KR>();
+        __syncthreads();
+        issue(min(kb + NST - 1, nkb - 1), (int)((kb + NST - 1) % NST));
+        const int st = (int)(kb % NST);
+        sh_f16v sacc[2];
+        auto mask_tail = [&]() {
+            if (ragged && kb == nkb - 1) {
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        if (kb * KB + 32 * tt + 8 * (r >> 2) + 4 * g + (r & 3) >= S) sacc[tt][r] = -INFINITY;
+            }
+        };
+        scores(st, sacc, kb > 0);
+        mask_tail();
+        // the block's maximum for this lane's query (lanes r32 and r32 + 32 hold complementary keys)
+        float bm = -INFINITY;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sacc[tt][r]);
+        bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+        const bool move = kb == 0 || bm > kTau;      // every block holds a valid key: bm is finite
+        if (__ballot(move) != 0) {                   // wave-uniform: m moves up, O and l rescale, scores again
+            const float shift = move ? bm : 0.f;
+            if (kb > 0) {
+                const float sc = sh_fast_exp2(-shift);
+#pragma unroll
+                for (int i = 0; i < DT; ++i) oacc[i] *= sc;
+                lsum *= sc;
+            }
+            mrun = (kb == 0 ? 0.f : mrun) + shift;
+            set_bias(mrun);
+            scores(st, sacc, true);
+            mask_tail();
+        }
+        sh_h8 pf[4];                                 // numerators p = 2^acc, fp16, as the P.V MFMA operands
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) pf[2 * tt + (r >> 3)][r & 7] = (_Float16)sh_fast_exp2(sacc[tt][r]);
+        if (kb == 0) {
+            attn_stamp(stamp, last, 3);
+            attn_stamp(stamp, last, 4);
+        }
+        const uint32_t vbase = lds0 + (uint32_t)st * STAGE + KCH * 16;
+        // V^T fragment j: substep j / DT, d tile j % DT (consecutive MFMAs alternate accumulators); read one ahead
+        auto vfrag = [&](int j) -> sh_h8 {
+            const int sp = j / DT, dt = j % DT;
+            const uint32_t d = 32 * dt + 16 * (q4 & 1) + 4 * (iq & 3);
+            const uint32_t k0 = 16 * sp + 4 * g + (iq >> 2), k1 = k0 + 8;
+            const sh_s4 lo = sh_ds_read_tr(vbase + k0 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k0)) + 2 * (d & 7));
+            const sh_s4 hi = sh_ds_read_tr(vbase + k1 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k1)) + 2 * (d & 7));
+            return __builtin_bit_cast(sh_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        };
+        constexpr int NJ = 4 * DT;
+        sh_h8 vq[2];
+        vq[0] = vfrag(0);
+#pragma unroll
+        for (int sp = 0; sp < 4; ++sp) {
+            const uint4 w = __builtin_bit_cast(uint4, pf[sp]);
+            lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(sh_h2, w.x), one2, lsum, false);
+            lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(sh_h2, w.y), one2, lsum, false);
+            lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(sh_h2, w.z), one2, lsum, false);
+            lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(sh_h2, w.w), one2, lsum, false);
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            if (j + 1 < NJ) vq[(j + 1) & 1] = vfrag(j + 1);
+            oacc[j % DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vq[j & 1], pf[j / DT], oacc[j % DT], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    sh_wait_vmcnt<0>();      // clamped tail loads land before the LDS is reused below
+    __syncthreads();
+    attn_stamp(stamp, last, 5);
+
+    const float inv = 1.f / (lsum + __shfl_xor(lsum, 32, 64));   // lanes g = 0, 1 hold complementary keys
+    uint16_t *so = (uint16_t *)(smem + 2 * KCH) + wave * (QPW * DH);     // this wave's query rows, now free
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const int d0 = 32 * dt + 8 * rb + 4 * g;
+            const uint32_t lo = (uint32_t)sh_dev_f2h(oacc[dt][4 * rb] * inv) | ((uint32_t)sh_dev_f2h(oacc[dt][4 * rb + 1] * inv) << 16);
+            const uint32_t hi = (uint32_t)sh_dev_f2h(oacc[dt][4 * rb + 2] * inv) | ((uint32_t)sh_dev_f2h(oacc[dt][4 * rb + 3] * inv) << 16);
+            const int ch = (d0 >> 3) ^ (r32 & 7);
+            *(uint2 *)(so + r32 * DH + ch * 8 + (d0 & 7)) = make_uint2(lo, hi);
+        }
+    sh_wait_lgkm0();                                 // the wave's own staging is complete
+    __builtin_amdgcn_wave_barrier();
+    for (int c = lane; c < QPW * DC; c += 64) {
+        const int row = c / DC, ch = c % DC;
+        const uint32_t qq = qw0 + row;
+        if (qq >= S) continue;
+        *(uint4 *)(O + (uint64_t)qq * a.ldo + 8 * ch) = ((const uint4 *)so)[row * DC + (ch ^ (row & 7))];
+    }
+    attn_stamp(stamp, last, 6);
+}
+
 // Any dh: one 256-thread block per (query, head, sequence); scores of the row in LDS (S <= 16384).
 __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
     extern __shared__ float sc[];
@@ -797,7 +1015,10 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
         static bool attr_m = false;
         if (!attr_m) { (void)hipFuncSetAttribute((const void *)k_attn_rows, hipFuncAttributeMaxDynamicSharedMemorySize, 16384 * 4); attr_m = true; }
         go(k_attn_rows, dim3(S, H, B), S * sizeof(float));
-    } else if ((dh == 64 || dh == 128) && vec && impl == 0) {
+    } else if ((dh == 64 || dh == 128) && vec && impl == 0 && fold) {
+        if (dh == 64) go2(k_flash3<64, 2>, grid, 0);
+        else go2(k_flash3<128, 2>, grid, 0);
+    } else if ((dh == 64 || dh == 128) && vec && (impl == 0 || impl == 2)) {
         if (dh == 64) fold ? go2(k_flash2<64, 2, false, true>, grid, 0) : go2(k_flash2<64, 2, false, false>, grid, 0);
         else fold ? go2(k_flash2<128, 2, false, true>, grid, 0) : go2(k_flash2<128, 2, false, false>, grid, 0);
     } else if ((dh == 64 || dh == 128) && vec && impl == 1) {
@@ -904,8 +1125,9 @@ int sh_attention_gqa(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t S,
 }
 
 // ns since the first workgroup of the last stamped launch started (phase 7 = 0): 0 the last workgroup's start,
-// 1-2 its operands staged, 3 scores (two-pass kernel: pass 1, the maximum), 4 softmax, 5 P.V, 6 stored. Kernels
-// without stamps report only 6, as the launch's event time.
+// 1-2 its operands staged, 3-4 the maximum known (one-pass kernel: after the first key block; two-pass kernel:
+// pass 1 done), 5 every key block done (P.V), 6 stored. Kernels without stamps report only 6, as the launch's
+// event time.
 uint32_t sh_attention_profile(uint32_t, uint32_t, uint32_t phase) {
     if (!g_prof.valid) return 0;
     phase &= 7;

@@ -104,8 +104,10 @@ def test_wide_heads_row_kernel(lib, gpu):
     assert bad == 0, err
 
 
-@pytest.mark.parametrize("scale", [-0.125, 0.0, 0.6])
+@pytest.mark.parametrize("scale", [-0.125, 0.0, 0.6, 1.0])
 def test_scale_edge_cases(lib, gpu, scale):
+    """Scales whose c = scale log2(e) folds into the query fragments (|c| <= 1: the one-pass kernel) and one that does
+    not (1.0: the two-pass kernel without the fold)."""
     S, D, H = 192, 256, 4
     q, k, v = data.normal((S, D), 8), data.normal((S, D), 9), data.normal((S, D), 10)
     O = _zeros(S, D)
@@ -126,9 +128,9 @@ def test_profile_reports_the_kernel_time(lib, gpu):
 @pytest.mark.parametrize("S", [256, 1024])
 def test_profile_phase_stamps_are_monotone(lib, gpu, S):
     """sh_attention_profile (reference sh_attention.inc.c:67-76, sh_ops.h:124-127): the last workgroup's stamps in
-    ns from the first workgroup's start (phase 7 = 0): start (0) <= operands staged (1, 2) <= scores (3; the
-    two-pass kernel of S = 1024: pass 1) <= softmax (4) <= P.V (5; pass 2) <= stored (6). A batched call leaves no
-    stamps (every phase reads 0)."""
+    ns from the first workgroup's start (phase 7 = 0): start (0) <= operands staged (1, 2) <= maximum known (3, 4;
+    the one-pass kernel: after the first key block) <= every key block done (5) <= stored (6). A batched call leaves
+    no stamps (every phase reads 0)."""
     D, H = 768, 12
     q = to_dev(data.normal((S, D), 3))
     O = _zeros(S, D)
