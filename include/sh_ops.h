@@ -137,9 +137,9 @@ uint32_t sh_attention_l1_bytes_q(uint32_t S, uint32_t dh, uint32_t sq);   /* sh_
 uint32_t sh_attention_l1_bytes(uint32_t S, uint32_t dh);                  /* sh_ops.h:119 */
 uint32_t sh_attention_q_block(uint32_t S, uint32_t dh, uint32_t H, uint32_t P);   /* sh_ops.h:123 same rule */
 /* sh_ops.h:127: ns stamps of the last attention call's last workgroup, from its first workgroup's start (phase 7
- * = 0): 0 start, 1-2 operands staged, 3-4 row maximum known, 5 every key block done, 6 stored (the kernels without
- * stamps report only 6, the launch's event time; all 0 when that call was sh_attention_batched or made under
- * stream capture, which carry no stamps). */
+ * = 0): 0 start, 1-2 operands staged, 3-4 first key block's scores / row maximum known, 5 every key block done,
+ * 6 stored (the kernels without stamps report only 6, the launch's event time; all 0 when that call was
+ * sh_attention_batched or made under stream capture, which carry no stamps). */
 uint32_t sh_attention_profile(uint32_t S, uint32_t dh, uint32_t phase);
 
 /* ---- Llama-style decoder ops (sh_ops.h:277-307, runtime/sh_llm.inc.c) -----------------------------------

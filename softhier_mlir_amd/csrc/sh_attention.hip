@@ -676,14 +676,15 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a, ui
 }
 
 // One-pass variant of k_flash2 (the default for aligned dh 64 / 128 heads whose scale folds, |c| <= 1, without a
-// token mask): each key block's scores come out of the MFMAs already shifted by the query's running maximum m (the
-// FOLD bias step: ones x (-m_hi, -m_lo)), so p = 2^acc. The first block sets m to its own maximum; a later block
-// whose maximum exceeds m by more than kTau (log2 units) moves m up to it, and only then are O and l rescaled by
-// 2^-shift and the block's scores computed again with the new bias (a wave-uniform branch, taken for the first
-// block and rarely after). Numerators therefore stay at or below 2^kTau, well inside fp16, and the row sums are the
-// sums of the same fp16 numerators the P.V product uses, so O / l is the softmax with every p rounded once. Against
-// k_flash2 this drops the maximum pass (its score MFMAs, K fragment reads and K DMAs) and the refill of the ring
-// between the passes. Same LDS ring, fragment prefetch and occupancy as k_flash2.
+// token mask): each key block's scores come out of the MFMAs already shifted by the query's reference m (the FOLD
+// bias step: ones x (-m_hi, -m_lo)), so p = 2^acc. m starts at 0 and moves to a block's maximum when that maximum
+// exceeds m by more than kTau (log2 units), or, for the first block, lies more than kTau below it; only then are O
+// and l rescaled by 2^-shift and the block's scores computed again with the new bias (a wave-uniform branch, rare
+// for attention inputs of moderate scale). m thus stays within kTau of the running maximum: numerators are at most
+// 2^kTau and the largest is at least 2^-kTau, well inside fp16's normal range, and the row sums are the sums of the
+// same fp16 numerators the P.V product uses, so O / l is the softmax with every p rounded once. Against k_flash2
+// this drops the maximum pass (its score MFMAs, K fragment reads and K DMAs) and the refill of the ring between the
+// passes. Same LDS ring, fragment prefetch and occupancy as k_flash2.
 constexpr float kTau = 8.f;
 template <int DH, int NST>
 __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, uint64_t *stamp) {
@@ -706,7 +707,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
     const uint32_t qw0 = qb * QPB + wave * QPW, myq = qw0 + r32;
     const uint32_t nkb = (S + KB - 1) / KB;
     const bool ragged = S % KB != 0;                 // the last key block is partial
-    // stamps (profile): 0-2 start, 3-4 first key block done (its maximum known), 5 all blocks done, 6 stored;
+    // stamps (profile): 0-2 start, 3-4 first key block done (the reference m set), 5 all blocks done, 6 stored;
     // 7 first workgroup
     const bool last = stamp && t == 0 && qb == gridDim.x - 1 && h == gridDim.y - 1 && b == gridDim.z - 1;
     attn_stamp(stamp, stamp && t == 0 && qb == 0 && h == 0 && b == 0, 7);
@@ -788,7 +789,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
 #pragma unroll
     for (int i = 0; i < DT; ++i) oacc[i] = sh_f16v{};
     float lsum = 0.f;                                // this lane's keys' fp16 numerators, summed in fp32
-    float mrun = 0.f;                                // running maximum of c s for this lane's query
+    float mrun = 0.f;                                // reference m of this lane's query (c s units)
     const sh_h2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
     for (uint32_t kb = 0; kb < nkb; ++kb) {
         sh_wait_vmcnt<(NST - 2) * 2 * KR>();
@@ -814,16 +815,16 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
 #pragma unroll
             for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sacc[tt][r]);
         bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-        const bool move = kb == 0 || bm > kTau;      // every block holds a valid key: bm is finite
-        if (__ballot(move) != 0) {                   // wave-uniform: m moves up, O and l rescale, scores again
+        // m starts at 0; the first block moves it when its maximum is more than kTau away on either side, a later one
+        // when its maximum exceeds m by more than kTau (every block holds a valid key: bm is finite)
+        const bool move = kb == 0 ? fabsf(bm) > kTau : bm > kTau;
+        if (__ballot(move) != 0) {                   // wave-uniform: m moves, O and l rescale, scores again
             const float shift = move ? bm : 0.f;
-            if (kb > 0) {
-                const float sc = sh_fast_exp2(-shift);
+            const float sc = sh_fast_exp2(-shift);
 #pragma unroll
-                for (int i = 0; i < DT; ++i) oacc[i] *= sc;
-                lsum *= sc;
-            }
-            mrun = (kb == 0 ? 0.f : mrun) + shift;
+            for (int i = 0; i < DT; ++i) oacc[i] *= sc;
+            lsum *= sc;
+            mrun += shift;
             set_bias(mrun);
             scores(st, sacc, true);
             mask_tail();
@@ -1125,8 +1126,8 @@ int sh_attention_gqa(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t S,
 }
 
 // ns since the first workgroup of the last stamped launch started (phase 7 = 0): 0 the last workgroup's start,
-// 1-2 its operands staged, 3-4 the maximum known (one-pass kernel: after the first key block; two-pass kernel:
-// pass 1 done), 5 every key block done (P.V), 6 stored. Kernels without stamps report only 6, as the launch's
+// 1-2 its operands staged, 3-4 the first key block's scores done (one-pass kernel) or the row maximum known
+// (two-pass kernel: pass 1 done), 5 every key block done (P.V), 6 stored. Kernels without stamps report only 6, as the launch's
 // event time.
 uint32_t sh_attention_profile(uint32_t, uint32_t, uint32_t phase) {
     if (!g_prof.valid) return 0;

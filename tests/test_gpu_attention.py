@@ -116,6 +116,26 @@ def test_scale_edge_cases(lib, gpu, scale):
     assert bad == 0, err
 
 
+@pytest.mark.parametrize("S", [256, 230])
+def test_running_reference_moves(lib, gpu, S):
+    """Scores laid out so the one-pass kernel's reference m moves in every way it can: the first key block's scaled
+    scores sit near -30 (m moves down from 0), the second near -10 and the third near +5 (m moves up by more than 8
+    after the first block), the last near 0 (no move; with S = 230 a partial block). Every query sees the same
+    score pattern (q rows of ones), the keys add a little noise, V is random."""
+    dh, scale = 64, 0.125
+    c = scale * np.log2(np.e)
+    rng = np.random.default_rng(7)
+    level = np.select([np.arange(S) < 64, np.arange(S) < 128, np.arange(S) < 192], [-30.0, -10.0, 5.0], 0.0)
+    q = np.ones((S, dh), np.float32)
+    k = (level[:, None] / (c * dh) + 0.05 * rng.standard_normal((S, dh))).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal((S, dh)).astype(np.float16).astype(np.float32)
+    O = _zeros(S, dh)
+    assert lib.sh_attention_batched(A(to_dev(q)), A(to_dev(k)), A(to_dev(v)), A(O), 1, S, dh, 1, dh, dh, dh, dh,
+                                    0, 0, 0, 0, scale, 0) == 0, shops.last_error()
+    bad, err, _ = refs.close(to_np(O), refs.attention(q, k, v, 1, scale))
+    assert bad == 0, err
+
+
 def test_profile_reports_the_kernel_time(lib, gpu):
     S, D, H = 256, 768, 12
     q = to_dev(data.normal((S, D), 1))
@@ -128,8 +148,8 @@ def test_profile_reports_the_kernel_time(lib, gpu):
 @pytest.mark.parametrize("S", [256, 1024])
 def test_profile_phase_stamps_are_monotone(lib, gpu, S):
     """sh_attention_profile (reference sh_attention.inc.c:67-76, sh_ops.h:124-127): the last workgroup's stamps in
-    ns from the first workgroup's start (phase 7 = 0): start (0) <= operands staged (1, 2) <= maximum known (3, 4;
-    the one-pass kernel: after the first key block) <= every key block done (5) <= stored (6). A batched call leaves
+    ns from the first workgroup's start (phase 7 = 0): start (0) <= operands staged (1, 2) <= first key block's
+    scores (3, 4) <= every key block done (5) <= stored (6). A batched call leaves
     no stamps (every phase reads 0)."""
     D, H = 768, 12
     q = to_dev(data.normal((S, D), 3))
