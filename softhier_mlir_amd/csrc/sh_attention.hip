@@ -790,6 +790,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
     for (int i = 0; i < DT; ++i) oacc[i] = sh_f16v{};
     float lsum = 0.f;                                // this lane's keys' fp16 numerators, summed in fp32
     float mrun = 0.f;                                // reference m of this lane's query (c s units)
+    bool biased = false;                             // some lane's m left 0 (wave-uniform): the bias step is needed
     const sh_h2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
     for (uint32_t kb = 0; kb < nkb; ++kb) {
         sh_wait_vmcnt<(NST - 2) * 2 * KR>();
@@ -806,7 +807,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
                         if (kb * KB + 32 * tt + 8 * (r >> 2) + 4 * g + (r & 3) >= S) sacc[tt][r] = -INFINITY;
             }
         };
-        scores(st, sacc, kb > 0);
+        scores(st, sacc, biased);                    // (while every m is 0 the bias step would add zeros)
         mask_tail();
         // the block's maximum for this lane's query (lanes r32 and r32 + 32 hold complementary keys)
         float bm = -INFINITY;
@@ -826,6 +827,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
             lsum *= sc;
             mrun += shift;
             set_bias(mrun);
+            biased = true;
             scores(st, sacc, true);
             mask_tail();
         }
