@@ -206,10 +206,12 @@ def test_softmax_short_rows(lib, gpu, cols, scale):
     assert (xi[:, cols:].view(np.uint16) == x[:, cols:].view(np.uint16)).all()
 
 
-@pytest.mark.parametrize("nbytes,so,do", [(16 << 20, 0, 0), (4096 + 48, 16, 32), (1000003, 3, 5), (1, 0, 7)])
+@pytest.mark.parametrize("nbytes,so,do", [(16 << 20, 0, 0), (4096 + 48, 16, 32), (1000003, 3, 5), (1, 0, 7),
+                                         ((256 << 20) + 48, 16, 32)])
 def test_dma_copy_moves_every_byte(lib, gpu, nbytes, so, do):
-    """sh_dma_copy (sh_ops.h:218): a 1-D copy of exactly `bytes`, aligned (streaming 16-byte path) or not (byte
-    path), leaving the bytes around the destination range untouched."""
+    """sh_dma_copy (sh_ops.h:218): a 1-D copy of exactly `bytes`, aligned (streaming 16-byte path; above 256 MiB one
+    chunk per thread with nontemporal stores) or not (byte path), leaving the bytes around the destination range
+    untouched."""
     import torch
     g = torch.Generator(device="cuda").manual_seed(5)
     src = torch.randint(0, 256, (nbytes + so + 64,), dtype=torch.uint8, device="cuda", generator=g)
@@ -218,3 +220,30 @@ def test_dma_copy_moves_every_byte(lib, gpu, nbytes, so, do):
     torch.cuda.synchronize()
     assert torch.equal(dst[do:do + nbytes], src[so:so + nbytes])
     assert (dst[:do] == 0xA5).all() and (dst[do + nbytes:] == 0xA5).all()
+
+
+def test_elementwise_above_the_infinity_cache(lib, gpu):
+    """Outputs of 256 MiB and more take the one-item-per-thread launch with nontemporal stores: on a [131072 x 1024]
+    tensor tiled from one 64-row block, every block of the GELU, add_bias and scale outputs equals the library's
+    result on the block alone (bit for bit: the same element-wise function), and add of integers is exact."""
+    import torch
+    rows, cols, blk = 131072, 1024, 64
+    x = data.normal((blk, cols), 41, 0.0, 2.0)
+    be = data.normal((1, cols), 42, 0.0, 0.1)
+    Xs, BE = to_dev(x), to_dev(be)
+    Xb = Xs.repeat(rows // blk, 1)
+    Ys, Yb = _empty(blk, cols), _empty(rows, cols)
+    for name, call in (("gelu", lambda y, x_, r: lib.sh_gelu(A(y), A(x_), r, cols, cols, ALL)),
+                       ("add_bias", lambda y, x_, r: lib.sh_add_bias(A(y), A(x_), A(BE), r, cols, cols, ALL)),
+                       ("scale", lambda y, x_, r: lib.sh_scale(A(y), A(x_), r, cols, cols, -1.75, ALL))):
+        call(Ys, Xs, blk)
+        call(Yb, Xb, rows)
+        torch.cuda.synchronize()
+        want = Ys.view(torch.int16).repeat(rows // blk, 1)
+        assert torch.equal(Yb.view(torch.int16), want), name
+    assert refs.close(to_np(Ys), refs.scale(x, -1.75))[0] == 0
+    ints = to_dev(lcg.fill_fp16(blk, cols, 43, -512, 512)).repeat(rows // blk, 1)
+    lib.sh_add(A(Yb), A(ints), A(ints), rows, cols, cols, ALL)
+    torch.cuda.synchronize()
+    assert torch.equal(Yb, ints * 2)
+
