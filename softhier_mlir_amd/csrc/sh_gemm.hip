@@ -1037,13 +1037,17 @@ __device__ __forceinline__ void store_all(const GemmArgs &a, const uint4 (&q)[FM
 // reads any more), then each store instruction writes 64 consecutive 16-byte chunks of those rows (whole row segments
 // of the block) instead of 32 rows x 32 bytes. The residual of the epilogue chain is added to the row chunks here
 // (the chain up to it was applied to q without it; the same fp16 adds, so the same bits). LDS instructions of
-// one wavefront execute in order, so no barrier is involved.
+// one wavefront execute in order, so no barrier is involved. Chunk lin of the row-major copy sits at lin ^ (row &
+// 15) within its 16-chunk line: the staging writes (lanes 0-31 at rows 0-31, CPRW chunks apart) then hit 16
+// distinct 16-byte bank groups per 16 lanes instead of 16 / gcd(CPRW, 16) of them (4- to 16-way conflicts), and
+// the reads of 16 consecutive chunks stay a permutation of one line.
 template <int TM, int TN, int FM, int FN, int NSLOT, int SSTRIDE>
 __device__ __forceinline__ void store_wave_staged(const GemmArgs &a, const uint4 (&q)[FM][FN][2], uint32_t rbase, uint32_t cbase,
                                                   char *slots) {
     constexpr int CPRW = TN / 8, HALF = 32 * CPRW, STEPS = HALF / 64;
     static_assert(HALF % 64 == 0 && STEPS <= NSLOT, "32 rows of the block fit in the wavefront's slots");
     const int lane = threadIdx.x & 63, g = lane >> 5, r32 = lane & 31;
+    auto phys = [](int lin) { return lin ^ ((lin / CPRW) & 15); };      // stays inside lin's 16-chunk line
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
         uint4 rq[STEPS];
@@ -1057,13 +1061,13 @@ __device__ __forceinline__ void store_wave_staged(const GemmArgs &a, const uint4
         for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
-                const int lin = r32 * CPRW + 4 * j + 2 * p + g;
-                *(uint4 *)(slots + (lin / 64) * SSTRIDE + (lin % 64) * 16) = q[i][j][p];
+                const int pl = phys(r32 * CPRW + 4 * j + 2 * p + g);
+                *(uint4 *)(slots + (pl / 64) * SSTRIDE + (pl % 64) * 16) = q[i][j][p];
             }
 #pragma unroll
         for (int u = 0; u < STEPS; ++u) {
             const int lin = u * 64 + lane, row = lin / CPRW, c = lin % CPRW;
-            uint4 v = *(const uint4 *)(slots + u * SSTRIDE + lane * 16);
+            uint4 v = *(const uint4 *)(slots + u * SSTRIDE + (phys(lin) % 64) * 16);
             if (a.res) v = make_uint4(sh_hadd2(v.x, rq[u].x), sh_hadd2(v.y, rq[u].y), sh_hadd2(v.z, rq[u].z), sh_hadd2(v.w, rq[u].w));
             const uint32_t gm = rbase + 32 * i + row, gn = cbase + 8 * c;
             if (gm < a.M && gn < a.N) *(uint4 *)(a.z + (uint64_t)gm * a.ldz + gn) = v;
