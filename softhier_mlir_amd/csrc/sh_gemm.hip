@@ -1041,13 +1041,20 @@ __device__ __forceinline__ void store_all(const GemmArgs &a, const uint4 (&q)[FM
 // 15) within its 16-chunk line: the staging writes (lanes 0-31 at rows 0-31, CPRW chunks apart) then hit 16
 // distinct 16-byte bank groups per 16 lanes instead of 16 / gcd(CPRW, 16) of them (4- to 16-way conflicts), and
 // the reads of 16 consecutive chunks stay a permutation of one line.
-template <int TM, int TN, int FM, int FN, int NSLOT, int SSTRIDE>
+// The slots may span NSTG free stages of the ring: slot s is slot s % NSLOT of stage (first + s / NSLOT) mod nst,
+// stages stage_bytes apart from `ring` (the ring base plus the wavefront's offset in a slot).
+template <int TM, int TN, int FM, int FN, int NSLOT, int SSTRIDE, int NSTG = 1>
 __device__ __forceinline__ void store_wave_staged(const GemmArgs &a, const uint4 (&q)[FM][FN][2], uint32_t rbase, uint32_t cbase,
-                                                  char *slots) {
+                                                  char *ring, uint32_t first, uint32_t nst, uint32_t stage_bytes) {
     constexpr int CPRW = TN / 8, HALF = 32 * CPRW, STEPS = HALF / 64;
-    static_assert(HALF % 64 == 0 && STEPS <= NSLOT, "32 rows of the block fit in the wavefront's slots");
+    static_assert(HALF % 64 == 0 && STEPS <= NSLOT * NSTG, "32 rows of the block fit in the wavefront's slots");
     const int lane = threadIdx.x & 63, g = lane >> 5, r32 = lane & 31;
     auto phys = [](int lin) { return lin ^ ((lin / CPRW) & 15); };      // stays inside lin's 16-chunk line
+    auto slot = [&](int sl) -> char * {
+        uint32_t st = first + (uint32_t)(sl / NSLOT);
+        if (st >= nst) st -= nst;
+        return ring + (size_t)st * stage_bytes + (size_t)(sl % NSLOT) * SSTRIDE;
+    };
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
         uint4 rq[STEPS];
@@ -1062,12 +1069,12 @@ __device__ __forceinline__ void store_wave_staged(const GemmArgs &a, const uint4
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
                 const int pl = phys(r32 * CPRW + 4 * j + 2 * p + g);
-                *(uint4 *)(slots + (pl / 64) * SSTRIDE + (pl % 64) * 16) = q[i][j][p];
+                *(uint4 *)(slot(pl / 64) + (pl % 64) * 16) = q[i][j][p];
             }
 #pragma unroll
         for (int u = 0; u < STEPS; ++u) {
             const int lin = u * 64 + lane, row = lin / CPRW, c = lin % CPRW;
-            uint4 v = *(const uint4 *)(slots + u * SSTRIDE + (phys(lin) % 64) * 16);
+            uint4 v = *(const uint4 *)(slot(u) + (phys(lin) % 64) * 16);
             if (a.res) v = make_uint4(sh_hadd2(v.x, rq[u].x), sh_hadd2(v.y, rq[u].y), sh_hadd2(v.z, rq[u].z), sh_hadd2(v.w, rq[u].w));
             const uint32_t gm = rbase + 32 * i + row, gn = cbase + 8 * c;
             if (gm < a.M && gn < a.N) *(uint4 *)(a.z + (uint64_t)gm * a.ldz + gn) = v;
@@ -1396,7 +1403,8 @@ __global__ __launch_bounds__(256, MINW) void k_gemm5(GemmArgs a) {
     // epilogue operands loaded early (PRE): fp16 bias chunks and residual chunks of this lane's outputs
     // (the largest tiles keep their registers for the accumulators: no early loads there)
     // (unsplit tiles are stored through each wavefront's DMA slots, and the residual is added there: no early load)
-    constexpr bool STAGED = !SPLIT && 4 * TN <= 64 * C::LOADS;
+    // (the staging may use every stage but the last slice's: NST - 1 stages of LOADS 1 KB slots per wavefront)
+    constexpr bool STAGED = !SPLIT && 4 * TN <= 64 * C::LOADS * (NST - 1);
     constexpr bool PRE_B = PRE && FM * FN <= 12, PRE_RES = PRE && FM * FN <= 6 && !STAGED;
     uint4 bq[PRE_B ? FN : 1][2], rq[PRE_RES ? FM : 1][PRE_RES ? FN : 1][2];
     // (a GEMM that also writes row partials adds the residual in the chain, before them)
@@ -1490,13 +1498,15 @@ __global__ __launch_bounds__(256, MINW) void k_gemm5(GemmArgs a) {
         }
         if (a.stats_out) stats_zt<FM, FN>(a, qc, m0 + wm * TM, n0 + wn * TN);
         if constexpr (STAGED) {
-            // stage KT % NST holds no slice (only the clamped tail DMAs, each wavefront's into its own slots); its
-            // last reads were slice KT - NST's, finished before the barrier of a later slice
+            // every stage but slice KT - 1's holds no slice any more (only the clamped tail DMAs, each wavefront's
+            // into its own slots): their last reads were slices <= KT - 2, finished before slice KT - 1's barrier
             sh_wait_vmcnt<0>();                      // this wavefront's tail DMAs have landed
-            char *slots = (char *)smem + (size_t)(KT % NST) * C::STAGE + (size_t)wave * 1024;
+            constexpr int NSTG = (4 * TN + 64 * C::LOADS - 1) / (64 * C::LOADS);      // stages the block needs
             GemmArgs as = a;
             if (!stage_res) as.res = nullptr;        // already added in the chain
-            store_wave_staged<TM, TN, FM, FN, C::LOADS, 4096>(as, qc, m0 + wm * TM, n0 + wn * TN, slots);
+            store_wave_staged<TM, TN, FM, FN, C::LOADS, 4096, NSTG>(as, qc, m0 + wm * TM, n0 + wn * TN,
+                                                                     (char *)smem + (size_t)wave * 1024, (uint32_t)(KT % NST),
+                                                                     (uint32_t)NST, (uint32_t)C::STAGE);
         } else {
             store_all<BM, BN, FM, FN>(a, qc, m0, n0, wm, wn);
         }
@@ -1740,10 +1750,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void k_gemm6(GemmArgs a) {
         if constexpr (STAGED) {
             // stage KT % NST holds no slice (only the clamped tail DMAs, each wavefront's into its own slots)
             sh_wait_vmcnt<0>();                          // this wavefront's tail DMAs have landed
-            char *slots = (char *)smem + (size_t)(KT % NST) * C::STAGE + (size_t)wave * 1024;
             GemmArgs as = a;
             if (!stage_res) as.res = nullptr;            // already added in the chain
-            store_wave_staged<TM, TN, FM, FN, C::LOADS, NT * 16>(as, qc, m0 + wm * TM, n0 + wn * TN, slots);
+            store_wave_staged<TM, TN, FM, FN, C::LOADS, NT * 16>(as, qc, m0 + wm * TM, n0 + wn * TN,
+                                                                  (char *)smem + (size_t)wave * 1024, (uint32_t)(KT % NST),
+                                                                  (uint32_t)NST, (uint32_t)C::STAGE);
         } else {
 #pragma unroll
             for (int i = 0; i < FM; ++i)
