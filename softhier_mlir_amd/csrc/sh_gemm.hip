@@ -62,7 +62,8 @@ struct GemmArgs {
 // (mu, r = 1 / sqrt(var + eps)) of row gm for the LayerNorm fold: given (ln_parts == 0), or formed from the row's
 // ln_parts partials (s_b, M2_b) of 32 columns each (Chan, Golub and LeVeque, "Algorithms for computing the sample
 // variance", 1983): mu = sum s_b / n, M2 = sum_b (M2_b + 32 (s_b / 32 - mu)^2), var = M2 / n, n = 32 ln_parts,
-// sums in block order. Up to 32 partials (K <= 1024) are loaded at once into registers, 16 bytes per load, and
+// sums in block order. Up to 32 partials (K <= 1024) are loaded at once into registers, 16 bytes per load (only the
+// P / 2 loads the row has: the partials are re-read by every column tile, so their volume is what this costs), and
 // summed twice; more are read twice from memory. Every consumer (register epilogues, split-K reduction) forms the
 // statistics with this one function.
 __device__ __forceinline__ float2 ln_row(const GemmArgs &a, uint32_t gm) {
@@ -71,22 +72,21 @@ __device__ __forceinline__ float2 ln_row(const GemmArgs &a, uint32_t gm) {
     const float2 *pp = (const float2 *)a.ln_stats + (uint64_t)gm * P;
     const float inv_n = 1.f / (32.f * (float)P);
     float s = 0.f, m2 = 0.f;
-    if (P <= 32 && P % 2 == 0) {                     // no branches: absent blocks re-read the last one, weight 0
-        const uint32_t last = P / 2 - 1;
+    if (P <= 32 && P % 2 == 0) {
+        const uint32_t last = P / 2 - 1;             // wave-uniform: the branches below skip whole loads
         float4 q[16];
-        float wgt[16];
 #pragma unroll
-        for (int h = 0; h < 16; ++h) {
-            q[h] = ((const float4 *)pp)[min((uint32_t)h, last)];
-            wgt[h] = (uint32_t)h <= last ? 1.f : 0.f;
-        }
+        for (int h = 0; h < 16; ++h)
+            if ((uint32_t)h <= last) q[h] = ((const float4 *)pp)[h];
 #pragma unroll
-        for (int h = 0; h < 16; ++h) s = fmaf(wgt[h], q[h].x + q[h].z, s);
+        for (int h = 0; h < 16; ++h)
+            if ((uint32_t)h <= last) s += q[h].x + q[h].z;
         const float mu = s * inv_n;
 #pragma unroll
         for (int h = 0; h < 16; ++h) {
+            if ((uint32_t)h > last) continue;
             const float d0 = fmaf(q[h].x, 1.f / 32.f, -mu), d1 = fmaf(q[h].z, 1.f / 32.f, -mu);
-            m2 = fmaf(wgt[h], fmaf(32.f * d0, d0, q[h].y) + fmaf(32.f * d1, d1, q[h].w), m2);
+            m2 += fmaf(32.f * d0, d0, q[h].y) + fmaf(32.f * d1, d1, q[h].w);
         }
         return make_float2(mu, sh_fast_rsq(fmaf(m2, inv_n, a.ln_eps)));
     }
