@@ -199,6 +199,8 @@ uint64_t    sh_captured(char *buf, uint64_t cap);
 
 /* Split-K GEMM: K is cut into `splits` contiguous ranges computed by separate workgroups into an fp32
  * workspace owned by the library, then reduced in a fixed order (deterministic) and rounded once to fp16.
+ * Two equal ranges (K % 128 == 0) run in one workgroup per tile instead, whose two halves add their fp32 sums
+ * in that same order: the same bits, no workspace, no reduction launch.
  * Shape/tile checks as sh_gemm (-1/-2); splits == 0 lets the library choose. */
 int sh_gemm_splitk(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
                    uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg, uint32_t splits, uint32_t cluster);

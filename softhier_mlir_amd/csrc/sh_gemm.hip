@@ -1302,18 +1302,28 @@ struct Cfg5 {
     static_assert(NST >= 2 && LOADS * (NST - 2) < 64 && LDS <= 160 * 1024, "resources");
 };
 
-template <int BM, int BN, int SK, int NST, bool WT, int MINW, bool SPLIT, bool PRE>
-__global__ __launch_bounds__(256, MINW) void k_gemm5(GemmArgs a) {
+// KG = 2: in-workgroup split-K. Two groups of four wavefronts (512 threads, two rings) compute one tile; group g
+// runs the slices of K range g (a.kps each, both ranges the same length, so both groups pass the same barriers)
+// through its own ring, then group 1 hands its fp32 accumulators to group 0 through its ring and group 0 adds them
+// (first range + second, as the reduction adds two partials) and runs the unsplit epilogue: the bits of the
+// two-partial path without the partials' HBM traffic or the reduction launch. One workgroup holds a CU, with two
+// wavefronts per SIMD where a tile grid of one workgroup per CU would leave one.
+template <int BM, int BN, int SK, int NST, bool WT, int MINW, bool SPLIT, bool PRE, int KG = 1>
+__global__ __launch_bounds__(256 * KG, MINW) void k_gemm5(GemmArgs a) {
     using C = Cfg5<BM, BN, SK, NST, WT>;
     constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, NS = C::NS, XCPR = C::XCPR;
+    static_assert(KG == 1 || (KG == 2 && !SPLIT && 2 * C::LDS <= 160 * 1024 && 16 * FN * 1024 <= (int)C::LDS), "k groups");
     extern __shared__ uint4 smem[];
     const int t = threadIdx.x, lane = t & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wave = __builtin_amdgcn_readfirstlane((t >> 6) & 3);
+    const int grp = KG > 1 ? __builtin_amdgcn_readfirstlane(t >> 8) : 0;
     const int wm = wave >> 1, wn = wave & 1, g = lane >> 5, r32 = lane & 31;
+    uint4 *const ring = smem + (size_t)grp * (C::LDS / 16);     // this group's stages
 
-    const uint32_t nblk = a.tiles_m * a.tiles_n * a.splits;
+    const uint32_t nblk = a.tiles_m * a.tiles_n * (KG > 1 ? 1u : a.splits);
     uint32_t tm, tn, split;
     tile_of(a, blockIdx.x, nblk, tm, tn, split);
+    if constexpr (KG > 1) split = (uint32_t)grp;
     const uint32_t m0 = tm * BM, n0 = tn * BN;
     const uint32_t kbeg = split * a.kps;
     const uint32_t kend = min(a.K, kbeg + a.kps);
@@ -1342,7 +1352,7 @@ __global__ __launch_bounds__(256, MINW) void k_gemm5(GemmArgs a) {
         }
     }
     const uint64_t wadv = WT ? (uint64_t)SK : (uint64_t)SK * a.ldw;
-    const uint32_t lds0 = sh_lds_addr(smem);
+    const uint32_t lds0 = sh_lds_addr(ring);
     const uint32_t wave_off = (uint32_t)wave * 1024u;
     auto dma = [&](int d, int src, int stage) {          // DMA instruction d of slice `src` into `stage`
         const uint32_t st = lds0 + (uint32_t)stage * (uint32_t)C::STAGE;
@@ -1363,12 +1373,12 @@ __global__ __launch_bounds__(256, MINW) void k_gemm5(GemmArgs a) {
         const uint32_t sb = (uint32_t)stage * (uint32_t)C::STAGE;
         const uint32_t c = (uint32_t)(2 * s + g);
         if (r < FM) {
-            const uint4 *X = (const uint4 *)((const char *)smem + sb);
+            const uint4 *X = (const uint4 *)((const char *)ring + sb);
             const uint32_t m = (uint32_t)(wm * TM + r * 32 + r32);
             xf[buf][r] = __builtin_bit_cast(sh_h8, X[m * XCPR + (c ^ xswz<SK>(m))]);
         } else if constexpr (WT) {
             const int j = r - FM;
-            const uint4 *W = (const uint4 *)((const char *)smem + sb + C::XCH * 16);
+            const uint4 *W = (const uint4 *)((const char *)ring + sb + C::XCH * 16);
             const uint32_t n = (uint32_t)(wn * TN + j * 32 + r32);
             wf[buf][j] = __builtin_bit_cast(sh_h8, W[n * XCPR + (c ^ xswz<SK>(n))]);
         } else {
@@ -1409,7 +1419,7 @@ __global__ __launch_bounds__(256, MINW) void k_gemm5(GemmArgs a) {
     uint4 bq[PRE_B ? FN : 1][2], rq[PRE_RES ? FM : 1][PRE_RES ? FN : 1][2];
     // (a GEMM that also writes row partials adds the residual in the chain, before them)
     const bool stage_res = STAGED && !a.stats_out;
-    const bool pre_ok = PRE_B && !a.accumulate && !(a.bias && a.bias_fp32) && (PRE_RES || stage_res || !a.res);
+    const bool pre_ok = PRE_B && grp == 0 && !a.accumulate && !(a.bias && a.bias_fp32) && (PRE_RES || stage_res || !a.res);
     auto prefetch = [&]() {
 #pragma unroll
         for (int j = 0; j < (PRE_B ? FN : 0); ++j)
@@ -1471,6 +1481,35 @@ __global__ __launch_bounds__(256, MINW) void k_gemm5(GemmArgs a) {
     for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wfrag((NS - 1) & 1, j), xf[(NS - 1) & 1][i], acc[i][j], 0, 0, 0);
+    if constexpr (KG > 1) {
+        sh_wait_vmcnt<0>();          // the clamped tail DMAs into the rings have landed ...
+        __syncthreads();             // ... for every wavefront, and every read of group 1's ring is done
+        // per row block i of fragments: 16 FN KB of group 1's ring, lane-contiguous 16-byte slots
+        float4 *park = (float4 *)((char *)smem + C::LDS) + wave * (FN * 4 * 64) + lane;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            if (grp == 1) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        park[(j * 4 + e) * 64] = make_float4(acc[i][j][4 * e], acc[i][j][4 * e + 1], acc[i][j][4 * e + 2], acc[i][j][4 * e + 3]);
+            }
+            __syncthreads();
+            if (grp == 0) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float4 v = park[(j * 4 + e) * 64];
+                        acc[i][j][4 * e] += v.x; acc[i][j][4 * e + 1] += v.y;
+                        acc[i][j][4 * e + 2] += v.z; acc[i][j][4 * e + 3] += v.w;
+                    }
+            }
+            if (i + 1 < FM) __syncthreads();          // group 0 has read the block before group 1 overwrites it
+        }
+        if (grp == 1) return;        // no barrier follows: group 0 stores through its own ring
+    }
     if constexpr (SPLIT) {
         store_partials_zt<BM, BN, FM, FN>(a, acc, m0, n0, split, wm, wn);
     } else {
@@ -1853,6 +1892,7 @@ struct KCfg {
     bool ktail = false; KernelFn tail[2] = {nullptr, nullptr};     // the K % 64 != 0 variants (unsplit, split)
     bool wt = false; KernelFn wt_vec[2] = {nullptr, nullptr}, wt_scalar[2] = {nullptr, nullptr};
     bool reg = false;            // the unsplit epilogue applies a LayerNorm fold and writes row partials from registers
+    KernelFn kg2 = nullptr;      // in-workgroup split-K over two equal K ranges (512 threads, two rings: 2 x lds bytes)
 };
 
 #define SH_KCFG(BM, BN, EFF) { BM, BN, 2, false, { k_gemm<BM, BN, true, false>, k_gemm<BM, BN, true, true> }, \
@@ -1879,6 +1919,11 @@ struct KCfg {
                                               k_gemm5<BM, BN, SK, NST, false, W, true, true> }, \
                                             { nullptr, nullptr }, Cfg5<BM, BN, SK, NST, false>::LDS, EFF, false, 256, \
                                             false, { nullptr, nullptr }, false, { nullptr, nullptr }, { nullptr, nullptr }, true }
+#define SH_KCFG5K(BM, BN, SK, NST, W, EFF) { BM, BN, NST, true, { k_gemm5<BM, BN, SK, NST, false, W, false, true>, \
+                                               k_gemm5<BM, BN, SK, NST, false, W, true, true> }, \
+                                             { nullptr, nullptr }, Cfg5<BM, BN, SK, NST, false>::LDS, EFF, false, 256, \
+                                             false, { nullptr, nullptr }, false, { nullptr, nullptr }, { nullptr, nullptr }, true, \
+                                             k_gemm5<BM, BN, SK, NST, false, 1, false, true, 2> }
 #define SH_KCFG3(BM, BN, EFF) { BM, BN, 2, true, { k_gemm3<BM, BN, false>, k_gemm3<BM, BN, true> }, \
                                 { nullptr, nullptr }, Cfg3<BM, BN>::LDS, EFF, false, 512 }
 // eff = sustained fraction of the MFMA peak per CU measured for each tile on MI355X (tile-time model of
@@ -1923,7 +1968,7 @@ KCfg g_cfgs[] = {
     SH_KCFG5(256, 192, 64, 2, 1, 0.38f),
     SH_KCFG5(256, 192, 32, 4, 1, 0.38f),
     SH_KCFG5(128, 192, 64, 3, 1, 0.36f),
-    SH_KCFG5(128, 192, 64, 2, 2, 0.36f),
+    SH_KCFG5K(128, 192, 64, 2, 2, 0.36f),
     SH_KCFG5(128, 256, 64, 2, 1, 0.36f),
     SH_KCFG5(256, 128, 64, 2, 1, 0.36f),
     // W^T operand (sh_gemm_ex_wt): 4 / 8 wavefronts, up to 256 x 384 tiles (k_gemm6)
@@ -1941,7 +1986,7 @@ KCfg g_cfgs[] = {
     SH_KCFG6(128, 64, 2, 2, 32, 4, 2, false, true, 0.16f),
     SH_KCFG6(64, 128, 2, 2, 32, 4, 2, false, true, 0.16f),
     SH_KCFG6(128, 128, 2, 2, 32, 4, 2, true, true, 0.25f),
-    SH_KCFG5(128, 192, 32, 4, 2, 0.36f),        // two workgroups per CU with a deeper ring of 32-k slices
+    SH_KCFG5K(128, 192, 32, 4, 2, 0.36f),       // two workgroups per CU with a deeper ring of 32-k slices
     SH_KCFG5(128, 128, 64, 2, 2, 0.30f),
     SH_KCFG5(128, 128, 32, 4, 2, 0.30f),
 };
@@ -1952,6 +1997,7 @@ KCfg g_cfgs[] = {
 #undef SH_KCFG4R
 #undef SH_KCFG4S
 #undef SH_KCFG5
+#undef SH_KCFG5K
 #undef SH_KCFG6
 constexpr int kNumCfg = sizeof(g_cfgs) / sizeof(g_cfgs[0]);
 
@@ -2060,6 +2106,7 @@ void set_attrs(KCfg &c) {
         if (c.wt_vec[v]) (void)hipFuncSetAttribute((const void *)c.wt_vec[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
         if (c.wt_scalar[v]) (void)hipFuncSetAttribute((const void *)c.wt_scalar[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
     }
+    if (c.kg2) (void)hipFuncSetAttribute((const void *)c.kg2, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(2 * c.lds));
     c.attr_set = true;
 }
 
@@ -2235,26 +2282,39 @@ int launch(const GemmReq &r, const char *name) {
         set_epi(t);
         p.cfg = tuned_cfg(t, p.cfg, sh_stream(), r.wt);
     }
-    KCfg &c = g_cfgs[p.cfg];
     const SplitK sk = split_k(r.K, p.splits);
     const uint32_t splits = sk.splits, kps = sk.kps;
-    const bool partials = splits > 1 || ((ln || stats) && !(want_reg && c.reg));
+    // Two equal K ranges (a caller's request for 2 splits, K % 128 == 0) planned on a direct-to-LDS tile run
+    // in-workgroup (k_gemm5 KG = 2): that family's bits for two partials and the reduction, without either (the
+    // register-staged tiles accumulate in another order). The planned tile if it has the variant, else the first
+    // that has. SH_GEMM_KG=0: the partials path (tests compare the two).
+    int kgc = -1;
+    if (fast && !r.wt && splits == 2 && 2 * kps == r.K && g_cfgs[p.cfg].v2 && (!(ln || stats) || want_reg) &&
+        env_int("SH_GEMM_KG", 1)) {
+        for (int i = 0; i < kNumCfg && kgc < 0; ++i)
+            if (g_cfgs[i].kg2) kgc = i;
+        if (g_cfgs[p.cfg].kg2) kgc = p.cfg;
+    }
+    const bool kg2 = kgc >= 0;
+    KCfg &c = g_cfgs[kg2 ? kgc : p.cfg];
+    const bool partials = !kg2 && (splits > 1 || ((ln || stats) && !(want_reg && c.reg)));
 
     GemmArgs a{};
     a.x = (const uint16_t *)r.x; a.w = (const uint16_t *)r.w; a.z = (uint16_t *)r.z;
     a.bias = (const void *)bias; a.res = (const uint16_t *)res;
     a.ldx = r.ldx; a.ldw = r.ldw; a.ldz = r.ldz; a.ldr = ldr;
     a.M = r.M; a.N = r.N; a.K = r.K; a.kps = kps;
-    a.tiles_m = sh_cdiv(r.M, c.bm); a.tiles_n = sh_cdiv(r.N, c.bn); a.splits = splits;
+    a.tiles_m = sh_cdiv(r.M, c.bm); a.tiles_n = sh_cdiv(r.N, c.bn); a.splits = kg2 ? 1 : splits;
     a.accumulate = r.accumulate; a.bias_fp32 = (e && e->bias_fmt == SH_BIAS_FP32) ? 1 : 0; a.act = e ? e->act : 0;
     set_epi(a);
-    const uint64_t nblk64 = (uint64_t)a.tiles_m * a.tiles_n * splits;
+    const uint64_t nblk64 = (uint64_t)a.tiles_m * a.tiles_n * a.splits;
     if (nblk64 > 0x7FFFFFFFull) { sh_set_error(-1, "[%s] problem too large", name); return -1; }
     const uint32_t nblk = grid_of(a);
 
     hipStream_t st = sh_stream();
     const bool split = partials;
-    KernelFn fn = r.wt ? (c.v2 ? c.vec[split] : vec ? c.wt_vec[split] : c.wt_scalar[split])
+    KernelFn fn = kg2 ? c.kg2
+                : r.wt ? (c.v2 ? c.vec[split] : vec ? c.wt_vec[split] : c.wt_scalar[split])
                        : (c.v2 && !fast) ? c.tail[split] : (vec || c.v2) ? c.vec[split] : c.scalar[split];   // !fast: K % 64 != 0
     set_attrs(c);
     if (split) {
@@ -2271,7 +2331,7 @@ int launch(const GemmReq &r, const char *name) {
             if (!a.part) return SH_EHIP;
         }
     }
-    hipLaunchKernelGGL(fn, dim3(nblk), dim3(c.threads), c.lds, st, a);
+    hipLaunchKernelGGL(fn, dim3(nblk), dim3(kg2 ? 2 * c.threads : c.threads), kg2 ? 2 * c.lds : c.lds, st, a);
     if (!sh_launch_ok(name)) return SH_EHIP;
     if (split) {
         const bool rvec = vec;

@@ -288,6 +288,80 @@ def test_splitk_matches_and_is_deterministic(lib, gpu):
     assert bad == 0, err
 
 
+KG2_CFGS = (38, 55)      # tiles with the in-workgroup split-K variant (k_gemm5 KG = 2)
+
+
+@pytest.mark.parametrize("M,N,K", [(1000, 760, 768), (520, 768, 3072), (8192, 768, 3072), (300, 256, 128)])
+def test_in_workgroup_split_k_stores_the_two_partial_bits(lib, gpu, monkeypatch, M, N, K):
+    """A request for two K ranges with K % 128 == 0 runs as one workgroup per tile whose two wavefront groups each
+    take one range and add their fp32 accumulators in LDS (k_gemm5 KG = 2). Its outputs are the bits of the
+    two-partial path on the same tile (SH_GEMM_KG=0: fp32 partials in HBM, the reduction adds first + second; a plan
+    on a register-staged tile, which accumulates in another order, keeps that path) for every epilogue:
+    none, bias + GELU, bias + residual with accumulate, the LayerNorm fold with GELU, and bias + residual writing
+    row partials (those match float64 sums over the stored output); both tiles with the variant agree, ragged M
+    and N included, nothing is written outside the view (ldz = N + 8), and sampled rows match the oracle."""
+    import torch
+    x = data.normal((M, K), 171)
+    w = data.normal((K, N), 172, std=1 / np.sqrt(K))
+    b = data.normal((1, N), 173, std=0.3)
+    r = data.normal((M, N), 174)
+    z0 = data.normal((M, N), 175)
+    g = (1.0 + data.normal((1, K), 176, std=0.2)).astype(np.float16)
+    be = data.normal((1, K), 177, std=0.2)
+    X, W, Bb, R, G, BE = (to_dev(v) for v in (x, w, b, r, g, be))
+    f32 = dict(dtype=torch.float32, device="cuda")
+    WP, C, D, S = torch.empty((K, N), dtype=torch.float16, device="cuda"), torch.empty(N, **f32), torch.empty(N, **f32), torch.empty((M, 2), **f32)
+    lib.sh_ln_fold(A(WP), A(C), A(D), A(W), A(G), A(BE), A(Bb), K, N, N, N)
+    lib.sh_row_stats(A(S), A(X), M, K, K, 1e-6)
+    assert shops.last_error()[0] == 0, shops.last_error()
+    P = N // 32
+    GELU, FP32 = shops.SH_ACT_GELU, shops.SH_BIAS_FP32
+    cases = {
+        "plain": (W, lambda st: shops.epi(splits=2), None),
+        "gelu": (W, lambda st: shops.epi(bias=A(Bb), act=GELU, splits=2), None),
+        "res_acc": (W, lambda st: shops.epi(bias=A(Bb), residual=A(R), ldr=N, splits=2), shops.cfg(accumulate=1)),
+        "lnfold": (WP, lambda st: shops.epi(bias=A(D), bias_fmt=FP32, act=GELU, ln_stats=A(S), ln_c=A(C), splits=2), None),
+    }
+    if N % 32 == 0:
+        cases["stats"] = (W, lambda st: shops.epi(bias=A(Bb), residual=A(R), ldr=N, stats_out=A(st), splits=2), None)
+
+    def run(name, kg, cfg_index):
+        Wm, mk, gcfg = cases[name]
+        monkeypatch.setenv("SH_GEMM_KG", str(kg))
+        if cfg_index is None:
+            monkeypatch.delenv("SH_GEMM_CFG", raising=False)
+        else:
+            monkeypatch.setenv("SH_GEMM_CFG", str(cfg_index))
+        Z = torch.full((M, N + 8), 7.0, dtype=torch.float16, device="cuda")
+        if gcfg is not None:
+            Z[:, :N] = to_dev(z0)
+        St = torch.zeros((M, max(P, 1), 2), **f32)
+        rc = lib.sh_gemm_ex(A(X), A(Wm), A(Z), M, N, K, K, N, N + 8, gcfg, mk(St))
+        assert rc == 0, (name, kg, cfg_index, shops.last_error())
+        assert (to_np(Z)[:, N:] == 7.0).all(), (name, kg, cfg_index)
+        return codes(Z)[:, :N], to_np(St)
+
+    rows = np.array([0, 1, 31, 127, 128, M // 2, M - 1])
+    for name in cases:
+        outs = []
+        for cfg_index in (None,) + KG2_CFGS:
+            want, _ = run(name, 0, cfg_index)
+            got, st = run(name, 1, cfg_index)
+            assert np.array_equal(got, want), (name, cfg_index, int((got != want).sum()))
+            outs.append(got)
+            if name == "stats":
+                zf = got.view(np.float16).astype(np.float64).reshape(M, P, 32)
+                s = zf.sum(2)
+                m2 = ((zf - s[..., None] / 32) ** 2).sum(2)
+                mag, u = np.abs(zf).sum(2), 2.0 ** -24
+                assert np.all(np.abs(st[..., 0] - s) <= 32 * u * mag)
+                assert np.all(np.abs(st[..., 1] - m2) <= 64 * u * (m2 + mag ** 2 / 32))
+        assert np.array_equal(outs[1], outs[2]), name
+        if name == "plain":
+            bad, err, _ = refs.close(want[rows].view(np.float16), refs.gemm(x[rows], w))
+            assert bad == 0, err
+
+
 def test_mesh_known_answer_and_lcg(lib, gpu):
     import torch
     M = N = K = 1024
