@@ -20,6 +20,7 @@
 #include "sh_common.h"
 #include <hip/hip_ext.h>
 #include <chrono>
+#include <type_traits>
 
 namespace {
 
@@ -692,7 +693,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
     constexpr int KCH = KB * DC;                     // 16-byte chunks per K (or V) block
     constexpr int KR = KCH / 256;                    // DMA rounds per thread per block, per operand
     constexpr uint32_t STAGE = 2u * KCH * 16u;       // K block then V block
-    static_assert(KCH % 256 == 0 && NST >= 2, "attention tiling");
+    static_assert(KCH % 256 == 0 && NST == 2, "attention tiling (the key-block loop is unrolled by the two stages)");
     __shared__ uint4 smem[NST * 2 * KCH];
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = lane >> 5, r32 = lane & 31;
@@ -715,26 +716,35 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
     attn_stamp(stamp, last, 1);
     attn_stamp(stamp, last, 2);
 
-    const uint16_t *kcol[KR];
-    const uint16_t *vcol[KR];
-    uint32_t kkey[KR];
+    // DMA sources: the block's first row (wave-uniform, scalar registers) plus each lane's 32-bit byte offset of its
+    // row and swizzled chunk (the host launches this kernel only when 64 rows of either stride span < 2 GiB)
+    uint32_t koff[KR], voff[KR];
 #pragma unroll
     for (int r = 0; r < KR; ++r) {
         const uint32_t p = r * 256 + wave * 64 + lane, key = p / DC, pc = p % DC;
-        kkey[r] = key;
-        kcol[r] = Kp + 8 * (pc ^ kswz<DH>(key));
-        vcol[r] = Vp + 8 * (pc ^ vfw<DH>(key));
+        koff[r] = key * (uint32_t)a.ldk * 2 + 16 * (pc ^ kswz<DH>(key));
+        voff[r] = key * (uint32_t)a.ldv * 2 + 16 * (pc ^ vfw<DH>(key));
     }
     const uint32_t lds0 = sh_lds_addr(smem);
     const uint32_t wave_off = (uint32_t)__builtin_amdgcn_readfirstlane(wave * 64 * 16);
     auto issue = [&](uint32_t kb, int stage) {
         const uint32_t st = lds0 + (uint32_t)stage * STAGE;
         const uint32_t k0 = kb * KB;
+        const char *kbase = (const char *)(Kp + (uint64_t)k0 * a.ldk), *vbase = (const char *)(Vp + (uint64_t)k0 * a.ldv);
+        if (k0 + KB <= S) {
 #pragma unroll
-        for (int r = 0; r < KR; ++r) {
-            const uint64_t row = min(k0 + kkey[r], S - 1);                      // rows past S read row S-1
-            sh_lds_dma16(kcol[r] + row * a.ldk, st + r * 4096 + wave_off);
-            sh_lds_dma16(vcol[r] + row * a.ldv, st + KCH * 16 + r * 4096 + wave_off);
+            for (int r = 0; r < KR; ++r) {
+                sh_lds_dma16_s(kbase, koff[r], st + r * 4096 + wave_off);
+                sh_lds_dma16_s(vbase, voff[r], st + KCH * 16 + r * 4096 + wave_off);
+            }
+        } else {                                     // the ragged last block: rows past S read row S - 1
+            const uint32_t lim = S - 1 - k0;
+#pragma unroll
+            for (int r = 0; r < KR; ++r) {
+                const uint32_t key = (uint32_t)(r * 256 + wave * 64 + lane) / DC, over = key > lim ? key - lim : 0u;
+                sh_lds_dma16_s(kbase, koff[r] - over * (uint32_t)a.ldk * 2, st + r * 4096 + wave_off);
+                sh_lds_dma16_s(vbase, voff[r] - over * (uint32_t)a.ldv * 2, st + KCH * 16 + r * 4096 + wave_off);
+            }
         }
     };
 #pragma unroll
@@ -766,21 +776,24 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
         const uint32_t key = 32 * (i & 1) + r32;
         return __builtin_bit_cast(sh_h8, sk[key * DC + ((2 * (i >> 1) + g) ^ kswz<DH>(key))]);
     };
-    auto scores = [&](int st, sh_f16v (&sacc)[2], bool bias) {
-        const uint4 *sk = smem + st * 2 * KCH;
+    // (stage and bias step are compile-time: fragment addresses fold the stage into the read's immediate offset,
+    // and without the bias step the first MFMA of each tile starts from a zero accumulator operand)
+    auto scores = [&](auto stc, sh_f16v (&sacc)[2], auto bias_c) {
+        constexpr bool bias = decltype(bias_c)::value;
+        const uint4 *sk = smem + decltype(stc)::value * 2 * KCH;
         constexpr int NI = 2 * NS;
         sh_h8 kf[3];
         kf[0] = kfrag(sk, 0);
         kf[1] = kfrag(sk, 1);
+        if constexpr (bias) {
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            sacc[tt] = sh_f16v{};
-            if (bias) sacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kbias, qbias, sacc[tt], 0, 0, 0);
+            for (int tt = 0; tt < 2; ++tt) sacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kbias, qbias, sh_f16v{}, 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             if (i + 2 < NI) kf[(i + 2) % 3] = kfrag(sk, i + 2);
-            sacc[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[i % 3], qf[i >> 1], sacc[i & 1], 0, 0, 0);
+            if (!bias && i < 2) sacc[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[i % 3], qf[i >> 1], sh_f16v{}, 0, 0, 0);
+            else sacc[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[i % 3], qf[i >> 1], sacc[i & 1], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -792,11 +805,15 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
     float mrun = 0.f;                                // reference m of this lane's query (c s units)
     bool biased = false;                             // some lane's m left 0 (wave-uniform): the bias step is needed
     const sh_h2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
-    for (uint32_t kb = 0; kb < nkb; ++kb) {
+    using Stage0 = std::integral_constant<int, 0>;
+    using Stage1 = std::integral_constant<int, 1>;
+    using Biased = std::true_type;
+    // key block kb, held in ring stage kb % 2 (= the compile-time stage of stc)
+    auto step = [&](uint32_t kb, auto stc) {
+        constexpr int st = decltype(stc)::value;
         sh_wait_vmcnt<(NST - 2) * 2 * KR>();
         __syncthreads();
-        issue(min(kb + NST - 1, nkb - 1), (int)((kb + NST - 1) % NST));
-        const int st = (int)(kb % NST);
+        issue(min(kb + NST - 1, nkb - 1), (st + NST - 1) % NST);
         sh_f16v sacc[2];
         auto mask_tail = [&]() {
             if (ragged && kb == nkb - 1) {
@@ -807,7 +824,8 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
                         if (kb * KB + 32 * tt + 8 * (r >> 2) + 4 * g + (r & 3) >= S) sacc[tt][r] = -INFINITY;
             }
         };
-        scores(st, sacc, biased);                    // (while every m is 0 the bias step would add zeros)
+        if (biased) scores(stc, sacc, Biased{});
+        else scores(stc, sacc, std::false_type{});   // (while every m is 0 the bias step would add zeros)
         mask_tail();
         // the block's maximum for this lane's query (lanes r32 and r32 + 32 hold complementary keys)
         float bm = -INFINITY;
@@ -828,7 +846,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
             mrun += shift;
             set_bias(mrun);
             biased = true;
-            scores(st, sacc, true);
+            scores(stc, sacc, Biased{});
             mask_tail();
         }
         sh_h8 pf[4];                                 // numerators p = 2^acc, fp16, as the P.V MFMA operands
@@ -867,6 +885,10 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
             oacc[j % DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vq[j & 1], pf[j / DT], oacc[j % DT], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
+    };
+    for (uint32_t kb = 0; kb < nkb; kb += 2) {
+        step(kb, Stage0{});
+        if (kb + 1 < nkb) step(kb + 1, Stage1{});
     }
     sh_wait_vmcnt<0>();      // clamped tail loads land before the LDS is reused below
     __syncthreads();
@@ -1018,7 +1040,8 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
         static bool attr_m = false;
         if (!attr_m) { (void)hipFuncSetAttribute((const void *)k_attn_rows, hipFuncAttributeMaxDynamicSharedMemorySize, 16384 * 4); attr_m = true; }
         go(k_attn_rows, dim3(S, H, B), S * sizeof(float));
-    } else if ((dh == 64 || dh == 128) && vec && impl == 0 && fold) {
+    } else if ((dh == 64 || dh == 128) && vec && impl == 0 && fold && (uint64_t)KB * (ldk > ldv ? ldk : ldv) * 2 < (1ull << 31)) {
+        // (k_flash3 addresses a key block's rows as a scalar base plus 32-bit lane offsets)
         if (dh == 64) go2(k_flash3<64, 2>, grid, 0);
         else go2(k_flash3<128, 2>, grid, 0);
     } else if ((dh == 64 || dh == 128) && vec && (impl == 0 || impl == 2)) {

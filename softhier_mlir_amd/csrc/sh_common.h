@@ -85,6 +85,11 @@ __device__ __forceinline__ float sh_wave_max(float v) {
 __device__ __forceinline__ void sh_lds_dma16(const void *src, uint32_t lds_wave_base) {
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_wave_base), "v"(src) : "memory", "m0");
 }
+// The same with the address split into a wave-uniform base (a scalar register pair) and each lane's 32-bit byte
+// offset from it: no 64-bit per-lane address arithmetic.
+__device__ __forceinline__ void sh_lds_dma16_s(const void *base, uint32_t off, uint32_t lds_wave_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_wave_base), "v"(off), "s"(base) : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // s_waitcnt vmcnt(N) with expcnt / lgkmcnt left unconstrained (gfx9 encoding: vmcnt[3:0], [15:14]).
