@@ -805,6 +805,17 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
     float mrun = 0.f;                                // reference m of this lane's query (c s units)
     bool biased = false;                             // some lane's m left 0 (wave-uniform): the bias step is needed
     const sh_h2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
+    // LDS byte address in stage 0 of each lane's V^T fragment j (rows k0 of its lower half; the upper half's rows
+    // k0 + 8 have the same swizzle, vfw reading only the two low bits of k): the loop adds the stage as an immediate
+    constexpr int NJ = 4 * DT;
+    uint32_t vaddr[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int sp = j / DT, dt = j % DT;
+        const uint32_t d = 32 * dt + 16 * (q4 & 1) + 4 * (iq & 3);
+        const uint32_t k0 = 16 * sp + 4 * g + (iq >> 2);
+        vaddr[j] = lds0 + KCH * 16 + k0 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k0)) + 2 * (d & 7);
+    }
     using Stage0 = std::integral_constant<int, 0>;
     using Stage1 = std::integral_constant<int, 1>;
     using Biased = std::true_type;
@@ -833,7 +844,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sacc[tt][r]);
-        bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+        bm = sh_max_xor32(bm);
         // m starts at 0; the first block moves it when its maximum is more than kTau away on either side, a later one
         // when its maximum exceeds m by more than kTau (every block holds a valid key: bm is finite)
         const bool move = kb == 0 ? fabsf(bm) > kTau : bm > kTau;
@@ -858,17 +869,13 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
             attn_stamp(stamp, last, 3);
             attn_stamp(stamp, last, 4);
         }
-        const uint32_t vbase = lds0 + (uint32_t)st * STAGE + KCH * 16;
         // V^T fragment j: substep j / DT, d tile j % DT (consecutive MFMAs alternate accumulators); read one ahead
         auto vfrag = [&](int j) -> sh_h8 {
-            const int sp = j / DT, dt = j % DT;
-            const uint32_t d = 32 * dt + 16 * (q4 & 1) + 4 * (iq & 3);
-            const uint32_t k0 = 16 * sp + 4 * g + (iq >> 2), k1 = k0 + 8;
-            const sh_s4 lo = sh_ds_read_tr(vbase + k0 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k0)) + 2 * (d & 7));
-            const sh_s4 hi = sh_ds_read_tr(vbase + k1 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k1)) + 2 * (d & 7));
+            const uint32_t at = vaddr[j] + (uint32_t)st * STAGE;
+            const sh_s4 lo = sh_ds_read_tr(at);
+            const sh_s4 hi = sh_ds_read_tr(at + 8 * (DH * 2));
             return __builtin_bit_cast(sh_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         };
-        constexpr int NJ = 4 * DT;
         sh_h8 vq[2];
         vq[0] = vfrag(0);
 #pragma unroll

@@ -92,6 +92,13 @@ __device__ __forceinline__ void sh_lds_dma16_s(const void *base, uint32_t off, u
 }
 #pragma clang diagnostic pop
 
+// The larger of v in lanes l and l ^ 32, in every lane: one v_permlane32_swap of v with itself puts each lane's
+// partner value in one of the two results and its own in the other (no LDS round trip).
+__device__ __forceinline__ float sh_max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // s_waitcnt vmcnt(N) with expcnt / lgkmcnt left unconstrained (gfx9 encoding: vmcnt[3:0], [15:14]).
 template <int N>
 __device__ __forceinline__ void sh_wait_vmcnt() {
