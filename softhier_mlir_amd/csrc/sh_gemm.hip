@@ -1414,11 +1414,12 @@ __global__ __launch_bounds__(256 * KG, MINW) void k_gemm5(GemmArgs a) {
     // (the largest tiles keep their registers for the accumulators: no early loads there)
     // (unsplit tiles are stored through each wavefront's DMA slots, and the residual is added there: no early load)
     // (the staging may use every stage but the last slice's: NST - 1 stages of LOADS 1 KB slots per wavefront)
+    // (a tile that holds a CU alone, MINW = 1, has the registers to load the residual early even when staged)
     constexpr bool STAGED = !SPLIT && 4 * TN <= 64 * C::LOADS * (NST - 1);
-    constexpr bool PRE_B = PRE && FM * FN <= 12, PRE_RES = PRE && FM * FN <= 6 && !STAGED;
+    constexpr bool PRE_B = PRE && FM * FN <= 12, PRE_RES = PRE && FM * FN <= 6 && (!STAGED || (MINW == 1 && KG == 1));
     uint4 bq[PRE_B ? FN : 1][2], rq[PRE_RES ? FM : 1][PRE_RES ? FN : 1][2];
     // (a GEMM that also writes row partials adds the residual in the chain, before them)
-    const bool stage_res = STAGED && !a.stats_out;
+    const bool stage_res = STAGED && !PRE_RES && !a.stats_out;
     const bool pre_ok = PRE_B && grp == 0 && !a.accumulate && !(a.bias && a.bias_fp32) && (PRE_RES || stage_res || !a.res);
     auto prefetch = [&]() {
 #pragma unroll
@@ -1989,6 +1990,7 @@ KCfg g_cfgs[] = {
     SH_KCFG5K(128, 192, 32, 4, 2, 0.36f),       // two workgroups per CU with a deeper ring of 32-k slices
     SH_KCFG5(128, 128, 64, 2, 2, 0.30f),
     SH_KCFG5(128, 128, 32, 4, 2, 0.30f),
+    SH_KCFG5(128, 192, 32, 4, 1, 0.36f),        // one workgroup per CU: residual and bias loaded during the last slice
 };
 #undef SH_KCFG
 #undef SH_KCFG2
@@ -2124,14 +2126,17 @@ void set_grid(GemmArgs &a, const KCfg &c) {
 
 // One-time timing of the tile configurations for a large unsplit problem. Every unsplit configuration
 // accumulates K in the same order with the same MFMA, so they store bit-identical results and the choice only
-// changes speed. Trial runs write a scratch output (no residual, no accumulate; bias and activation as in the
-// call); the winner is cached per shape. Skipped under stream capture, for small problems, or SH_GEMM_TUNE=0.
-typedef std::tuple<uint32_t, uint32_t, uint32_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t> TuneKey;   // + wt
+// changes speed. Trial runs write a scratch output (no accumulate; bias, activation, residual, LayerNorm fold and
+// row partials as in the call: the residual and fold rows are only read, the row partials are written again by
+// the call itself); the winner is cached per shape and epilogue. Skipped under stream capture, for small
+// problems, or SH_GEMM_TUNE=0.
+typedef std::tuple<uint32_t, uint32_t, uint32_t, uint64_t, uint64_t, uint32_t, uint32_t, uint32_t> TuneKey;   // + flags
 std::map<TuneKey, int> g_tuned;
 
 // SH_GEMM_TUNE_FILE=path: choices are read from that file at the first tuning decision and every new choice is
-// appended to it ("M N K ldx ldw bias act wt cfg" per line), so a later process (a counter run, under which the
-// timing itself would be distorted) launches exactly the tiles an earlier timed run chose.
+// appended to it ("M N K ldx ldw bias act flags cfg" per line; flags: 1 W^T, 2 LayerNorm fold or row partials,
+// 4 residual), so a later process (a counter run, under which the timing itself would be distorted) launches
+// exactly the tiles an earlier timed run chose.
 void tune_file_load() {
     static bool done = false;
     if (done) return;
@@ -2167,7 +2172,7 @@ int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st, bool wt) {
     if (thr < 6e-6) return heur;                     // the throughput estimate: small problems keep the model's tile
     tune_file_load();
     const TuneKey key{call.M, call.N, call.K, call.ldx, call.ldw, call.bias ? 1u + call.bias_fp32 : 0u, call.act,
-                      (wt ? 1u : 0u) | (reg_only ? 2u : 0u)};
+                      (wt ? 1u : 0u) | (reg_only ? 2u : 0u) | (call.res ? 4u : 0u)};
     auto it = g_tuned.find(key);
     if (it != g_tuned.end()) return it->second;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -2178,7 +2183,7 @@ int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st, bool wt) {
     int best = heur;
     if (hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess) {
         GemmArgs a = call;
-        a.z = scratch; a.ldz = call.N; a.res = nullptr; a.ldr = 0; a.accumulate = 0; a.splits = 1; a.part = nullptr;
+        a.z = scratch; a.ldz = call.N; a.accumulate = 0; a.splits = 1; a.part = nullptr;
         // three interleaved rounds, the minimum per configuration: one slow sample does not decide the choice
         float mins[kNumCfg];
         for (float &m : mins) m = 1e30f;
@@ -2279,6 +2284,7 @@ int launch(const GemmReq &r, const char *name) {
         t.x = (const uint16_t *)r.x; t.w = (const uint16_t *)r.w; t.bias = (const void *)bias;
         t.ldx = r.ldx; t.ldw = r.ldw; t.M = r.M; t.N = r.N; t.K = r.K; t.kps = sh_cdiv(r.K, BK) * BK; t.splits = 1;
         t.bias_fp32 = (e && e->bias_fmt == SH_BIAS_FP32) ? 1 : 0; t.act = e ? e->act : 0;
+        t.res = (const uint16_t *)res; t.ldr = ldr;
         set_epi(t);
         p.cfg = tuned_cfg(t, p.cfg, sh_stream(), r.wt);
     }

@@ -18,7 +18,7 @@ from softhier_mlir_amd import data, shops
 
 pytestmark = pytest.mark.gpu
 A = shops.addr
-REG_CFGS = list(range(25, 29)) + list(range(33, 41)) + [55, 56, 57]   # W layout tiles with the fold in registers
+REG_CFGS = list(range(25, 29)) + list(range(33, 41)) + [55, 56, 57, 58]   # W layout tiles with the fold in registers
 EPS = 1e-6
 
 
