@@ -52,6 +52,7 @@ struct GemmArgs {
     uint32_t tiles_m, tiles_n, splits;
     uint32_t accumulate, bias_fp32, act;
     uint32_t xcd_groups;         // > 1: XCD-aware block remap with this many XCDs (requires divisibility)
+    uint32_t group_m;            // > 1: tiles ordered in bands of this many tile rows, column by column within a band
     const float *ln_stats;       // LayerNorm fold (or null): (mu, r) per row, fp32 [M][2], or ln_parts partials ...
     const float *ln_c;           // ... and c per column (fp32 [N]); the fp32 bias row is then d
     uint32_t ln_parts;           // > 0: ln_stats holds ln_parts (sum, M2) pairs of 32 columns per row (row_partials)
@@ -134,16 +135,25 @@ __device__ __forceinline__ float ln_apply(const GemmArgs &a, float2 st, float p,
 }
 
 // Logical tile of block b -> (split, tile row, tile column). Dispatch deals workgroups round-robin over the
-// XCDs, so block b becomes logical index (b % X) (T / X) + b / X: each XCD walks a contiguous run of the
-// row-major tile order and the operand panels it shares stay in that XCD's L2.
+// XCDs, so block b becomes logical index (b % X) (T / X) + b / X: each XCD walks a contiguous run of the tile
+// order and the operand panels it shares stay in that XCD's L2. The order is row-major, or (group_m > 1) in bands
+// of group_m tile rows taken column by column, so the tiles an XCD runs at once span group_m row panels of X and
+// a few column panels of W instead of every column panel (a bijection: a band's last, short one included).
 __device__ __forceinline__ void tile_of(const GemmArgs &a, uint32_t b, uint32_t nblk, uint32_t &tm, uint32_t &tn, uint32_t &split) {
     uint32_t L = b;
     if (a.xcd_groups > 1) L = (b % a.xcd_groups) * (nblk / a.xcd_groups) + b / a.xcd_groups;
     const uint32_t per = a.tiles_m * a.tiles_n;
     split = L / per;
     const uint32_t l = L - split * per;
-    tm = l / a.tiles_n;
-    tn = l % a.tiles_n;
+    if (a.group_m > 1) {
+        const uint32_t band = l / (a.group_m * a.tiles_n), first = band * a.group_m;
+        const uint32_t rows = min(a.group_m, a.tiles_m - first), w = l - band * a.group_m * a.tiles_n;
+        tm = first + w % rows;
+        tn = w / rows;
+    } else {
+        tm = l / a.tiles_n;
+        tn = l % a.tiles_n;
+    }
 }
 
 // Zero-filled stand-in read by the epilogue for operands a call does not have (never written).
@@ -2117,6 +2127,10 @@ uint32_t grid_of(GemmArgs &a) {
     const uint32_t nblk = a.tiles_m * a.tiles_n * a.splits;
     const int X = sh_num_xcds();
     a.xcd_groups = (X > 1 && nblk % (uint32_t)X == 0) ? (uint32_t)X : 1;
+    // bands of 8 tile rows: an XCD's 64 first tiles of a 128x192 tiling span 8 row panels and 8 column panels
+    // (3.9 MB of operands at K = 768, inside its 4 MB L2) instead of 4 and every one (SH_GEMM_GROUP=1: row-major)
+    static const int gm = env_int("SH_GEMM_GROUP", 8);
+    a.group_m = gm > 1 ? (uint32_t)gm : 1;
     return nblk;
 }
 
