@@ -288,6 +288,45 @@ def test_splitk_matches_and_is_deterministic(lib, gpu):
     assert bad == 0, err
 
 
+_ORDER_CHILD = r"""
+import os, sys
+import numpy as np, torch
+from softhier_mlir_amd import shops
+lib = shops.load(); lib.sh_init()
+M, N, K = 1000, 1128, 768                     # 8 x 6 tiles of 128 x 192 (the last row and column partial)
+g = torch.Generator(device="cuda").manual_seed(5)
+x = torch.randn((M, K), dtype=torch.float16, device="cuda", generator=g)
+w = (torch.randn((K, N), dtype=torch.float16, device="cuda", generator=g) * 0.04).contiguous()
+b = torch.randn((1, N), dtype=torch.float16, device="cuda", generator=g)
+r = torch.randn((M, N), dtype=torch.float16, device="cuda", generator=g)
+z = torch.zeros((M, N), dtype=torch.float16, device="cuda")
+A = shops.addr
+e = shops.epi(bias=A(b), residual=A(r), ldr=N)
+assert lib.sh_gemm_ex(A(x), A(w), A(z), M, N, K, K, N, N, None, e) == 0, shops.last_error()
+torch.cuda.synchronize()
+np.save(sys.argv[1], z.cpu().numpy().view(np.uint16))
+"""
+
+
+def test_tile_order_bands_store_identical_bits(lib, gpu, tmp_path):
+    """The tile order (row-major, or bands of SH_GEMM_GROUP tile rows taken column by column; read once per process,
+    so each setting runs in its own child process, one after another) only moves tiles between workgroups: bands of
+    1 (row-major), 3 (a short last band on this 8-row grid) and 8 (the default) store the same bits, with a
+    128x192 tile, bias and residual."""
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    outs = {}
+    for band in (1, 3, 8):
+        env = dict(os.environ, SH_GEMM_GROUP=str(band), SH_GEMM_CFG="55", PYTHONPATH=root)
+        f = tmp_path / f"z{band}.npy"
+        rc = subprocess.run([sys.executable, "-c", _ORDER_CHILD, str(f)], env=env, cwd=root, timeout=110,
+                            capture_output=True, text=True)
+        assert rc.returncode == 0, (band, rc.stderr[-2000:])
+        outs[band] = np.load(f)
+    assert np.array_equal(outs[1], outs[3]) and np.array_equal(outs[1], outs[8])
+
+
 KG2_CFGS = (38, 55)      # tiles with the in-workgroup split-K variant (k_gemm5 KG = 2)
 
 
