@@ -43,14 +43,15 @@ __device__ __forceinline__ uint32_t slot_col(int lane, int u, int i) {
 // Makes q's value available at this point (an empty asm that reads and writes it), so its load is not moved later.
 __device__ __forceinline__ void pin4(uint4 &q) { __asm__ volatile("" : "+v"(q.x), "+v"(q.y), "+v"(q.z), "+v"(q.w)); }
 
-// 16-byte store; nt: nontemporal (streaming), used when the output is larger than the Infinity Cache, where no
-// consumer could find it cached anyway and plain stores only evict what it could use.
+// 16-byte store; nt: nontemporal (streaming), used when the output is at least half the 256 MB Infinity Cache: with
+// its input it does not stay there, so no consumer could find it cached and plain stores only evict what it could
+// use (at 16x the encoder's rows, ~200 MB outputs: LayerNorm 5.7 against 5.5 TB/s, add_bias 6.0 against 5.6).
 typedef uint32_t sh_u4v __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void st16(void *p, uint4 v, bool nt) {
     if (nt) __builtin_nontemporal_store((sh_u4v){v.x, v.y, v.z, v.w}, (sh_u4v *)p);
     else *(uint4 *)p = v;
 }
-constexpr uint64_t kNtBytes = uint64_t(256) << 20;     // MI355X Infinity Cache
+constexpr uint64_t kNtBytes = uint64_t(128) << 20;     // half the MI355X Infinity Cache
 
 template <int NCH>
 __device__ __forceinline__ void load_raw(const uint16_t *__restrict__ p, uint32_t cols, int lane, uint4 (&raw)[NCH]) {
@@ -631,7 +632,7 @@ void launch_elementwise(int op, uint64_t y, uint64_t a, uint64_t b, uint32_t row
     uint16_t *Y = (uint16_t *)y; const uint16_t *A = (const uint16_t *)a, *B = (const uint16_t *)b;
     const uint32_t nt = (uint64_t)rows * cols * 2 >= kNtBytes;
     // one item per thread (the most workgroups in flight) for GELU, whose VALU work wants the most wavefronts, and
-    // for outputs above the Infinity Cache; four per thread for the other ops below it (fewer, fuller launches).
+    // for streamed (nontemporal) outputs; four per thread for the other ops below it (fewer, fuller launches).
     // Measured on [131072 x 3072] GELU: 6.2 against 5.7 TB/s; at the configured sizes add / add_bias prefer four.
     const bool one = op == OP_GELU || nt;
     const dim3 grid(sh_cdiv(items, 256u * (one ? 1u : 4u))), block(256);
@@ -835,8 +836,8 @@ void sh_dma_copy(uint64_t dst, uint64_t src, uint32_t bytes) {
     hipStream_t st = sh_stream();
     const uint32_t cap = (uint32_t)(sh_num_cus() > 0 ? sh_num_cus() : 256) * 8;
     if ((dst | src | bytes) % 16 == 0) {
-        // above the Infinity Cache one chunk per thread streams best (a 1 GiB copy: 6.2 TB/s against 5.4 with
-        // eight); below it eight per thread
+        // for streamed sizes one chunk per thread streams best (a 1 GiB copy: 6.2 TB/s against 5.4 with eight);
+        // below them eight per thread
         const uint64_t n16 = bytes / 16;
         const bool big = bytes >= kNtBytes;
         const uint32_t per_block = big ? 256u : 256u * 8u;

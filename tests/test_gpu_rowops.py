@@ -207,9 +207,9 @@ def test_softmax_short_rows(lib, gpu, cols, scale):
 
 
 @pytest.mark.parametrize("nbytes,so,do", [(16 << 20, 0, 0), (4096 + 48, 16, 32), (1000003, 3, 5), (1, 0, 7),
-                                         ((256 << 20) + 48, 16, 32)])
+                                         ((160 << 20) + 48, 16, 32), ((256 << 20) + 48, 16, 32)])
 def test_dma_copy_moves_every_byte(lib, gpu, nbytes, so, do):
-    """sh_dma_copy (sh_ops.h:218): a 1-D copy of exactly `bytes`, aligned (streaming 16-byte path; above 256 MiB one
+    """sh_dma_copy (sh_ops.h:218): a 1-D copy of exactly `bytes`, aligned (streaming 16-byte path; from 128 MiB one
     chunk per thread with nontemporal stores) or not (byte path), leaving the bytes around the destination range
     untouched."""
     import torch
@@ -223,7 +223,7 @@ def test_dma_copy_moves_every_byte(lib, gpu, nbytes, so, do):
 
 
 def test_elementwise_above_the_infinity_cache(lib, gpu):
-    """Outputs of 256 MiB and more take the one-item-per-thread launch with nontemporal stores: on a [131072 x 1024]
+    """Outputs of 128 MiB and more take the one-item-per-thread launch with nontemporal stores: on a [131072 x 1024]
     tensor tiled from one 64-row block, every block of the GELU, add_bias and scale outputs equals the library's
     result on the block alone (bit for bit: the same element-wise function), and add of integers is exact."""
     import torch
