@@ -52,6 +52,19 @@ __device__ __forceinline__ void st16(void *p, uint4 v, bool nt) {
     else *(uint4 *)p = v;
 }
 constexpr uint64_t kNtBytes = uint64_t(128) << 20;     // half the MI355X Infinity Cache
+// 16-byte load, nontemporal under NT: the kernels that stream a nontemporal output read their input once too, so
+// its lines need not stay cached either (at 16x the encoder's rows: softmax, add and the copy +2-4 %, GELU, add_bias
+// and transpose +2 %). LayerNorm keeps plain loads: its row groups walk rows with a stride, and nontemporal loads
+// measured 8 % slower there.
+template <bool NT>
+__device__ __forceinline__ uint4 ld16(const void *p) {
+    if constexpr (NT) {
+        const sh_u4v q = __builtin_nontemporal_load((const sh_u4v *)p);
+        return make_uint4(q.x, q.y, q.z, q.w);
+    } else {
+        return *(const uint4 *)p;
+    }
+}
 
 template <int NCH>
 __device__ __forceinline__ void load_raw(const uint16_t *__restrict__ p, uint32_t cols, int lane, uint4 (&raw)[NCH]) {
@@ -164,9 +177,9 @@ __global__ __launch_bounds__(256) void k_layernorm(uint16_t *y, const uint16_t *
 // chunks per lane, each group walking rows row0, row0 + groups, ...: the next row's loads are issued before the
 // current row's statistics, so every group keeps two rows in flight; gamma and beta are loaded once per group.
 // Same two-pass statistics as k_layernorm (mean, then the mean of squared deviations, fp32).
-template <int LPR, int NCH>
+template <int LPR, int NCH, bool NT>
 __global__ __launch_bounds__(256) void k_layernorm_p(uint16_t *y, const uint16_t *x, const uint16_t *gamma, const uint16_t *beta,
-                                                     uint32_t rows, uint32_t cols, uint64_t ldy, uint64_t ldx, float eps, uint32_t nt) {
+                                                     uint32_t rows, uint32_t cols, uint64_t ldy, uint64_t ldx, float eps) {
     constexpr int GPW = 64 / LPR;                         // row groups per wavefront
     const int lane = threadIdx.x & 63, gl = lane % LPR;
     const uint32_t group = (blockIdx.x * 4 + (threadIdx.x >> 6)) * GPW + lane / LPR;
@@ -186,13 +199,13 @@ __global__ __launch_bounds__(256) void k_layernorm_p(uint16_t *y, const uint16_t
     uint4 cur[NCH];
     const uint32_t r0 = row < rows ? row : 0u;
 #pragma unroll
-    for (int u = 0; u < NCH; ++u) cur[u] = *(const uint4 *)(x + r0 * ldx + (col(u) < cols ? col(u) : 0u));
+    for (int u = 0; u < NCH; ++u) cur[u] = ld16<false>(x + r0 * ldx + (col(u) < cols ? col(u) : 0u));
     const float inv_n = 1.f / (float)cols;
     for (; row < rows; row += ngroups) {                  // the trip count differs between the groups of a wave
         const uint32_t nrow = row + ngroups < rows ? row + ngroups : row;
         uint4 nxt[NCH];
 #pragma unroll
-        for (int u = 0; u < NCH; ++u) nxt[u] = *(const uint4 *)(x + nrow * ldx + (col(u) < cols ? col(u) : 0u));
+        for (int u = 0; u < NCH; ++u) nxt[u] = ld16<false>(x + nrow * ldx + (col(u) < cols ? col(u) : 0u));
         float v[NCH][8];
         float s = 0.f;
 #pragma unroll
@@ -221,7 +234,7 @@ __global__ __launch_bounds__(256) void k_layernorm_p(uint16_t *y, const uint16_t
             float o8[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) o8[i] = (v[u][i] - mean) * rs * g[u][i] + b[u][i];
-            st16(y + row * ldy + col(u), pack8(o8), nt);
+            st16(y + row * ldy + col(u), pack8(o8), NT);
         }
 #pragma unroll
         for (int u = 0; u < NCH; ++u) cur[u] = nxt[u];
@@ -296,19 +309,19 @@ __global__ __launch_bounds__(256) void k_ln_fold(uint16_t *wp, float *c, float *
 
 // Streaming 1-D copy of n16 16-byte chunks: U chunks per thread, all loaded before any is stored, one pass per
 // thread (no grid-stride loop: a thread's next loads would queue behind its stores in the memory counter).
-template <int U>
-__global__ __launch_bounds__(256) void k_copy16(uint4 *__restrict__ dst, const uint4 *__restrict__ src, uint64_t n16, uint32_t nt) {
+template <int U, bool NT>
+__global__ __launch_bounds__(256) void k_copy16(uint4 *__restrict__ dst, const uint4 *__restrict__ src, uint64_t n16) {
     const uint64_t base = (uint64_t)blockIdx.x * 256u * U + threadIdx.x;
     uint4 v[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const uint64_t i = base + (uint64_t)u * 256u;
-        v[u] = src[i < n16 ? i : 0];
+        v[u] = ld16<NT>(src + (i < n16 ? i : 0));
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const uint64_t i = base + (uint64_t)u * 256u;
-        if (i < n16) st16(dst + i, v[u], nt);
+        if (i < n16) st16(dst + i, v[u], NT);
     }
 }
 
@@ -366,9 +379,8 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-template <int LPR, int RIT>
-__global__ __launch_bounds__(256) void k_softmax_narrow(uint16_t *y, const uint16_t *x, uint32_t rows, uint32_t cols, uint64_t ld, float c,
-                                                        uint32_t nt) {
+template <int LPR, int RIT, bool NT>
+__global__ __launch_bounds__(256) void k_softmax_narrow(uint16_t *y, const uint16_t *x, uint32_t rows, uint32_t cols, uint64_t ld, float c) {
     constexpr int RPW = 64 / LPR;                     // rows per wavefront per group
     const int lane = threadIdx.x & 63, sub = lane / LPR, l = lane % LPR;
     const uint32_t row0 = (blockIdx.x * kRowWaves + (threadIdx.x >> 6)) * (uint32_t)(RPW * RIT) + (uint32_t)sub;
@@ -378,7 +390,7 @@ __global__ __launch_bounds__(256) void k_softmax_narrow(uint16_t *y, const uint1
 #pragma unroll
     for (int r = 0; r < RIT; ++r) {                   // rows past the end re-read row 0 and are not stored
         const uint32_t row = row0 + (uint32_t)(r * RPW);
-        raw[r] = *(const uint4 *)(x + (row < rows ? row : 0u) * ld + (colok ? c0 : 0u));
+        raw[r] = ld16<NT>(x + (row < rows ? row : 0u) * ld + (colok ? c0 : 0u));
     }
 #pragma unroll
     for (int r = 0; r < RIT; ++r) pin4(raw[r]);
@@ -403,7 +415,7 @@ __global__ __launch_bounds__(256) void k_softmax_narrow(uint16_t *y, const uint1
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] *= inv;
         const uint32_t row = row0 + (uint32_t)(r * RPW);
-        if (row < rows && colok) st16(y + row * ld + c0, pack8(v), nt);
+        if (row < rows && colok) st16(y + row * ld + c0, pack8(v), NT);
     }
 }
 
@@ -460,9 +472,9 @@ __device__ __forceinline__ float ew(float a, float b, float s) {
     return a + b;   // OP_ADD, OP_BIAS (rounded once to fp16 by the caller)
 }
 
-template <int OP, bool VEC, int U>
+template <int OP, bool VEC, int U, bool NT>
 __global__ __launch_bounds__(256) void k_elementwise(uint16_t *y, const uint16_t *a, const uint16_t *b, uint32_t rows,
-                                                     uint32_t per_row, ShDiv div, uint64_t ld, float s, uint32_t items, uint32_t nt) {
+                                                     uint32_t per_row, ShDiv div, uint64_t ld, float s, uint32_t items) {
     // U items per thread, issued together
     const uint32_t base = blockIdx.x * (256u * U) + threadIdx.x;
     (void)rows;
@@ -479,8 +491,8 @@ __global__ __launch_bounds__(256) void k_elementwise(uint16_t *y, const uint16_t
             const uint32_t itc = ok[u] ? it : 0u;
             const uint32_t r = sh_div(itc, div), cc = itc - r * per_row;
             off[u] = r * ld + 8ull * cc;
-            ra[u] = *(const uint4 *)(a + off[u]);
-            if (OP == OP_ADD || OP == OP_SILU_MUL) rb[u] = *(const uint4 *)(b + off[u]);
+            ra[u] = ld16<NT>(a + off[u]);
+            if (OP == OP_ADD || OP == OP_SILU_MUL) rb[u] = ld16<NT>(b + off[u]);
             else if (OP == OP_BIAS) rb[u] = *(const uint4 *)(b + 8ull * cc);
             else rb[u] = make_uint4(0, 0, 0, 0);
         }
@@ -489,7 +501,7 @@ __global__ __launch_bounds__(256) void k_elementwise(uint16_t *y, const uint16_t
             if (!ok[u]) continue;
             if (OP == OP_GELU) {                      // on fp16 pairs, as the GEMM epilogue does
                 const uint4 q = ra[u];
-                st16(y + off[u], make_uint4(sh_gelu_u32(q.x), sh_gelu_u32(q.y), sh_gelu_u32(q.z), sh_gelu_u32(q.w)), nt);
+                st16(y + off[u], make_uint4(sh_gelu_u32(q.x), sh_gelu_u32(q.y), sh_gelu_u32(q.z), sh_gelu_u32(q.w)), NT);
                 continue;
             }
             float fa[8], fb[8];
@@ -497,7 +509,7 @@ __global__ __launch_bounds__(256) void k_elementwise(uint16_t *y, const uint16_t
             unpack8(rb[u], fb);
 #pragma unroll
             for (int i = 0; i < 8; ++i) fa[i] = ew<OP>(fa[i], fb[i], s);
-            st16(y + off[u], pack8(fa), nt);
+            st16(y + off[u], pack8(fa), NT);
         }
         return;
     }
@@ -520,8 +532,9 @@ __global__ __launch_bounds__(256) void k_elementwise(uint16_t *y, const uint16_t
 }
 
 // dst[cols, rows] = src[rows, cols]^T, 128 x 128 tile per block, 8 x 8 blocks per thread.
+template <bool NT>
 __global__ __launch_bounds__(256) void k_transpose8(uint16_t *dst, const uint16_t *src, uint32_t rows, uint32_t cols,
-                                                    uint64_t lds, uint64_t ldd, uint32_t nt) {
+                                                    uint64_t lds, uint64_t ldd) {
     __shared__ uint4 tile[128 * 16];                      // [dst row local][16-byte chunk ^ swizzle]
     const int t = threadIdx.x;
     const uint32_t tr = blockIdx.y * 128u, tc = blockIdx.x * 128u;
@@ -531,7 +544,7 @@ __global__ __launch_bounds__(256) void k_transpose8(uint16_t *dst, const uint16_
         uint32_t w[8][4];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint4 q = *(const uint4 *)(src + (uint64_t)(r0 + i) * lds + c0);
+            const uint4 q = ld16<NT>(src + (uint64_t)(r0 + i) * lds + c0);
             w[i][0] = q.x; w[i][1] = q.y; w[i][2] = q.z; w[i][3] = q.w;
         }
 #pragma unroll
@@ -552,7 +565,7 @@ __global__ __launch_bounds__(256) void k_transpose8(uint16_t *dst, const uint16_
     for (int k = 0; k < 8; ++k) {
         const int R = (t >> 4) + 16 * k;
         const uint32_t drow = tc + R, dcol = tr + 8u * C;
-        if (drow < cols && dcol < rows) st16(dst + (uint64_t)drow * ldd + dcol, tile[R * 16 + (C ^ ((R >> 3) & 15))], nt);
+        if (drow < cols && dcol < rows) st16(dst + (uint64_t)drow * ldd + dcol, tile[R * 16 + (C ^ ((R >> 3) & 15))], NT);
     }
 }
 
@@ -606,7 +619,8 @@ void launch_layernorm(uint64_t y, uint64_t x, uint64_t g, uint64_t b, uint32_t r
         const uint32_t cap = (uint32_t)(sh_num_cus() > 0 ? sh_num_cus() : 256) * 16;
         const dim3 g(std::max<uint32_t>(1, std::min<uint32_t>(sh_cdiv(rows, gpb), cap)));
         const uint32_t nt = (uint64_t)rows * cols * 2 >= kNtBytes;
-#define SH_LNP(L, N) hipLaunchKernelGGL((k_layernorm_p<L, N>), g, dim3(256), 0, st, Y, X, G, B, rows, cols, (uint64_t)ldy, (uint64_t)ldx, eps, nt)
+#define SH_LNP(L, N) do { if (nt) hipLaunchKernelGGL((k_layernorm_p<L, N, true>), g, dim3(256), 0, st, Y, X, G, B, rows, cols, (uint64_t)ldy, (uint64_t)ldx, eps); \
+                         else hipLaunchKernelGGL((k_layernorm_p<L, N, false>), g, dim3(256), 0, st, Y, X, G, B, rows, cols, (uint64_t)ldy, (uint64_t)ldx, eps); } while (0)
         if (lpr == 32) { if (cols <= 256) SH_LNP(32, 1); else if (cols <= 512) SH_LNP(32, 2); else if (cols <= 768) SH_LNP(32, 3); else SH_LNP(32, 4); }
         else { if (cols <= 2048) SH_LNP(64, 4); else if (cols <= 3072) SH_LNP(64, 6); else SH_LNP(64, 8); }
 #undef SH_LNP
@@ -637,10 +651,11 @@ void launch_elementwise(int op, uint64_t y, uint64_t a, uint64_t b, uint32_t row
     const bool one = op == OP_GELU || nt;
     const dim3 grid(sh_cdiv(items, 256u * (one ? 1u : 4u))), block(256);
 #define SH_EW(OP) do { \
-        if (one) { if (vec) hipLaunchKernelGGL((k_elementwise<OP, true, 1>), grid, block, 0, st, Y, A, B, rows, per_row, div, (uint64_t)ld, s, items, nt); \
-                   else hipLaunchKernelGGL((k_elementwise<OP, false, 1>), grid, block, 0, st, Y, A, B, rows, per_row, div, (uint64_t)ld, s, items, nt); } \
-        else { if (vec) hipLaunchKernelGGL((k_elementwise<OP, true, 4>), grid, block, 0, st, Y, A, B, rows, per_row, div, (uint64_t)ld, s, items, nt); \
-               else hipLaunchKernelGGL((k_elementwise<OP, false, 4>), grid, block, 0, st, Y, A, B, rows, per_row, div, (uint64_t)ld, s, items, nt); } } while (0)
+        if (one) { if (vec && nt) hipLaunchKernelGGL((k_elementwise<OP, true, 1, true>), grid, block, 0, st, Y, A, B, rows, per_row, div, (uint64_t)ld, s, items); \
+                   else if (vec) hipLaunchKernelGGL((k_elementwise<OP, true, 1, false>), grid, block, 0, st, Y, A, B, rows, per_row, div, (uint64_t)ld, s, items); \
+                   else hipLaunchKernelGGL((k_elementwise<OP, false, 1, false>), grid, block, 0, st, Y, A, B, rows, per_row, div, (uint64_t)ld, s, items); } \
+        else { if (vec) hipLaunchKernelGGL((k_elementwise<OP, true, 4, false>), grid, block, 0, st, Y, A, B, rows, per_row, div, (uint64_t)ld, s, items); \
+               else hipLaunchKernelGGL((k_elementwise<OP, false, 4, false>), grid, block, 0, st, Y, A, B, rows, per_row, div, (uint64_t)ld, s, items); } } while (0)
     switch (op) {
         case OP_GELU: SH_EW(OP_GELU); break;
         case OP_ADD: SH_EW(OP_ADD); break;
@@ -842,8 +857,8 @@ void sh_dma_copy(uint64_t dst, uint64_t src, uint32_t bytes) {
         const bool big = bytes >= kNtBytes;
         const uint32_t per_block = big ? 256u : 256u * 8u;
         const uint32_t blocks = (uint32_t)((n16 + per_block - 1) / per_block);
-        if (big) hipLaunchKernelGGL(k_copy16<1>, dim3(blocks), dim3(256), 0, st, (uint4 *)dst, (const uint4 *)src, n16, 1u);
-        else hipLaunchKernelGGL(k_copy16<8>, dim3(blocks), dim3(256), 0, st, (uint4 *)dst, (const uint4 *)src, n16, 0u);
+        if (big) hipLaunchKernelGGL((k_copy16<1, true>), dim3(blocks), dim3(256), 0, st, (uint4 *)dst, (const uint4 *)src, n16);
+        else hipLaunchKernelGGL((k_copy16<8, false>), dim3(blocks), dim3(256), 0, st, (uint4 *)dst, (const uint4 *)src, n16);
     } else {
         const uint32_t blocks = (uint32_t)std::min<uint64_t>((bytes + 255) / 256, cap);
         hipLaunchKernelGGL(k_copy1, dim3(blocks), dim3(256), 0, st, (uint8_t *)dst, (const uint8_t *)src, (uint64_t)bytes);
@@ -867,9 +882,9 @@ void sh_softmax_rows(uint64_t y, uint64_t x, uint32_t rows, uint32_t cols, uint3
         const uint32_t lpr = cols <= 64 ? 8 : cols <= 128 ? 16 : 32;
         const dim3 g(sh_cdiv(rows, kRowWaves * (64 / lpr) * RIT));
         const uint32_t nt = (uint64_t)rows * cols * 2 >= kNtBytes;
-        if (lpr == 8) hipLaunchKernelGGL((k_softmax_narrow<8, RIT>), g, dim3(256), 0, st, Y, X, rows, cols, (uint64_t)ld, c, nt);
-        else if (lpr == 16) hipLaunchKernelGGL((k_softmax_narrow<16, RIT>), g, dim3(256), 0, st, Y, X, rows, cols, (uint64_t)ld, c, nt);
-        else hipLaunchKernelGGL((k_softmax_narrow<32, RIT>), g, dim3(256), 0, st, Y, X, rows, cols, (uint64_t)ld, c, nt);
+        if (lpr == 8) { if (nt) hipLaunchKernelGGL((k_softmax_narrow<8, RIT, true>), g, dim3(256), 0, st, Y, X, rows, cols, (uint64_t)ld, c); else hipLaunchKernelGGL((k_softmax_narrow<8, RIT, false>), g, dim3(256), 0, st, Y, X, rows, cols, (uint64_t)ld, c); }
+        else if (lpr == 16) { if (nt) hipLaunchKernelGGL((k_softmax_narrow<16, RIT, true>), g, dim3(256), 0, st, Y, X, rows, cols, (uint64_t)ld, c); else hipLaunchKernelGGL((k_softmax_narrow<16, RIT, false>), g, dim3(256), 0, st, Y, X, rows, cols, (uint64_t)ld, c); }
+        else { if (nt) hipLaunchKernelGGL((k_softmax_narrow<32, RIT, true>), g, dim3(256), 0, st, Y, X, rows, cols, (uint64_t)ld, c); else hipLaunchKernelGGL((k_softmax_narrow<32, RIT, false>), g, dim3(256), 0, st, Y, X, rows, cols, (uint64_t)ld, c); }
         sh_launch_ok("sh_softmax_rows");
         return;
     }
@@ -911,8 +926,10 @@ void sh_transpose(uint64_t dst, uint64_t src, uint32_t rows, uint32_t cols, uint
     const bool vec = rows % 8 == 0 && vec_ok(cols, {dst, src}, {ld_src, ld_dst});
     if (vec) {
         const dim3 grid(sh_cdiv(cols, 128), sh_cdiv(rows, 128));
-        hipLaunchKernelGGL(k_transpose8, grid, dim3(256), 0, st, D, S, rows, cols, (uint64_t)ld_src, (uint64_t)ld_dst,
-                           (uint32_t)((uint64_t)rows * cols * 2 >= kNtBytes));
+        if ((uint64_t)rows * cols * 2 >= kNtBytes)
+            hipLaunchKernelGGL((k_transpose8<true>), grid, dim3(256), 0, st, D, S, rows, cols, (uint64_t)ld_src, (uint64_t)ld_dst);
+        else
+            hipLaunchKernelGGL((k_transpose8<false>), grid, dim3(256), 0, st, D, S, rows, cols, (uint64_t)ld_src, (uint64_t)ld_dst);
     } else {
         const dim3 grid(sh_cdiv(cols, 32), sh_cdiv(rows, 32));
         hipLaunchKernelGGL(k_transpose1, grid, dim3(256), 0, st, D, S, rows, cols, (uint64_t)ld_src, (uint64_t)ld_dst);
