@@ -288,6 +288,40 @@ def test_splitk_matches_and_is_deterministic(lib, gpu):
     assert bad == 0, err
 
 
+
+def test_splitk_on_two_streams_keeps_partials_apart(lib, gpu):
+    """Split-K calls alternating on two torch streams with no synchronisation between them: each stream has its
+    own partial workspace, so every result equals the same call run alone, bit for bit, and the fp32 product
+    within tolerance. The two streams run different shapes and split counts, so a shared workspace would mix
+    their partials."""
+    import torch
+    shapes = [(256, 768, 3072, 4), (512, 512, 2048, 3)]
+    ins = []
+    for si, (M, N, K, _) in enumerate(shapes):
+        x = data.uniform(M, K, 51 + si)
+        w = (data.uniform(K, N, 61 + si).astype(np.float32) / np.sqrt(K)).astype(np.float16)
+        ins.append((x, w))
+    alone = [codes(_run_gemm(lib, x, w, splits=s)[2]) for (_, _, _, s), (x, w) in zip(shapes, ins)]
+    dev = [(to_dev(x), to_dev(w)) for x, w in ins]
+    outs = [[torch.zeros((M, N), dtype=torch.float16, device="cuda") for _ in range(3)] for M, N, _, _ in shapes]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    prev = lib.sh_get_stream()
+    torch.cuda.synchronize()
+    try:
+        for rep in range(3):
+            for si, ((M, N, K, s), (X, W)) in enumerate(zip(shapes, dev)):
+                lib.sh_set_stream(streams[si].cuda_stream)
+                rc = lib.sh_gemm_splitk(A(X), A(W), A(outs[si][rep]), M, N, K, K, N, N, None, s, shops.SH_ALL)
+                assert rc == 0, shops.last_error()
+    finally:
+        lib.sh_set_stream(prev)
+    torch.cuda.synchronize()
+    for si in range(len(shapes)):
+        for rep in range(3):
+            assert np.array_equal(codes(outs[si][rep]), alone[si]), (si, rep)
+        bad, err, _ = refs.close(to_np(outs[si][0]), refs.gemm(*ins[si]))
+        assert bad == 0, err
+
 _ORDER_CHILD = r"""
 import os, sys
 import numpy as np, torch
