@@ -247,3 +247,41 @@ def test_elementwise_above_the_infinity_cache(lib, gpu):
     torch.cuda.synchronize()
     assert torch.equal(Yb, ints * 2)
 
+
+
+def test_row_ops_above_the_infinity_cache(lib, gpu):
+    """LayerNorm, softmax and transpose on tensors of 128 MiB and more take their nontemporal builds (nontemporal
+    stores; softmax and transpose also nontemporal loads; LayerNorm walks rows over at most 32 blocks per CU): on
+    inputs tiled from one 64-row block, every block of the output equals the library's result on the block alone,
+    bit for bit (each row is reduced by one lane group in the same order), and that result matches the oracle."""
+    import torch
+    blk = 64
+    for name, rows, cols in (("layernorm", 131072, 768), ("softmax", 262144, 256), ("transpose", 131072, 768)):
+        x = data.normal((blk, cols), 44, 0.5, 1.5)
+        Xs = to_dev(x)
+        Xb = Xs.repeat(rows // blk, 1)
+        if name == "layernorm":
+            g, be = data.normal((1, cols), 45, 1.0, 0.2), data.normal((1, cols), 46, 0.0, 0.2)
+            G, BE = to_dev(g), to_dev(be)
+            Ys, Yb = _empty(blk, cols), _empty(rows, cols)
+            lib.sh_layernorm(A(Ys), A(Xs), A(G), A(BE), blk, cols, cols, 1e-5, ALL)
+            lib.sh_layernorm(A(Yb), A(Xb), A(G), A(BE), rows, cols, cols, 1e-5, ALL)
+            want = refs.layernorm(x, g, be, 1e-5)
+        elif name == "softmax":
+            Ys, Yb = _empty(blk, cols), _empty(rows, cols)
+            lib.sh_softmax_rows(A(Ys), A(Xs), blk, cols, cols, 0.7, ALL)
+            lib.sh_softmax_rows(A(Yb), A(Xb), rows, cols, cols, 0.7, ALL)
+            want = refs.softmax(x, 0.7)
+        else:
+            Ys, Yb = _empty(cols, blk), _empty(cols, rows)
+            lib.sh_transpose(A(Ys), A(Xs), blk, cols, cols, blk, ALL)
+            lib.sh_transpose(A(Yb), A(Xb), rows, cols, cols, rows, ALL)
+        torch.cuda.synchronize()
+        assert shops.last_error()[0] == 0, (name, shops.last_error())
+        if name == "transpose":
+            assert np.array_equal(codes(Ys), codes(Xs).T), name
+            assert torch.equal(Yb.view(torch.int16), Ys.view(torch.int16).repeat(1, rows // blk)), name
+        else:
+            assert torch.equal(Yb.view(torch.int16), Ys.view(torch.int16).repeat(rows // blk, 1)), name
+            assert refs.close(to_np(Ys), want)[0] == 0, name
+        del Xb, Yb
