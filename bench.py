@@ -55,7 +55,26 @@ def parse():
                          "layer's epilogue) next to torch.matmul (hipBLASLt), one JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 3 plain device copies of 512 MiB (a known-size kernel for scaling HBM counters)")
+    ap.add_argument("--stack", action="store_true",
+                    help="instead of the layer line: the 12-layer stack only (K forwards after W warm-up forwards), with "
+                         "per-layer HIP-event times, one JSON line (for kernel traces of the stack)")
+    ap.add_argument("--copy-curve", action="store_true",
+                    help="instead of the layer line: device copy bandwidth from 1 MB to 1.6 GB, cold, for the library's "
+                         "streaming copy and the HIP runtime's device-to-device copy, one JSON line")
     return ap.parse_args()
+
+
+def traced_avg_us(op: str):
+    """(kernel, average us per launch) of `op` in the committed layer kernel trace
+    (profiles/encoder_layer_b32_s256_kernel_trace.md, rocprofv3 --kernel-trace), or None."""
+    f = ROOT / "profiles" / "encoder_layer_b32_s256_kernel_trace.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 5 and cells[0] == op and cells[3].isdigit():
+            return cells[1].strip("`"), float(cells[4])
+    return None
 
 
 def counted_traffic(op: str):
@@ -151,24 +170,80 @@ def rowops_bandwidth(lib, torch, B: int, S: int, D: int, F: int, H: int, reps: i
     return out
 
 
-def extra_configs(lib, torch, enc, x, lp, p, B: int, S: int, D: int, F: int, H: int) -> dict:
-    """The other BASELINE config-4/5 measurements, outside the timed region: the 12-layer stack (layer l reads
-    layer l-1's output; weights of layer l seeded 100 + l) and batched attention at B=8, S=1024."""
-    from softhier_mlir_amd import data, encoder, shops
-    out = {}
+def stack12(torch, enc, x, B: int, S: int, D: int, F: int, reps: int = 5, warmup: int = 1) -> dict:
+    """The 12-layer stack (layer l reads layer l-1's output, weights of layer l seeded 100 + l):
+    `reps` forwards timed on the host clock between synchronisations, then one forward with HIP events around every
+    layer (the first layer also computes its input's row statistics; the others read the row partials the layer
+    before wrote)."""
+    from softhier_mlir_amd import data, encoder
     layers = [encoder.LayerParams.from_host(data.encoder_params(D, F, seed=100 + l)) for l in range(12)]
     y = torch.empty_like(x)
-    enc.forward(x, layers, B, S, out=y)                 # warm-up (buffers, tile choices)
+    for _ in range(max(1, warmup)):
+        enc.forward(x, layers, B, S, out=y)             # warm-up (buffers, tile choices)
     torch.cuda.synchronize()
-    reps = 5
     t0 = time.perf_counter()
     for _ in range(reps):
         enc.forward(x, layers, B, S, out=y)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / reps
+    # per layer: the same ping-pong as Encoder.forward, one event pair per layer
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(13)]
+    tmp = enc._pingpong
+    cur = x
+    ev[0].record()
+    for i, lp in enumerate(layers):
+        dst = y if (11 - i) % 2 == 0 else tmp
+        enc.layer_fused(cur, dst, lp, B, S, x_parts=i > 0)
+        ev[i + 1].record()
+        cur = dst
+    torch.cuda.synchronize()
+    per = [ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(12)]
     flop = 12 * encoder.flops_per_layer(B, S, D, F)
-    out["stack12"] = {"layers": 12, "ms_per_forward": round(ms, 3), "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 1)}
     del layers, y
+    return {"layers": 12, "ms_per_forward": round(ms, 3), "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 1),
+            "per_layer_us": [round(v, 1) for v in per], "us_per_layer_2_to_12": round(sum(per[1:]) / 11, 1)}
+
+
+def copy_curve(lib, torch) -> dict:
+    """Device copy bandwidth against size, cold (buffer sets rotated over >= 512 MiB, twice the Infinity Cache):
+    the library's streaming copy (sh_dma_copy) and the HIP runtime's device-to-device copy (torch copy_ =
+    hipMemcpyAsync). Traffic = 2 x bytes (read + write); median of single launches with events around each."""
+    from softhier_mlir_amd import shops
+    A = shops.addr
+    rows = []
+    for mb in (1, 2, 4, 8, 16, 25, 32, 64, 100, 128, 256, 400, 512, 1024, 1600):
+        n = mb << 20
+        nsets = max(2, (512 << 20) // n + 1)
+        sets = [(torch.empty(n // 2, dtype=torch.float16, device="cuda").fill_(1.0),
+                 torch.empty(n // 2, dtype=torch.float16, device="cuda")) for _ in range(nsets)]
+        res = {"MB": mb}
+        for name, fn in (("library", lambda a, b: lib.sh_dma_copy(A(b), A(a), n)), ("hip_d2d", lambda a, b: b.copy_(a))):
+            for a, b in sets:
+                fn(a, b)
+            torch.cuda.synchronize()
+            ts = []
+            for _ in range(3 if mb < 512 else 2):
+                for a, b in sets:
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    fn(a, b)
+                    e1.record()
+                    ts.append((e0, e1))
+            torch.cuda.synchronize()
+            us = sorted(e0.elapsed_time(e1) for e0, e1 in ts)[len(ts) // 2] * 1e3
+            res[f"{name}_us"] = round(us, 2)
+            res[f"{name}_GB/s"] = round(2 * n / (us * 1e-6) / 1e9, 1)
+        rows.append(res)
+        del sets
+        torch.cuda.empty_cache()
+    return {"copy_curve": rows}
+
+
+def extra_configs(lib, torch, enc, x, lp, p, B: int, S: int, D: int, F: int, H: int) -> dict:
+    """The other BASELINE config-4/5 measurements, outside the timed region: the 12-layer stack and batched
+    attention at B=8, S=1024."""
+    from softhier_mlir_amd import shops
+    out = {"stack12": stack12(torch, enc, x, B, S, D, F)}
     Bl, Sl = 8, 1024
     A = shops.addr
     qkv = torch.randn((Bl * Sl, 3 * D), dtype=torch.float16, device="cuda")
@@ -486,6 +561,9 @@ def main() -> int:
     if args.library_gemm:
         print(json.dumps({"library_gemm": library_gemm_table(lib, torch, args.batch, args.seq)}), flush=True)
         return 0
+    if args.copy_curve:
+        print(json.dumps(copy_curve(lib, torch)), flush=True)
+        return 0
     B, S, D, F, H = args.batch, args.seq, 768, 3072, 12
     p = data.encoder_params(D, F, seed=100)
     xh = data.normal((B * S, D), 7)
@@ -493,6 +571,9 @@ def main() -> int:
     out = torch.empty_like(x)
     enc = encoder.Encoder(D, F, H)
     enc.row_partials = not args.row_stats
+    if args.stack:
+        print(json.dumps({"stack12": stack12(torch, enc, x, B, S, D, F, reps=args.steps, warmup=args.warmup)}), flush=True)
+        return 0
     lp = encoder.LayerParams.from_host(p)
     if args.sequence == "fused":
         # one layer of the 12-layer stack as it runs there: each step reads the rows the previous step stored, and
@@ -624,6 +705,11 @@ def main() -> int:
                         "frac": round(ach / PEAK_TFLOPS, 4), "traffic": counted_traffic(dom),
                         "algorithmic_flop_per_launch": c["flop"], "algorithmic_bytes_per_launch": c["bytes"],
                         "avg_launch_us": round(us, 2)}
+            tr = traced_avg_us(dom)
+            if tr is not None:          # the committed kernel trace's average for the same op, and its fraction
+                roofline.update({"trace_kernel": tr[0], "trace_avg_launch_us": tr[1],
+                                 "trace_frac": round(c["flop"] / (tr[1] * 1e-6) / 1e12 / PEAK_TFLOPS, 4),
+                                 "trace_source": "profiles/encoder_layer_b32_s256_kernel_trace.md"})
         else:
             ach = c["bytes"] / (us * 1e-6) / 1e9
             roofline = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_GBS, "unit": "GB/s",

@@ -190,6 +190,14 @@ int         sh_last_error(void);         /* 0, or the code of the last failure (
 const char *sh_last_error_str(void);     /* message of the last failure ("" if none) */
 void        sh_set_stream(uint64_t stream);   /* hipStream_t to enqueue on (0 = legacy null stream) */
 uint64_t    sh_get_stream(void);
+/* Split-K calls keep an fp32 partials workspace per stream they ran on (at least 64 MiB each, grown geometrically,
+ * outgrown buffers kept because graphs captured earlier may address them), so a caller that creates and destroys
+ * streams would otherwise hold that memory until exit. sh_stream_release(stream) waits for the stream, then frees
+ * everything the library holds for it (0, or SH_EHIP); the next split-K call on that stream allocates again. Call
+ * it only when no graph captured on that stream will be replayed. sh_stream_workspace_bytes: the live workspace
+ * of a stream (0 if none). */
+int         sh_stream_release(uint64_t stream);
+uint64_t    sh_stream_workspace_bytes(uint64_t stream);
 double      sh_timer_last_ns(void);      /* the period sh_timer_end() printed last */
 /* Text capture for in-process callers: while on, everything the library prints (sh_printf, sample dumps,
  * timer lines) is appended to an internal buffer instead of stdout. sh_captured copies it out (NUL
@@ -209,8 +217,10 @@ int sh_gemm_splitk(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, u
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments, checks and results
  * (the same kernels and summation order, so the same bits); the fp32 partials live in a fixed 16 MiB array of
  * the library's code object on each GPU, so the call makes no hipMalloc / hipFree and skips the one-time tile
- * timing. Returns -1 (before any GPU work) when the launched split count needs more than 16 MiB of partials
- * (splits x M x N x 4 bytes). All calls on one GPU share that array: calls that overlap on one GPU race. */
+ * timing. Returns -1 (before any GPU work) when a launch that writes partials needs more than 16 MiB of them
+ * (splits x M x N x 4 bytes); a request of two equal K ranges (K % 128 == 0, 16-byte aligned operands) runs both
+ * ranges in one workgroup and writes none, at any size. All calls on one GPU share that array: calls that overlap
+ * on one GPU race. */
 int sh_gemm_splitk_noalloc(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
                            uint32_t ldx, uint32_t ldw, uint32_t ldz, const sh_gemm_cfg *cfg, uint32_t splits, uint32_t cluster);
 
@@ -229,8 +239,9 @@ typedef struct {
     uint32_t splits;      /* 1: none; 0: library choice */
     /* LayerNorm folded into the GEMM (0: off). With X the raw rows and W' = diag(gamma) W, c = 1^T W' and
      * d = beta^T W + b from sh_ln_fold, the product p = X . W' becomes z = r p - r mu c + d before the rest of the
-     * chain (act, residual), which is LN(X) . W + b; ln_stats: fp32 [M][2] (mu, r) rows from sh_row_stats, ln_c:
-     * fp32 row of N, and the bias must then be the fp32 row d (SH_BIAS_FP32). Rounded once to fp16. */
+     * chain (act, residual), which is LN(X) . W + b; ln_stats: fp32 [M][2] (mu, r) rows from sh_row_stats (8-byte
+     * aligned, else -1), ln_c: fp32 row of N, and the bias must then be the fp32 row d (SH_BIAS_FP32). Rounded once
+     * to fp16. */
     uint64_t ln_stats;
     uint64_t ln_c;
     /* Row partials (0: off): the GEMM also writes, for each stored row of Z and each 32 columns of it, the fp32 pair
@@ -257,6 +268,17 @@ int sh_gemm_ex_wt(uint64_t x, uint64_t wt, uint64_t z, uint32_t M, uint32_t N, u
  * out[2] its tile rows / columns, out[3] the split count. A large problem's first call may still replace the
  * configuration by its one-time timing. Runs no GPU work. 0, or -1 for an empty problem / NULL out. */
 int sh_gemm_plan(uint32_t M, uint32_t N, uint32_t K, uint32_t splits, uint32_t *out);
+
+/* Additive (no counterpart in the reference): the GEMM tile table that sh_gemm_plan indexes and SH_GEMM_CFG forces.
+ * sh_gemm_tile_count: its entries. sh_gemm_tile_info(i, out): out[0] / out[1] tile rows / columns, out[2] kernel
+ * family (1 register-staged: any alignment and K; 2 direct-to-LDS with a partial last k-slice variant; 5
+ * direct-to-LDS, register epilogue; 6 direct-to-LDS for the W^T operand), out[3] threads per workgroup, out[4] W^T
+ * operand, out[5] register epilogue (LayerNorm fold and row partials without fp32 partials), out[6] in-workgroup
+ * split of two equal K ranges, out[7] partial-k-slice variant. Unsplit direct-to-LDS configurations (families 2, 5
+ * and 6) store the same bits; the register-staged ones (1) store the same bits among themselves. 0, or -1 for i out
+ * of range / NULL out. No GPU work. */
+int sh_gemm_tile_count(void);
+int sh_gemm_tile_info(uint32_t i, uint32_t *out);
 
 /* Batched multi-head attention (the reference has no batch dimension): sequence b uses q + b*bsq*2 bytes,
  * likewise k/v/o with their own batch strides in elements (e.g. S*ld for rows stacked as [B*S, ld]).

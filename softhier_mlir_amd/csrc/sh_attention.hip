@@ -255,172 +255,14 @@ __global__ __launch_bounds__(256) void k_flash(AttnArgs a) {
     }
 }
 
-// ---- DMA variant (dh == 64 or 128, 16-byte aligned operands) ------------------------------------------
-// K and V key blocks are copied HBM -> LDS by global_load_lds_dwordx4 into a ring of NST stages (all four
-// blocks of an S = 256 head are requested before the first is used). K rows keep the A-operand layout of the
-// score MFMA; V stays in its natural [key][d] layout and the O^T MFMA reads its A operand (8 keys of one d per
-// lane) with two ds_read_b64_tr_b16: lane group g of a 16-key substep supplies keys 4g..4g+3 and 8+4g..8+4g+3,
-// the order in which the score accumulators hold P. Keys past S are fetched from row S-1 (valid memory) and
-// get zero weight.
+// ---- V layout of the DMA kernels (dh == 64 or 128, 16-byte aligned operands) -------------------------------
+// K and V key blocks are copied HBM -> LDS by global_load_lds_dwordx4. V stays in its natural [key][d] layout and
+// the O^T MFMA reads its A operand (8 keys of one d per lane) with two ds_read_b64_tr_b16: lane group g of a 16-key
+// substep supplies keys 4g..4g+3 and 8+4g..8+4g+3, the order in which the score accumulators hold P.
 // V rows are DC chunks wide; chunk c of row k sits at c ^ vfw(k) so a transpose read's 4 rows x 64 bytes
 // land on distinct banks (row pitch 128 B: alternate rows share a bank half; 256 B: every row starts at bank 0)
 template <int DH>
 __device__ __forceinline__ uint32_t vfw(uint32_t k) { return DH == 128 ? 4u * (k & 3u) : 4u * ((k >> 1) & 1u); }
-
-template <int DH, int NST>
-__global__ __launch_bounds__(256) void k_flash_dma(AttnArgs a) {
-    constexpr int DC = DH / 8, NS = DH / 16, DT = DH / 32;
-    constexpr int KCH = KB * DC;                     // 16-byte chunks per K (or V) block
-    constexpr int KR = KCH / 256;                    // DMA rounds per thread per block, per operand
-    constexpr int LOADS = 2 * KR;                    // DMA instructions per wave per block (K and V)
-    constexpr uint32_t STAGE = 2u * KCH * 16u;       // K block then V block
-    static_assert(KCH % 256 == 0 && NST >= 2, "attention tiling");
-    __shared__ uint4 smem[NST * 2 * KCH];
-
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = lane >> 5, r32 = lane & 31;
-    const int q4 = lane >> 4, iq = lane & 15;
-    const uint32_t b = blockIdx.z, h = blockIdx.y;
-    const uint32_t S = a.S;
-    const uint16_t *Q = a.q + b * a.bsq + (uint64_t)h * DH;
-    const uint16_t *Kp = a.k + b * a.bsk + (uint64_t)(h / a.grp) * DH;
-    const uint16_t *Vp = a.v + b * a.bsv + (uint64_t)(h / a.grp) * DH;
-    uint16_t *O = a.o + b * a.bso + (uint64_t)h * DH;
-    const uint32_t qw0 = blockIdx.x * QPB + wave * QPW, myq = qw0 + r32;
-    const uint32_t nkb = (S + KB - 1) / KB;
-
-    // per-lane DMA sources: slot p of a block -> (key, physical chunk) -> logical chunk (column part only;
-    // the row is added per block, clamped to S - 1)
-    const uint16_t *kcol[KR];
-    const uint16_t *vcol[KR];
-    uint32_t kkey[KR];
-#pragma unroll
-    for (int r = 0; r < KR; ++r) {
-        const uint32_t p = r * 256 + wave * 64 + lane, key = p / DC, pc = p % DC;
-        kkey[r] = key;
-        kcol[r] = Kp + 8 * (pc ^ kswz<DH>(key));
-        vcol[r] = Vp + 8 * (pc ^ vfw<DH>(key));
-    }
-    const uint32_t lds0 = sh_lds_addr(smem);
-    const uint32_t wave_off = (uint32_t)__builtin_amdgcn_readfirstlane(wave * 64 * 16);
-    auto issue = [&](uint32_t kb, int stage) {
-        const uint32_t st = lds0 + (uint32_t)stage * STAGE;
-        const uint32_t k0 = kb * KB;
-#pragma unroll
-        for (int r = 0; r < KR; ++r) {
-            const uint64_t row = min(k0 + kkey[r], S - 1);                      // rows past S read row S-1
-            sh_lds_dma16(kcol[r] + row * a.ldk, st + r * 4096 + wave_off);
-            sh_lds_dma16(vcol[r] + row * a.ldv, st + KCH * 16 + r * 4096 + wave_off);
-        }
-    };
-
-    sh_h8 qf[NS];
-#pragma unroll
-    for (int s = 0; s < NS; ++s) qf[s] = __builtin_bit_cast(sh_h8, ld8<true>(Q, a.ldq, myq, 16 * s + 8 * g, S, DH));
-    sh_f16v oacc[DT];
-#pragma unroll
-    for (int i = 0; i < DT; ++i) oacc[i] = sh_f16v{};
-    float m_run = -INFINITY, l_run = 0.f;
-
-#pragma unroll
-    for (int s = 0; s < NST - 1; ++s) issue(min((uint32_t)s, nkb - 1), s);
-
-    for (uint32_t kb = 0; kb < nkb; ++kb) {
-        sh_wait_vmcnt<(NST - 2) * LOADS>();
-        __syncthreads();
-        issue(min(kb + NST - 1, nkb - 1), (int)((kb + NST - 1) % NST));
-        const int st = (int)(kb % NST);
-        const uint4 *sk = smem + st * 2 * KCH;
-        const uint32_t vbase = lds0 + (uint32_t)st * STAGE + KCH * 16;
-
-        sh_f16v sacc[2];
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            sacc[tt] = sh_f16v{};
-            const uint32_t key = 32 * tt + r32;
-#pragma unroll
-            for (int s = 0; s < NS; ++s) {
-                const sh_h8 kf = __builtin_bit_cast(sh_h8, sk[key * DC + ((2 * s + g) ^ kswz<DH>(key))]);
-                sacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], sacc[tt], 0, 0, 0);
-            }
-        }
-        const bool masked = (kb + 1) * KB > S;
-        if (masked) {
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    if (kb * KB + 32 * tt + 8 * (r >> 2) + 4 * g + (r & 3) >= S) sacc[tt][r] = a.c >= 0.f ? -INFINITY : INFINITY;
-        }
-        float mb;
-        if (a.c >= 0.f) {
-            mb = -INFINITY;
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) mb = fmaxf(mb, sacc[tt][r]);
-            mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
-        } else {
-            mb = INFINITY;
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) mb = fminf(mb, sacc[tt][r]);
-            mb = fminf(mb, __shfl_xor(mb, 32, 64));
-        }
-        const float m_new = fmaxf(m_run, a.c * mb);
-        const float alpha = sh_fast_exp2(m_run - m_new);
-        m_run = m_new;
-        float psum = 0.f;
-        sh_h8 pf[4];
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float p = sh_fast_exp2(fmaf(sacc[tt][r], a.c, -m_new));
-                if (masked && kb * KB + 32 * tt + 8 * (r >> 2) + 4 * g + (r & 3) >= S) p = 0.f;
-                psum += p;
-                pf[2 * tt + (r >> 3)][r & 7] = (_Float16)p;
-            }
-        l_run = l_run * alpha + psum;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            const uint32_t d = 32 * dt + 16 * (q4 & 1) + 4 * (iq & 3);
-#pragma unroll
-            for (int sp = 0; sp < 4; ++sp) {
-                const uint32_t k0 = 16 * sp + 4 * g + (iq >> 2), k1 = k0 + 8;
-                const sh_s4 lo = sh_ds_read_tr(vbase + k0 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k0)) + 2 * (d & 7));
-                const sh_s4 hi = sh_ds_read_tr(vbase + k1 * (DH * 2) + 16 * ((d >> 3) ^ vfw<DH>(k1)) + 2 * (d & 7));
-                const sh_h8 vf = __builtin_bit_cast(sh_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-                oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[sp], oacc[dt], 0, 0, 0);
-            }
-        }
-    }
-    sh_wait_vmcnt<0>();      // clamped tail loads land before the LDS is reused below
-    __syncthreads();
-
-    const float l = l_run + __shfl_xor(l_run, 32, 64);
-    const float inv = 1.f / l;
-    uint16_t *so = (uint16_t *)smem + wave * (QPW * DH);
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-            const int d0 = 32 * dt + 8 * rb + 4 * g;
-            const uint32_t lo = (uint32_t)sh_dev_f2h(oacc[dt][4 * rb] * inv) | ((uint32_t)sh_dev_f2h(oacc[dt][4 * rb + 1] * inv) << 16);
-            const uint32_t hi = (uint32_t)sh_dev_f2h(oacc[dt][4 * rb + 2] * inv) | ((uint32_t)sh_dev_f2h(oacc[dt][4 * rb + 3] * inv) << 16);
-            const int ch = (d0 >> 3) ^ (r32 & 7);
-            *(uint2 *)(so + r32 * DH + ch * 8 + (d0 & 7)) = make_uint2(lo, hi);
-        }
-    __syncthreads();
-    for (int c = lane; c < QPW * DC; c += 64) {
-        const int row = c / DC, ch = c % DC;
-        const uint32_t qq = qw0 + row;
-        if (qq >= S) continue;
-        *(uint4 *)(O + (uint64_t)qq * a.ldo + 8 * ch) = ((const uint4 *)so)[row * DC + (ch ^ (row & 7))];
-    }
-}
 
 // Profiling stamp: the 100 MHz real-time counter into slot i of the stamp buffer (a vector store).
 __device__ __forceinline__ void attn_stamp(uint64_t *stamp, bool on, int i) {
@@ -430,7 +272,7 @@ __device__ __forceinline__ void attn_stamp(uint64_t *stamp, bool on, int i) {
     }
 }
 
-// Two-pass variant of k_flash_dma for dh 64 / 128 (aligned heads with a token mask or a scale that does not
+// Two-pass flash attention for dh 64 / 128 (aligned heads with a token mask or a scale that does not
 // fold, |c| > 1; SH_ATTN_IMPL=2 selects it for every aligned head). On CDNA the softmax
 // VALU work, not the MFMA work, bounds attention, so the row maximum is found first in a cheap pass over the
 // keys (S^T = K . Q^T on MFMA, then max3 only); the second pass recomputes the scores and, with the final
@@ -850,7 +692,9 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
         const bool move = kb == 0 ? fabsf(bm) > kTau : bm > kTau;
         if (__ballot(move) != 0) {                   // wave-uniform: m moves, O and l rescale, scores again
             const float shift = move ? bm : 0.f;
-            const float sc = sh_fast_exp2(-shift);
+            // before the first block O and l are still zero: nothing to rescale (2^-shift overflows to +inf for a
+            // first-block maximum below -128, and 0 x inf would be NaN)
+            const float sc = kb == 0 ? 1.f : sh_fast_exp2(-shift);
 #pragma unroll
             for (int i = 0; i < DT; ++i) oacc[i] *= sc;
             lsum *= sc;
@@ -1047,16 +891,13 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
         static bool attr_m = false;
         if (!attr_m) { (void)hipFuncSetAttribute((const void *)k_attn_rows, hipFuncAttributeMaxDynamicSharedMemorySize, 16384 * 4); attr_m = true; }
         go(k_attn_rows, dim3(S, H, B), S * sizeof(float));
-    } else if ((dh == 64 || dh == 128) && vec && impl == 0 && fold && (uint64_t)KB * (ldk > ldv ? ldk : ldv) * 2 < (1ull << 31)) {
+    } else if ((dh == 64 || dh == 128) && vec && impl != 2 && fold && (uint64_t)KB * (ldk > ldv ? ldk : ldv) * 2 < (1ull << 31)) {
         // (k_flash3 addresses a key block's rows as a scalar base plus 32-bit lane offsets)
         if (dh == 64) go2(k_flash3<64, 2>, grid, 0);
         else go2(k_flash3<128, 2>, grid, 0);
-    } else if ((dh == 64 || dh == 128) && vec && (impl == 0 || impl == 2)) {
+    } else if ((dh == 64 || dh == 128) && vec) {
         if (dh == 64) fold ? go2(k_flash2<64, 2, false, true>, grid, 0) : go2(k_flash2<64, 2, false, false>, grid, 0);
         else fold ? go2(k_flash2<128, 2, false, true>, grid, 0) : go2(k_flash2<128, 2, false, false>, grid, 0);
-    } else if ((dh == 64 || dh == 128) && vec && impl == 1) {
-        if (dh == 64) go(k_flash_dma<64, 4>, grid, 0);
-        else go(k_flash_dma<128, 2>, grid, 0);
     } else if (dh <= 128) {
         if (dh <= 64) {
             if (vec) go(k_flash<64, true>, grid, 0);

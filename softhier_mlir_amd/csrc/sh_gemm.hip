@@ -63,17 +63,18 @@ struct GemmArgs {
 // (mu, r = 1 / sqrt(var + eps)) of row gm for the LayerNorm fold: given (ln_parts == 0), or formed from the row's
 // ln_parts partials (s_b, M2_b) of 32 columns each (Chan, Golub and LeVeque, "Algorithms for computing the sample
 // variance", 1983): mu = sum s_b / n, M2 = sum_b (M2_b + 32 (s_b / 32 - mu)^2), var = M2 / n, n = 32 ln_parts,
-// sums in block order. Up to 32 partials (K <= 1024) are loaded at once into registers, 16 bytes per load (only the
-// P / 2 loads the row has: the partials are re-read by every column tile, so their volume is what this costs), and
-// summed twice; more are read twice from memory. Every consumer (register epilogues, split-K reduction) forms the
-// statistics with this one function.
+// sums in block order. Up to 32 partials (K <= 1024) of a 16-byte aligned array are loaded at once into registers,
+// 16 bytes per load (only the P / 2 loads the row has: the partials are re-read by every column tile, so their volume
+// is what this costs), and summed twice; more, or an array that is only 8-byte aligned, are read twice from memory
+// 8 bytes at a time (the same sums in the same order). Every consumer (register epilogues, split-K reduction) forms
+// the statistics with this one function.
 __device__ __forceinline__ float2 ln_row(const GemmArgs &a, uint32_t gm) {
     if (a.ln_parts == 0) return ((const float2 *)a.ln_stats)[gm];
     const uint32_t P = a.ln_parts;
     const float2 *pp = (const float2 *)a.ln_stats + (uint64_t)gm * P;
     const float inv_n = 1.f / (32.f * (float)P);
     float s = 0.f, m2 = 0.f;
-    if (P <= 32 && P % 2 == 0) {
+    if (P <= 32 && P % 2 == 0 && ((uintptr_t)a.ln_stats & 15u) == 0) {
         const uint32_t last = P / 2 - 1;             // wave-uniform: the branches below skip whole loads
         float4 q[16];
 #pragma unroll
@@ -621,233 +622,6 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs a) {
     epilogue<BM, BN, true, SPLIT, C::FM, C::FN>(a, acc, m0, n0, split, (uint16_t *)smem);
 }
 
-// Sum of the split partials in split order, then the epilogue of k_gemm. Item = 8 columns (VEC) or 1.
-// ---- v3: 8-wave ping-pong ----------------------------------------------------------------------------------
-// Two groups of four wavefronts share a CU (two waves per SIMD) and alternate, barrier by barrier, between a
-// memory phase (issue global->LDS DMA, read one whole k-slice of fragments from LDS into registers) and a
-// compute phase (the slice's MFMAs back to back, all operands already in registers). Group 1 starts one
-// barrier late, so while one group computes the other feeds: the MFMA pipe of every SIMD always has a wave
-// with ready operands. Group g owns output rows [g BM/2, (g+1) BM/2) of the tile; within a group the waves
-// form a 2 x 2 grid of (BM/4) x (BN/2) sub-tiles. Two LDS stages. Barrier indices (i-th __syncthreads of the
-// block): group 0 reads slice k between barriers 2k and 2k+1 and computes it before 2k+2; group 1 reads it
-// between 2k+1 and 2k+2 and computes it before 2k+3. Group 0 loads the X rows of slice k+1 while it reads
-// slice k and waits for them before barrier 2k+2; group 1 loads the W rows of slice k+1 during its compute
-// phase of slice k-1 (barriers 2k..2k+1) and waits before barrier 2k+2. Every stage is refilled only after
-// both groups passed the barrier that ends their reads of it, and is complete at the barrier that starts
-// the first read.
-template <int BM, int BN>
-struct Cfg3 {
-    static constexpr int TM = BM / 4, TN = BN / 2, FM = TM / 32, FN = TN / 32;
-    static constexpr int XCH = BM * 8;               // 16-byte chunks per X slice (BM rows x 64 k)
-    static constexpr int WCPR = BN / 8;              // chunks per W row
-    static constexpr int WCH = BK * WCPR;            // chunks per W slice
-    static constexpr int XR = XCH / 256, WR = WCH / 256;   // DMA rounds per thread of the loading group
-    static constexpr size_t STAGE = (size_t)(XCH + WCH) * 16;
-    static constexpr size_t LDS = 2 * STAGE > (size_t)BM * BN * 2 ? 2 * STAGE : (size_t)BM * BN * 2;
-    static_assert(BM % 128 == 0 && BN % 64 == 0 && XCH % 256 == 0 && WCH % 256 == 0 && FM >= 1 && FN >= 1, "tile");
-    static_assert(LDS <= 160 * 1024, "resources");
-};
-
-// Accumulators -> Z for the 8-wave layout (wave origin row0 / col0 in the tile), otherwise as epilogue().
-template <int BM, int BN, int NT, bool SPLIT, int FM, int FN>
-__device__ __forceinline__ void epilogue8(const GemmArgs &a, sh_f16v (&acc)[FM][FN], uint32_t m0, uint32_t n0, uint32_t split,
-                                          uint16_t *sC, uint32_t row0, uint32_t col0) {
-    const int t = threadIdx.x, lane = t & 63, g = lane >> 5, r32 = lane & 31;
-    if (SPLIT) {
-        float *P = a.part + (uint64_t)split * a.M * a.N;
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const uint32_t gn = n0 + col0 + j * 32 + r32;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const uint32_t gm = m0 + row0 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                    if (gm < a.M && gn < a.N) P[(uint64_t)gm * a.N + gn] = acc[i][j][r];
-                }
-            }
-        return;
-    }
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const uint32_t col = col0 + j * 32 + r32;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t row = row0 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                sC[row * BN + (((col >> 3) ^ (row & 7)) << 3) + (col & 7)] = sh_dev_f2h(acc[i][j][r]);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    __syncthreads();
-    const bool plain = !a.accumulate && !a.bias && a.act == SH_ACT_NONE && !a.res;
-    constexpr int CPR = BN / 8;
-    if (plain) {
-        for (int c = t; c < BM * CPR; c += NT) {
-            const int row = c / CPR, ch = c % CPR;
-            const uint32_t gm = m0 + row, gn = n0 + 8 * ch;
-            if (gm < a.M && gn < a.N) *(uint4 *)(a.z + (uint64_t)gm * a.ldz + gn) = ((const uint4 *)sC)[row * CPR + (ch ^ (row & 7))];
-        }
-        return;
-    }
-    constexpr int ITER = BM * CPR / NT, NB = ITER % 4 == 0 ? 4 : ITER % 2 == 0 ? 2 : 1;
-    static_assert(ITER * NT == BM * CPR, "epilogue chunk split");
-    const uint16_t *zero = (const uint16_t *)g_epi_zero;
-    const uint16_t *zs = a.accumulate ? a.z : zero, *rs = a.res ? a.res : zero;
-    const uint64_t ldzs = a.accumulate ? a.ldz : 0, ldrs = a.res ? a.ldr : 0;
-    const uint32_t zcs = a.accumulate ? 1 : 0, rcs = a.res ? 1 : 0;
-    const char *bs = a.bias ? (const char *)a.bias : (const char *)zero;
-    const uint32_t besz = a.bias ? (a.bias_fp32 ? 4 : 2) : 0, b1off = (a.bias && a.bias_fp32) ? 16 : 0;
-#pragma unroll 1
-    for (int i0 = 0; i0 < ITER; i0 += NB) {
-        uint4 q[NB], zo[NB], b0[NB], b1[NB], rq[NB];
-        uint32_t gms[NB], gns[NB];
-        bool ok[NB];
-#pragma unroll
-        for (int j = 0; j < NB; ++j) {
-            const int c = t + NT * (i0 + j), row = c / CPR, ch = c % CPR;
-            ok[j] = m0 + row < a.M && n0 + 8 * ch < a.N;
-            gms[j] = ok[j] ? m0 + row : m0;
-            gns[j] = ok[j] ? n0 + 8 * ch : n0;
-            zo[j] = *(const uint4 *)(zs + gms[j] * ldzs + gns[j] * zcs);
-            b0[j] = *(const uint4 *)(bs + gns[j] * besz);
-            b1[j] = *(const uint4 *)(bs + gns[j] * besz + b1off);
-            rq[j] = *(const uint4 *)(rs + gms[j] * ldrs + gns[j] * rcs);
-        }
-#pragma unroll
-        for (int j = 0; j < NB; ++j) {
-            const int c = t + NT * (i0 + j), row = c / CPR, ch = c % CPR;
-            q[j] = ((const uint4 *)sC)[row * CPR + (ch ^ (row & 7))];
-        }
-#pragma unroll
-        for (int j = 0; j < NB; ++j) q[j] = epi_chain8(a, q[j], zo[j], b0[j], b1[j], rq[j]);
-#pragma unroll
-        for (int j = 0; j < NB; ++j)
-            if (ok[j]) *(uint4 *)(a.z + (uint64_t)gms[j] * a.ldz + gns[j]) = q[j];
-    }
-}
-
-// One block barrier that the compiler cannot move other instructions across (MFMAs included).
-__device__ __forceinline__ void hard_barrier() {
-    __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();
-    __builtin_amdgcn_sched_barrier(0);
-}
-
-template <int BM, int BN, bool SPLIT>
-__global__ __launch_bounds__(512) void k_gemm3(GemmArgs a) {
-    using C = Cfg3<BM, BN>;
-    extern __shared__ uint4 smem[];
-    const int t = threadIdx.x, lane = t & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(t >> 6), grp = wave >> 2, w4 = wave & 3;   // wave-uniform
-    const int wm = w4 >> 1, wn = w4 & 1, g = lane >> 5, r32 = lane & 31;
-    const int lt = t & 255;                            // thread index within the group
-
-    const uint32_t nblk = a.tiles_m * a.tiles_n * a.splits;
-    uint32_t tm, tn, split;
-    tile_of(a, blockIdx.x, nblk, tm, tn, split);
-    const uint32_t m0 = tm * BM, n0 = tn * BN;
-    const uint32_t kbeg = split * a.kps;
-    const uint32_t kend = min(a.K, kbeg + a.kps);
-    const int KT = kend > kbeg ? (int)((kend - kbeg) / BK) : 0;
-
-    // DMA sources of this thread's rounds: group 0 owns the X slice, group 1 the W slice
-    constexpr int NR = C::XR > C::WR ? C::XR : C::WR;
-    const uint16_t *src[NR];
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-        const uint32_t p = r * 256 + lt;
-        if (grp == 0) {
-            const uint32_t m = p >> 3, c = (p & 7) ^ swz(m);
-            src[r] = a.x + (uint64_t)min(m0 + m, a.M - 1) * a.ldx + kbeg + 8 * c;
-        } else {
-            const uint32_t k = p / C::WCPR, c = (p % C::WCPR) ^ fw<BN>(k);
-            uint32_t gn = n0 + 8 * c;
-            if (gn >= a.N) gn = a.N - 8;
-            src[r] = a.w + (uint64_t)(kbeg + k) * a.ldw + gn;
-        }
-    }
-    const uint32_t lds0 = sh_lds_addr(smem);
-    const uint32_t wave_off = (uint32_t)__builtin_amdgcn_readfirstlane(w4 * 64 * 16);
-    const int my_rounds = grp == 0 ? C::XR : C::WR;
-    auto issue = [&](int slice, int stage) {        // this thread's share of slice `slice` into `stage`
-        const uint32_t st = lds0 + (uint32_t)stage * (uint32_t)C::STAGE + (grp == 0 ? 0u : (uint32_t)C::XCH * 16u);
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-            if (r >= my_rounds) break;
-            const uint64_t adv = grp == 0 ? (uint64_t)slice * BK : (uint64_t)slice * BK * a.ldw;
-            sh_lds_dma16(src[r] + adv, st + r * 4096 + wave_off);
-        }
-    };
-
-    sh_f16v acc[C::FM][C::FN];
-#pragma unroll
-    for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-        for (int j = 0; j < C::FN; ++j) acc[i][j] = sh_f16v{};
-    const uint32_t row0 = grp * (BM / 2) + wm * C::TM, col0 = wn * C::TN;
-    const int q = lane >> 4, iq = lane & 15;
-
-    sh_h8 af[4][C::FM], bf[4][C::FN];
-    auto read_slice = [&](int stage) {
-        const uint4 *X = (const uint4 *)((const char *)smem + (uint32_t)stage * (uint32_t)C::STAGE);
-        const uint32_t wbase = lds0 + (uint32_t)stage * (uint32_t)C::STAGE + C::XCH * 16;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-#pragma unroll
-            for (int i = 0; i < C::FM; ++i) {
-                const uint32_t m = row0 + i * 32 + r32;
-                af[s][i] = __builtin_bit_cast(sh_h8, X[m * 8 + ((2 * s + g) ^ swz(m))]);
-            }
-#pragma unroll
-            for (int j = 0; j < C::FN; ++j) {
-                const uint32_t n = (uint32_t)(col0 + j * 32 + 16 * (q & 1) + 4 * (iq & 3));
-                const uint32_t k0 = 16 * s + 8 * g + (iq >> 2), k1 = k0 + 4;
-                const sh_s4 lo = sh_ds_read_tr(wbase + k0 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k0)) + 2 * (n & 7));
-                const sh_s4 hi = sh_ds_read_tr(wbase + k1 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k1)) + 2 * (n & 7));
-                bf[s][j] = __builtin_bit_cast(sh_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-            }
-        }
-    };
-    auto compute_slice = [&]() {
-        __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-#pragma unroll
-            for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-                for (int j = 0; j < C::FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[s][i], bf[s][j], acc[i][j], 0, 0, 0);
-        __builtin_amdgcn_s_setprio(0);
-    };
-
-    // prologue: slice 0 complete at barrier 0; group 1 also has its share of slice 1 in flight
-    if (KT > 0) {
-        issue(0, 0);
-        if (grp == 1 && KT > 1) { issue(1, 1); sh_wait_vmcnt<C::WR>(); }
-        else sh_wait_vmcnt<0>();
-    }
-    hard_barrier();                                   // barrier 0
-    if (grp == 1) hard_barrier();                     // barrier 1: group 1 runs one phase behind
-    for (int k = 0; k < KT; ++k) {
-        const int st = k & 1;
-        // memory phase
-        if (grp == 0 && k + 1 < KT) issue(k + 1, st ^ 1);
-        read_slice(st);
-        if (grp == 1) sh_wait_vmcnt<0>();                // group 1's share of slice k+1 (issued a phase ago)
-        __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0): the fragments are in registers
-        hard_barrier();
-        // compute phase
-        if (grp == 1 && k + 2 < KT) issue(k + 2, st);
-        compute_slice();
-        if (grp == 0) sh_wait_vmcnt<0>();                // group 0's share of slice k+1
-        hard_barrier();
-    }
-    if (grp == 0) hard_barrier();                     // both groups end on the same barrier count
-    epilogue8<BM, BN, 512, SPLIT, C::FM, C::FN>(a, acc, m0, n0, split, (uint16_t *)smem, row0, col0);
-}
-
 // ---- epilogue from registers (Z^T accumulator layout) ------------------------------------------------------
 // Kernels that pass the MFMA operands swapped (first = W fragment, second = X fragment) hold every 32 x 32
 // accumulator as a block of Z^T: lane l has row l % 32 of Z and columns 8 q + 4 g + e in register 4 q + e
@@ -1013,18 +787,6 @@ __device__ __forceinline__ void chain_chunks(const GemmArgs &a, uint4 (&q)[FM][F
     }
 }
 
-// Accumulators (Z^T layout) -> fp16 chunks with the epilogue chain applied.
-template <int BM, int BN, int FM, int FN>
-__device__ __forceinline__ void finish_chunks(const GemmArgs &a, sh_f16v (&acc)[FM][FN], uint32_t m0, uint32_t n0,
-                                              uint4 (&q)[FM][FN][2], int wm, int wn, const LnRows<FM> &ln) {
-    if (a.ln_stats) ln_fold_zt<FM, FN>(a, acc, ln, n0 + wn * (BN / 2));
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) zt_chunks<FM, FN>(acc, i, j, q[i][j]);
-    chain_chunks<BM, BN, FM, FN>(a, q, m0, n0, wm, wn);
-}
-
 // Store a finished tile's chunks (origin m0, n0).
 template <int BM, int BN, int FM, int FN>
 __device__ __forceinline__ void store_all(const GemmArgs &a, const uint4 (&q)[FM][FN][2], uint32_t m0, uint32_t n0, int wm, int wn) {
@@ -1112,187 +874,23 @@ __device__ __forceinline__ void store_partials_zt(const GemmArgs &a, const sh_f1
             }
 }
 
-// ---- v4: 256-row tiles, 32-k slices through a deep DMA ring ------------------------------------------------
-// NT / 64 wavefronts: four as 2 x 2 (each owning 128 x BN/2 outputs, one wavefront per SIMD) or eight as 2 x 4
-// (128 x BN/4 each, two per SIMD: while one waits on LDS the other issues MFMAs). 256 x BN is the largest tile
-// one workgroup of a CU can hold, which keeps the per-CU operand feed at (256 + BN) x 32 x 2 bytes per 32-k
-// slice (about 70-90 GB/s per CU at the MFMA rate). Slices of 32 k flow through a STAGES-deep LDS ring, so
-// the loads of slice kt + STAGES - 1 are issued right after the barrier that opens slice kt and have
-// STAGES - 1 slices of MFMA time to land. The two k-substeps of a slice alternate fragment buffers, and the
-// MFMAs of substep 1 of slice kt run after the barrier of slice kt + 1, while the first fragment reads of
-// slice kt + 1 are in flight, so no barrier leaves the MFMA pipe without work.
-// LDS X rows are 64 bytes (4 chunks of 16 B), chunk c of row m stored at c ^ ((m >> 2) & 3): the 16 rows read
-// by 16 lanes of one ds_read_b128 then cover 16 distinct 16-byte bank groups. W rows (k-major, BN halves) are
-// laid out and read with ds_read_b64_tr_b16 as in k_gemm2. Every lane keeps the k order of k_gemm2 (substep s,
-// lane group g -> k chunk 2 s + g), so both kernels sum the products of one output element in the same order.
-template <int BN, int STAGES, int NT = 256, int BM_ = 256, int SK_ = 32>
-struct Cfg4 {
-    static constexpr int WGN = NT / 128;               // wavefronts along N (2 x WGN grid)
-    static constexpr int BM = BM_, SK = SK_, TM = BM / 2, TN = BN / WGN, FM = TM / 32, FN = TN / 32;
-    static constexpr int XCPR = SK / 8;                // 16-byte chunks per X row of a slice
-    static constexpr int NS = SK / 16;                 // MFMA k-substeps per slice
-    static constexpr int XCH = BM * XCPR;              // 16-byte chunks per X slice
-    static constexpr int WCPR = BN / 8;                // chunks per W row (k-major W)
-    static constexpr int WCH = SK * WCPR;              // chunks per W slice
-    static constexpr int XR = XCH / NT, WR = WCH / NT;
-    static constexpr int LOADS = XR + WR;              // DMA instructions per wave per slice
-    static constexpr size_t STAGE = (size_t)(XCH + WCH) * 16;
-    static constexpr size_t LDS = STAGES * STAGE > (size_t)BM * BN * 2 ? STAGES * STAGE : (size_t)BM * BN * 2;
-    static_assert((NT == 256 || NT == 512) && (BM == 128 || BM == 256) && BN % 64 == 0 && BN <= 256 && TN % 32 == 0 &&
-                  (SK == 32 || SK == 64) && XCH % NT == 0 && WCH % NT == 0 && FN >= 1, "tile");
-    static_assert(STAGES >= 2 && LOADS * (STAGES - 2) < 64 && LDS <= 160 * 1024, "resources");
-};
-
+// X row swizzle of a slice. 32-k slices have 64-byte LDS rows (4 chunks of 16 B): chunk c of row m is stored at
+// c ^ ((m >> 2) & 3), so the 16 rows read by 16 lanes of one ds_read_b128 cover 16 distinct 16-byte bank groups.
+// 64-k slices have 128-byte rows, swizzled as in k_gemm2.
 __device__ __forceinline__ uint32_t sx4(uint32_t m) { return (m >> 2) & 3u; }
-// X row swizzle of a slice: 64-byte rows (32-k slices) as above, 128-byte rows (64-k slices) as in k_gemm2
 template <int SK>
 __device__ __forceinline__ uint32_t xswz(uint32_t m) { return SK == 32 ? sx4(m) : swz(m); }
 
-// MINW: minimum wavefronts per SIMD the register allocation must allow (3 lets three 128 x 192 workgroups with a
-// 2-stage ring share a CU: 40 KB of LDS and <= 168 registers each).
-// REG (four wavefronts only): MFMA operands swapped and the epilogue straight from registers (see above).
-// SK: k per slice. With 64 (four k-substeps per slice) every X row segment a DMA instruction fetches is one
-// whole 128-byte line: the global -> LDS path costs per cache line touched, and 32-k slices (64-byte segments,
-// 16 rows per instruction) halve its throughput for X. The k order, hence every stored bit, is the same.
-template <int BN, int STAGES, bool SPLIT, int NT = 256, int BM_ = 256, int MINW = 1, bool REG = false, int SK_ = 32>
-__global__ __launch_bounds__(NT, MINW) void k_gemm4(GemmArgs a) {
-    static_assert(!REG || NT == 256, "register epilogue: 2 x 2 wavefronts");
-    using C = Cfg4<BN, STAGES, NT, BM_, SK_>;
-    constexpr int BM = C::BM, SK = C::SK, FM = C::FM, FN = C::FN;
-    extern __shared__ uint4 smem[];
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int wm = wave / C::WGN, wn = wave % C::WGN, g = lane >> 5, r32 = lane & 31;
-
-    const uint32_t nblk = a.tiles_m * a.tiles_n * a.splits;
-    uint32_t tm, tn, split;
-    tile_of(a, blockIdx.x, nblk, tm, tn, split);
-    const uint32_t m0 = tm * BM, n0 = tn * BN;
-    const uint32_t kbeg = split * a.kps;
-    const uint32_t kend = min(a.K, kbeg + a.kps);
-    const int KT = kend > kbeg ? (int)((kend - kbeg) / SK) : 0;
-
-    // per-lane DMA sources of every round (rows past M / columns past N are read from clamped valid addresses
-    // and only feed outputs that are never stored)
-    const uint16_t *xs[C::XR];
-    const uint16_t *ws[C::WR];
-#pragma unroll
-    for (int r = 0; r < C::XR; ++r) {
-        const uint32_t p = r * NT + wave * 64 + lane, m = p / C::XCPR, c = (p % C::XCPR) ^ xswz<SK>(m);
-        xs[r] = a.x + (uint64_t)min(m0 + m, a.M - 1) * a.ldx + kbeg + 8 * c;
-    }
-#pragma unroll
-    for (int r = 0; r < C::WR; ++r) {
-        const uint32_t p = r * NT + wave * 64 + lane, k = p / C::WCPR, c = (p % C::WCPR) ^ fw<BN>(k);
-        uint32_t gn = n0 + 8 * c;
-        if (gn >= a.N) gn = a.N - 8;
-        ws[r] = a.w + (uint64_t)(kbeg + k) * a.ldw + gn;
-    }
-    const uint32_t lds0 = sh_lds_addr(smem);
-    const uint32_t wave_off = (uint32_t)__builtin_amdgcn_readfirstlane(wave * 64 * 16);
-    const uint64_t wadv = (uint64_t)SK * a.ldw;
-    auto issue_all = [&](int src, int stage) {      // the LOADS DMAs of k-slice `src` into LDS stage `stage`
-        const uint32_t st = lds0 + (uint32_t)stage * (uint32_t)C::STAGE;
-#pragma unroll
-        for (int d = 0; d < C::XR; ++d) sh_lds_dma16(xs[d] + (uint64_t)src * SK, st + d * NT * 16 + wave_off);
-#pragma unroll
-        for (int d = 0; d < C::WR; ++d) sh_lds_dma16(ws[d] + (uint64_t)src * wadv, st + C::XCH * 16 + d * NT * 16 + wave_off);
-    };
-
-    sh_f16v acc[FM][FN];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = sh_f16v{};
-
-    const int q = lane >> 4, iq = lane & 15;
-    auto load_frags = [&](int stage, int s, sh_h8 (&af)[FM], sh_h8 (&bf)[FN]) {
-        const uint4 *X = (const uint4 *)((const char *)smem + (uint32_t)stage * (uint32_t)C::STAGE);
-        const uint32_t c = (uint32_t)(2 * s + g);
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            const uint32_t m = (uint32_t)(wm * C::TM + i * 32 + r32);
-            af[i] = __builtin_bit_cast(sh_h8, X[m * C::XCPR + (c ^ xswz<SK>(m))]);
-        }
-        const uint32_t wbase = lds0 + (uint32_t)stage * (uint32_t)C::STAGE + C::XCH * 16;
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const uint32_t n = (uint32_t)(wn * C::TN + j * 32 + 16 * (q & 1) + 4 * (iq & 3));
-            const uint32_t k0 = 16 * s + 8 * g + (iq >> 2), k1 = k0 + 4;
-            const sh_s4 lo = sh_ds_read_tr(wbase + k0 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k0)) + 2 * (n & 7));
-            const sh_s4 hi = sh_ds_read_tr(wbase + k1 * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k1)) + 2 * (n & 7));
-            bf[j] = __builtin_bit_cast(sh_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-        }
-    };
-    auto mfmas = [&](const sh_h8 (&af)[FM], const sh_h8 (&bf)[FN]) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                if constexpr (REG) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[j], af[i], acc[i][j], 0, 0, 0);
-                else acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-            }
-    };
-
-    const LnRows<FM> lnw = ln_rows<FM>(a, m0 + wm * C::TM);   // (before the first DMAs: no wait on them)
-    // prologue: slices 0 .. STAGES-2 (past the end: the last slice again, into stages nobody reads), so every
-    // iteration waits for a constant number of outstanding DMAs
-    if (KT > 0) {
-#pragma unroll
-        for (int s = 0; s < STAGES - 1; ++s) issue_all(min(s, KT - 1), s);
-    }
-
-    sh_h8 a0[FM], b0[FN], a1[FM], b1[FN];
-    for (int kt = 0; kt < KT; ++kt) {
-        sh_wait_vmcnt<(STAGES - 2) * C::LOADS>();        // slice kt has landed (this wave's share) ...
-        __builtin_amdgcn_s_waitcnt(0xC07F);           // ... and this wave's reads of slice kt - 1 are done
-        __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_barrier();                 // every share landed; the stage of slice kt - 1 is free
-        __builtin_amdgcn_sched_barrier(0);
-        issue_all(min(kt + STAGES - 1, KT - 1), (kt + STAGES - 1) % STAGES);
-        const int st = kt % STAGES;
-        load_frags(st, 0, a0, b0);
-        __builtin_amdgcn_sched_barrier(0);
-        if (kt > 0) mfmas(a1, b1);                    // last substep of slice kt - 1, under the reads just issued
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int ss = 1; ss < C::NS; ++ss) {          // substep ss loads while substep ss - 1 computes
-            if (ss & 1) load_frags(st, ss, a1, b1);
-            else load_frags(st, ss, a0, b0);
-            __builtin_amdgcn_sched_barrier(0);
-            if (ss & 1) mfmas(a0, b0);
-            else mfmas(a1, b1);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-    if (KT > 0) mfmas(a1, b1);
-    if constexpr (REG) {
-        if constexpr (SPLIT) {
-            store_partials_zt<BM, BN, FM, FN>(a, acc, m0, n0, split, wm, wn);
-        } else {
-            uint4 q[FM][FN][2];
-            finish_chunks<BM, BN, FM, FN>(a, acc, m0, n0, q, wm, wn, lnw);
-            if (a.stats_out) stats_zt<FM, FN>(a, q, m0 + wm * (BM / 2), n0 + wn * (BN / 2));
-            store_all<BM, BN, FM, FN>(a, q, m0, n0, wm, wn);
-        }
-        sh_wait_vmcnt<0>();     // no DMA may still target this workgroup's LDS when it exits
-        return;
-    }
-    sh_wait_vmcnt<0>();     // the clamped tail loads must land before the tile is staged in the same LDS
-    __syncthreads();
-    if constexpr (NT == 256) epilogue<BM, BN, true, SPLIT, FM, FN>(a, acc, m0, n0, split, (uint16_t *)smem);
-    else epilogue8<BM, BN, NT, SPLIT, FM, FN>(a, acc, m0, n0, split, (uint16_t *)smem, (uint32_t)(wm * C::TM), (uint32_t)(wn * C::TN));
-}
-
 // ---- v5: LDS-lean tiles, MFMAs interleaved one by one with the LDS reads and DMAs ---------------------------
 // Four wavefronts (2 x 2, one per SIMD), each owning a (BM/2) x (BN/2) block of Z^T accumulators (MFMA operands
-// swapped as in k_gemm4 REG, epilogue straight from registers). SK-wide k-slices (32 or 64) flow through an
+// swapped, epilogue straight from registers: see above). SK-wide k-slices (32 or 64) flow through an
 // NST-stage LDS ring filled by global_load_lds_dwordx4; one barrier per slice. Within a slice the work is cut
 // into one segment per 16-k substep: segment s issues the fragment reads of substep s and its share of the
 // DMAs of slice kt + NST - 1, each placed between two MFMAs of substep s - 1 (the MFMAs of a slice's last
 // substep run in the next slice's first segment, after its barrier). The order is fixed in source with
 // sched_barrier fences: every 32-cycle MFMA has at most a few other instructions between it and the next, so
 // the MFMA pipe never waits on a burst of reads, and each read is issued several MFMAs before its first use.
-// W is read either in the caller's [K, N] layout (LDS transpose reads, as k_gemm4) or, with WT, as W^T [N, K]
+// W is read either in the caller's [K, N] layout (LDS transpose reads, as k_gemm2) or, with WT, as W^T [N, K]
 // (rows of k like X: plain 16-byte LDS reads, half the LDS read cost). The k order per lane is k_gemm2's
 // (substep s, lane group g -> 8-k chunk 2 s + g), so every configuration stores the same bits.
 // PRE: the epilogue's bias row and residual are loaded into registers at the start of the last slice, so the
@@ -1820,6 +1418,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void k_gemm6(GemmArgs a) {
     sh_wait_vmcnt<0>();      // no DMA may still target this workgroup's LDS when it exits
 }
 
+// Sum of the split partials in split order, then the epilogue chain. Item = 8 columns (VEC) or 1.
 template <bool VEC>
 // One item per thread in 64-thread workgroups: a split-K output is usually small (M of a few hundred), and
 // single-wave workgroups spread its items over every CU.
@@ -1918,14 +1517,6 @@ struct KCfg {
 #define SH_KCFG2(BM, BN, ST, EFF) { BM, BN, ST, true, { k_gemm2<BM, BN, ST, false>, k_gemm2<BM, BN, ST, true> }, \
                                     { nullptr, nullptr }, Cfg2<BM, BN, ST>::LDS, EFF, false, 256, true, \
                                     { k_gemm2<BM, BN, ST, false, true>, k_gemm2<BM, BN, ST, true, true> } }
-#define SH_KCFG4(BM, BN, ST, NT, W, EFF) { BM, BN, ST, true, { k_gemm4<BN, ST, false, NT, BM, W>, k_gemm4<BN, ST, true, NT, BM, W> }, \
-                                           { nullptr, nullptr }, Cfg4<BN, ST, NT, BM>::LDS, EFF, false, NT }
-#define SH_KCFG4R(BM, BN, ST, W, EFF) { BM, BN, ST, true, { k_gemm4<BN, ST, false, 256, BM, W, true>, k_gemm4<BN, ST, true, 256, BM, W, true> }, \
-                                       { nullptr, nullptr }, (size_t)(ST) * Cfg4<BN, ST, 256, BM>::STAGE, EFF, false, 256, \
-                                       false, { nullptr, nullptr }, false, { nullptr, nullptr }, { nullptr, nullptr }, true }
-#define SH_KCFG4S(BM, BN, ST, W, EFF) { BM, BN, ST, true, { k_gemm4<BN, ST, false, 256, BM, W, true, 64>, k_gemm4<BN, ST, true, 256, BM, W, true, 64> }, \
-                                       { nullptr, nullptr }, (size_t)(ST) * Cfg4<BN, ST, 256, BM, 64>::STAGE, EFF, false, 256, \
-                                       false, { nullptr, nullptr }, false, { nullptr, nullptr }, { nullptr, nullptr }, true }
 #define SH_KCFG5(BM, BN, SK, NST, W, EFF) { BM, BN, NST, true, { k_gemm5<BM, BN, SK, NST, false, W, false, true>, \
                                               k_gemm5<BM, BN, SK, NST, false, W, true, true> }, \
                                             { nullptr, nullptr }, Cfg5<BM, BN, SK, NST, false>::LDS, EFF, false, 256, \
@@ -1935,8 +1526,6 @@ struct KCfg {
                                              { nullptr, nullptr }, Cfg5<BM, BN, SK, NST, false>::LDS, EFF, false, 256, \
                                              false, { nullptr, nullptr }, false, { nullptr, nullptr }, { nullptr, nullptr }, true, \
                                              k_gemm5<BM, BN, SK, NST, false, 1, false, true, 2> }
-#define SH_KCFG3(BM, BN, EFF) { BM, BN, 2, true, { k_gemm3<BM, BN, false>, k_gemm3<BM, BN, true> }, \
-                                { nullptr, nullptr }, Cfg3<BM, BN>::LDS, EFF, false, 512 }
 // eff = sustained fraction of the MFMA peak per CU measured for each tile on MI355X (tile-time model of
 // est_time below); it only ranks the configurations.
 KCfg g_cfgs[] = {
@@ -1948,40 +1537,17 @@ KCfg g_cfgs[] = {
     SH_KCFG(64, 64, 0.10f),
     SH_KCFG2(256, 256, 2, 0.35f),
     SH_KCFG2(256, 128, 3, 0.33f),
-    SH_KCFG2(128, 256, 3, 0.32f),
-    SH_KCFG2(128, 192, 3, 0.27f),
-    SH_KCFG2(128, 128, 3, 0.25f),
     SH_KCFG2(128, 192, 2, 0.30f),
     SH_KCFG2(128, 128, 2, 0.27f),
-    SH_KCFG3(256, 128, 0.28f),
-    SH_KCFG3(128, 256, 0.28f),
-    SH_KCFG3(128, 128, 0.26f),
-    SH_KCFG4(256, 256, 4, 256, 1, 0.36f),
-    SH_KCFG4(256, 192, 5, 256, 1, 0.30f),
-    SH_KCFG4(256, 256, 4, 512, 1, 0.45f),
-    SH_KCFG4(256, 128, 6, 512, 1, 0.40f),
-    SH_KCFG4(128, 192, 4, 256, 1, 0.32f),
-    SH_KCFG4(128, 256, 4, 256, 1, 0.32f),
-    SH_KCFG4(128, 128, 4, 256, 1, 0.30f),
-    SH_KCFG4(128, 192, 2, 256, 3, 0.33f),
-    SH_KCFG4(128, 192, 3, 256, 2, 0.33f),
-    SH_KCFG4R(128, 192, 2, 3, 0.34f),
-    SH_KCFG4R(128, 192, 3, 2, 0.34f),
-    SH_KCFG4R(128, 192, 4, 1, 0.34f),
-    SH_KCFG4S(128, 192, 2, 2, 0.36f),
     SH_KCFG2(64, 64, 2, 0.12f),             // small tiles: many workgroups for small problems (latency-bound)
     SH_KCFG2(64, 64, 3, 0.13f),
     SH_KCFG2(64, 128, 2, 0.16f),
     SH_KCFG2(128, 64, 2, 0.16f),
     // LDS-lean tiles with MFMA / read / DMA interleaving (k_gemm5)
-    SH_KCFG5(256, 256, 64, 2, 1, 0.40f),
-    SH_KCFG5(256, 256, 32, 4, 1, 0.40f),
     SH_KCFG5(256, 192, 64, 2, 1, 0.38f),
-    SH_KCFG5(256, 192, 32, 4, 1, 0.38f),
     SH_KCFG5(128, 192, 64, 3, 1, 0.36f),
     SH_KCFG5K(128, 192, 64, 2, 2, 0.36f),
     SH_KCFG5(128, 256, 64, 2, 1, 0.36f),
-    SH_KCFG5(256, 128, 64, 2, 1, 0.36f),
     // W^T operand (sh_gemm_ex_wt): 4 / 8 wavefronts, up to 256 x 384 tiles (k_gemm6)
     SH_KCFG6(256, 384, 2, 4, 64, 2, 2, false, false, 0.50f),
     SH_KCFG6(256, 384, 2, 4, 32, 4, 2, false, false, 0.50f),
@@ -1998,16 +1564,11 @@ KCfg g_cfgs[] = {
     SH_KCFG6(64, 128, 2, 2, 32, 4, 2, false, true, 0.16f),
     SH_KCFG6(128, 128, 2, 2, 32, 4, 2, true, true, 0.25f),
     SH_KCFG5K(128, 192, 32, 4, 2, 0.36f),       // two workgroups per CU with a deeper ring of 32-k slices
-    SH_KCFG5(128, 128, 64, 2, 2, 0.30f),
     SH_KCFG5(128, 128, 32, 4, 2, 0.30f),
     SH_KCFG5(128, 192, 32, 4, 1, 0.36f),        // one workgroup per CU: residual and bias loaded during the last slice
 };
 #undef SH_KCFG
 #undef SH_KCFG2
-#undef SH_KCFG3
-#undef SH_KCFG4
-#undef SH_KCFG4R
-#undef SH_KCFG4S
 #undef SH_KCFG5
 #undef SH_KCFG5K
 #undef SH_KCFG6
@@ -2376,7 +1937,8 @@ int check_ln(const char *name, const sh_gemm_epi *e, const sh_gemm_cfg &c, uint3
         sh_set_error(-1, "[%s] LayerNorm fold needs ln_stats, ln_c and the fp32 bias row d, without accumulate", name);
         return -1;
     }
-    if ((e->ln_stats | e->ln_c | e->bias) % 4) { sh_set_error(-1, "[%s] LayerNorm fold rows must be 4-byte aligned", name); return -1; }
+    if ((e->ln_c | e->bias) % 4) { sh_set_error(-1, "[%s] LayerNorm fold rows must be 4-byte aligned", name); return -1; }
+    if (e->ln_stats % 8) { sh_set_error(-1, "[%s] ln_stats ((mu, r) or partial pairs) must be 8-byte aligned", name); return -1; }
     if (e->ln_parts && (uint64_t)e->ln_parts * 32 != K) {
         sh_set_error(-1, "[%s] %u row partials of 32 columns do not cover K = %u", name, e->ln_parts, K);
         return -1;
@@ -2440,8 +2002,9 @@ int sh_gemm_splitk(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, u
 }
 
 // sh_gemm_splitk with the partials in the library's fixed scratch array: no hipMalloc / hipFree and no one-time
-// tile timing (that allocates a trial output). The launched split count must need at most 16 MiB of fp32
-// partials (splits x M x N x 4 bytes), else -1 before any GPU work. Every call on one GPU shares its array:
+// tile timing (that allocates a trial output). A launch that writes fp32 partials must need at most 16 MiB of them
+// (splits x M x N x 4 bytes), else -1 before any GPU work (launch() checks it on that path only: two equal K ranges
+// of a direct-to-LDS plan run in one workgroup and write no partials). Every call on one GPU shares its array:
 // calls that overlap on one GPU (different streams, or host threads) race on it. Each call writes every partial
 // it reads, so nothing has to be cleared between calls.
 int sh_gemm_splitk_noalloc(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint32_t N, uint32_t K,
@@ -2449,17 +2012,22 @@ int sh_gemm_splitk_noalloc(uint64_t x, uint64_t w, uint64_t z, uint32_t M, uint3
     sh_gemm_cfg c;
     cfg_fill(&c, cfg);
     if (int rc = check_tiled("sh_gemm_splitk_noalloc", c, x, w, z, M, N, K)) return rc;
-    const SplitK sk = split_k(K, splits);
-    if ((size_t)sk.splits * M * N * sizeof(float) > kNoAllocScratchBytes && sk.splits > 1) {
-        sh_set_error(-1, "[sh_gemm_splitk_noalloc] %u splits of %ux%u fp32 partials exceed the %zu B scratch", sk.splits, M, N,
-                     kNoAllocScratchBytes);
-        return -1;
-    }
     sh_ensure_init();
     float *part = scratch_ptr();
     if (!part) return SH_EHIP;
     GemmReq r{x, w, z, M, N, K, ldx, ldw, ldz, c.accumulate, nullptr, splits, false, part};
     return launch(r, "sh_gemm_splitk_noalloc");
+}
+
+int sh_gemm_tile_count(void) { return kNumCfg; }
+
+int sh_gemm_tile_info(uint32_t i, uint32_t *out) {
+    if (i >= (uint32_t)kNumCfg || !out) { sh_set_error(-1, "[sh_gemm_tile_info] no configuration %u or NULL output", i); return -1; }
+    const KCfg &c = g_cfgs[i];
+    out[0] = (uint32_t)c.bm; out[1] = (uint32_t)c.bn;
+    out[2] = !c.v2 ? 1u : c.wt ? 6u : c.ktail ? 2u : 5u;
+    out[3] = (uint32_t)c.threads; out[4] = c.wt; out[5] = c.reg; out[6] = c.kg2 != nullptr; out[7] = c.ktail;
+    return 0;
 }
 
 // The cost model's plan for 16-byte-aligned operands (what a call would launch before the one-time timing of a

@@ -22,10 +22,10 @@ struct ShState {
     size_t arena_bytes = 0;
     std::vector<void *> mallocs;
     // split-K partial workspaces, one per stream (calls on different streams never share partials); an outgrown
-    // buffer is retired, not freed, because a HIP graph captured earlier may still address it
-    struct Ws { void *p = nullptr; size_t bytes = 0; };
+    // buffer is retired, not freed, because a HIP graph captured earlier may still address it. Everything a stream
+    // holds is freed by sh_stream_release.
+    struct Ws { void *p = nullptr; size_t bytes = 0; std::vector<void *> retired; };
     std::map<hipStream_t, Ws> ws;
-    std::vector<void *> ws_retired;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     bool timer_running = false;
     double last_ns = 0.0;
@@ -84,7 +84,7 @@ void *sh_workspace(size_t bytes) {
     if (want < 2 * w.bytes) want = 2 * w.bytes;
     void *p = nullptr;
     if (!sh_hip_ok(hipMalloc(&p, want), "workspace hipMalloc")) return nullptr;
-    if (w.p) g.ws_retired.push_back(w.p);
+    if (w.p) w.retired.push_back(w.p);
     w.p = p;
     w.bytes = want;
     return w.p;
@@ -103,6 +103,26 @@ void sh_init(void) {
     if (hipDeviceGetAttribute(&v, hipDeviceAttributeNumberOfXccs, g.device) == hipSuccess && v > 0) g.xcds = v;
     sh_hip_ok(hipEventCreate(&g.ev0), "hipEventCreate");
     sh_hip_ok(hipEventCreate(&g.ev1), "hipEventCreate");
+}
+
+int sh_stream_release(uint64_t stream) {
+    sh_ensure_init();
+    const hipStream_t st = (hipStream_t)stream;
+    auto it = g.ws.find(st);
+    if (it == g.ws.end()) return 0;
+    if (!sh_hip_ok(hipStreamSynchronize(st), "sh_stream_release hipStreamSynchronize")) return SH_EHIP;
+    int rc = 0;
+    if (it->second.p && !sh_hip_ok(hipFree(it->second.p), "sh_stream_release hipFree")) rc = SH_EHIP;
+    for (void *p : it->second.retired)
+        if (!sh_hip_ok(hipFree(p), "sh_stream_release hipFree")) rc = SH_EHIP;
+    g.ws.erase(it);
+    return rc;
+}
+
+uint64_t sh_stream_workspace_bytes(uint64_t stream) {
+    auto it = g.ws.find((hipStream_t)stream);
+    if (it == g.ws.end()) return 0;
+    return it->second.bytes;
 }
 
 void sh_barrier_global(void) { sh_ensure_init(); sh_hip_ok(hipStreamSynchronize(g.stream), "sh_barrier_global"); }

@@ -73,6 +73,7 @@ _SIGS: dict[str, tuple] = {
     "sh_gemm_ex": (i32, [u64, u64, u64, u32, u32, u32, u32, u32, u32, C.POINTER(sh_gemm_cfg), C.POINTER(sh_gemm_epi)]),
     "sh_gemm_ex_wt": (i32, [u64, u64, u64, u32, u32, u32, u32, u32, u32, C.POINTER(sh_gemm_cfg), C.POINTER(sh_gemm_epi)]),
     "sh_gemm_plan": (i32, [u32, u32, u32, u32, C.POINTER(C.c_uint32)]),
+    "sh_gemm_tile_count": (i32, []), "sh_gemm_tile_info": (i32, [u32, C.POINTER(C.c_uint32)]),
     # row ops
     "sh_layernorm": (None, [u64, u64, u64, u64, u32, u32, u32, f32, u32]),
     "sh_layernorm_ld": (None, [u64, u64, u64, u64, u32, u32, u32, u32, f32]),
@@ -103,6 +104,7 @@ _SIGS: dict[str, tuple] = {
     "sh_fp16_to_f32": (f32, [i16]), "sh_f32_to_fp16": (i16, [f32]),
     # additive runtime
     "sh_last_error": (i32, []), "sh_last_error_str": (_P, []), "sh_set_stream": (None, [u64]), "sh_get_stream": (u64, []),
+    "sh_stream_release": (i32, [u64]), "sh_stream_workspace_bytes": (u64, [u64]),
     "sh_timer_last_ns": (C.c_double, []), "sh_capture": (None, [i32]), "sh_captured": (u64, [C.c_void_p, u64]),
 }
 # variadic / function-pointer entry points: bound without a prototype
@@ -152,6 +154,19 @@ def epi(bias: int = 0, bias_fmt: int = SH_BIAS_FP16, act: int = SH_ACT_NONE, res
 def addr(t, elem_offset: int = 0) -> int:
     """Device byte address of a torch tensor's storage start plus `elem_offset` elements (a strided view)."""
     return int(t.data_ptr()) + int(elem_offset) * t.element_size()
+
+
+def tile_table() -> list[dict]:
+    """The GEMM tile table (sh_gemm_tile_info of every entry, in index order)."""
+    lib = load()
+    keys = ("bm", "bn", "family", "threads", "wt", "reg", "kg2", "ktail")
+    rows = []
+    for i in range(lib.sh_gemm_tile_count()):
+        out = (C.c_uint32 * 8)()
+        if lib.sh_gemm_tile_info(i, out) != 0:
+            raise RuntimeError(f"sh_gemm_tile_info({i}) failed")
+        rows.append(dict(zip(keys, (int(v) for v in out))))
+    return rows
 
 
 def last_error() -> tuple[int, str]:

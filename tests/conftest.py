@@ -16,6 +16,16 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 
+# Indices into the GEMM tile table (g_cfgs in sh_gemm.hip), by kernel family; tests/test_abi.py pins each set against
+# sh_gemm_tile_info, so parametrised tests can name them at collection time without the library.
+TILE_CFGS = 35
+REGSTAGED_CFGS = tuple(range(0, 6))            # register-staged k_gemm (any alignment, any K; both W layouts)
+K2_CFGS = tuple(range(6, 14))                  # direct-to-LDS k_gemm2 (also takes a partial last k-slice)
+K5_CFGS = (14, 15, 16, 17, 32, 33, 34)         # direct-to-LDS k_gemm5, register epilogue (fold, row partials)
+WT_CFGS = tuple(range(18, 32))                 # direct-to-LDS k_gemm6, W^T operand
+KG2_CFGS = (16, 32)                            # k_gemm5 tiles with the in-workgroup split of two K ranges
+
+
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU; calls libshops.so on cuda:0")
 

@@ -169,6 +169,24 @@ def test_gemm_tile_plan_without_gpu(lib):
     assert lib.sh_gemm_plan(0, 8, 8, 0, out) == -1
 
 
+def test_gemm_tile_table_families(lib):
+    """The tile-table index sets the GPU tests name (tests/conftest.py) are the library's families: register-staged
+    (1), direct-to-LDS with the partial-slice variant (2), register epilogue (5), W^T operand (6), and the tiles with
+    the in-workgroup split of two K ranges; out of range is -1."""
+    from conftest import K2_CFGS, K5_CFGS, KG2_CFGS, REGSTAGED_CFGS, TILE_CFGS, WT_CFGS
+    t = shops.tile_table()
+    assert len(t) == TILE_CFGS == lib.sh_gemm_tile_count()
+    fam = lambda f: tuple(i for i, r in enumerate(t) if r["family"] == f)   # noqa: E731
+    assert (fam(1), fam(2), fam(5), fam(6)) == (REGSTAGED_CFGS, K2_CFGS, K5_CFGS, WT_CFGS)
+    assert tuple(i for i, r in enumerate(t) if r["kg2"]) == KG2_CFGS
+    assert all(t[i]["reg"] for i in K5_CFGS) and all(t[i]["ktail"] for i in K2_CFGS)
+    assert all(r["wt"] == (i in WT_CFGS) for i, r in enumerate(t))
+    assert all(r["bm"] % 64 == 0 and r["bn"] % 64 == 0 and r["threads"] in (256, 512, 768) for r in t)
+    out = (C.c_uint32 * 8)()
+    assert lib.sh_gemm_tile_info(TILE_CFGS, out) == -1
+    assert lib.sh_gemm_tile_info(0, None) == -1
+
+
 def test_gemm_plan_reports_the_launched_split_count(lib):
     """sh_gemm_plan reports the split count the launch runs: each K range is a whole number of 64-k slices
     (kps = 64 ceil(ceil(K / s) / 64)) and no trailing range is empty, so a request for more splits than K has

@@ -116,23 +116,27 @@ def test_scale_edge_cases(lib, gpu, scale):
     assert bad == 0, err
 
 
+@pytest.mark.parametrize("first", [-30.0, -200.0])
 @pytest.mark.parametrize("S", [256, 230])
-def test_running_reference_moves(lib, gpu, S):
+def test_running_reference_moves(lib, gpu, S, first):
     """Scores laid out so the one-pass kernel's reference m moves in every way it can: the first key block's scaled
-    scores sit near -30 (m moves down from 0), the second near -10 and the third near +5 (m moves up by more than 8
-    after the first block), the last near 0 (no move; with S = 230 a partial block). Every query sees the same
-    score pattern (q rows of ones), the keys add a little noise, V is random."""
+    scores sit near `first` (m moves down from 0; at -200, 2^200 would overflow fp32 if the still-empty O and l were
+    rescaled), the second near -10 and the third near +5 (m moves up by more than 8 after the first block), the last
+    near 0 (no move; with S = 230 a partial block). Every query sees the same score pattern (q rows of ones), the keys
+    add a little noise, V is random."""
     dh, scale = 64, 0.125
     c = scale * np.log2(np.e)
     rng = np.random.default_rng(7)
-    level = np.select([np.arange(S) < 64, np.arange(S) < 128, np.arange(S) < 192], [-30.0, -10.0, 5.0], 0.0)
+    level = np.select([np.arange(S) < 64, np.arange(S) < 128, np.arange(S) < 192], [first, -10.0, 5.0], 0.0)
     q = np.ones((S, dh), np.float32)
     k = (level[:, None] / (c * dh) + 0.05 * rng.standard_normal((S, dh))).astype(np.float16).astype(np.float32)
     v = rng.standard_normal((S, dh)).astype(np.float16).astype(np.float32)
     O = _zeros(S, dh)
     assert lib.sh_attention_batched(A(to_dev(q)), A(to_dev(k)), A(to_dev(v)), A(O), 1, S, dh, 1, dh, dh, dh, dh,
                                     0, 0, 0, 0, scale, 0) == 0, shops.last_error()
-    bad, err, _ = refs.close(to_np(O), refs.attention(q, k, v, 1, scale))
+    o = to_np(O)
+    assert np.isfinite(o).all()
+    bad, err, _ = refs.close(o, refs.attention(q, k, v, 1, scale))
     assert bad == 0, err
 
 

@@ -48,6 +48,24 @@ def test_twelve_layer_stack(lib, gpu):
     assert bad == 0, err
 
 
+def test_fused_stack_reference_lcg_layers(lib, gpu):
+    """The fused sequence over four layers with the reference's LCG parameter table, whose seeds move by 100 per
+    layer (siglip.py:110-124): non-trivial gamma / beta and biases reach every folded GEMM, and layers 1-3 take
+    their LayerNorm statistics from the row partials the previous layer's FFN-down wrote. Two sequences (the
+    reference's LCG input and a second one derived from it), every element against the oracle's stack."""
+    S, D, F, H, B = 256, 768, 3072, 12, 2
+    x0 = refs.siglip_input_lcg(S, D)
+    x = np.concatenate([x0, (-x0.astype(np.float32)[::-1]).astype(np.float16)], 0)
+    ps = [refs.siglip_params_lcg(D, F, layer=L) for L in range(4)]
+    enc = encoder.Encoder(D, F, H)
+    out = enc.forward(to_dev(x), [encoder.LayerParams.from_host(p) for p in ps], B=B, S=S, sequence="fused")
+    got = to_np(out)
+    want = refs.encoder_stack(x, ps, H, B=B)
+    bad, err, _ = refs.close(got, want)
+    assert bad == 0, err
+    assert np.isfinite(got).all()
+
+
 def test_baseline_config5_twelve_layer_stack_b32(lib, gpu):
     """BASELINE config 5 as configured: the 12-layer stack at B = 32, S = 256 (layer l seeded 100 + l, input
     seed 7: the workload bench.py measures), every element of the last layer's output against the oracle's

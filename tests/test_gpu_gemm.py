@@ -12,12 +12,12 @@ import os
 import numpy as np
 import pytest
 
-from conftest import codes, to_dev, to_np
+from conftest import K2_CFGS, K5_CFGS, KG2_CFGS, REGSTAGED_CFGS, TILE_CFGS, codes, to_dev, to_np
 from oracle import lcg, refs
 from softhier_mlir_amd import data, shops
 
 pytestmark = pytest.mark.gpu
-NUM_TILE_CFGS = 59      # entries of the GEMM tile table (g_cfgs in sh_gemm.hip)
+NUM_TILE_CFGS = TILE_CFGS      # entries of the GEMM tile table (g_cfgs in sh_gemm.hip)
 A = shops.addr
 
 
@@ -105,22 +105,23 @@ def test_unsplit_tile_configs_store_identical_bits(lib, gpu, monkeypatch):
         Z = torch.zeros((M, N), dtype=torch.float16, device="cuda")
         assert lib.sh_gemm_ex(A(X), A(W), A(Z), M, N, K, K, N, N, None, None) == 0, shops.last_error()
         outs.append(to_np(Z).view(np.uint16))
-    # the direct-to-LDS kernels the cost model and the one-time timing choose between (configurations 6-40 and
-    # 55-58: 64-row to 256-row tiles, 64-k and 32-k slices, 4 and 8 wavefronts, LDS-staged or register epilogue)
-    # agree bit for bit; so do the register-staged fallbacks (0-5) among themselves
-    for lo, hi in ((6, NUM_TILE_CFGS), (0, 6)):
-        for i in range(lo, hi):
-            assert (outs[i] == outs[lo]).all(), f"config {i} differs from config {lo}"
-    for i in (0, 6):
+    # the direct-to-LDS kernels the cost model and the one-time timing choose between (k_gemm2 and k_gemm5: 64-row
+    # to 256-row tiles, 64-k and 32-k slices, LDS-staged or register epilogue; a W^T configuration forced on a W
+    # call runs the model's choice) agree bit for bit; so do the register-staged fallbacks among themselves
+    direct = [i for i in range(NUM_TILE_CFGS) if i not in REGSTAGED_CFGS]
+    for group in (direct, list(REGSTAGED_CFGS)):
+        for i in group:
+            assert (outs[i] == outs[group[0]]).all(), f"config {i} differs from config {group[0]}"
+    for i in (REGSTAGED_CFGS[0], direct[0]):
         assert refs.close(outs[i].view(np.float16), refs.gemm(x, w))[0] == 0
 
 
-REG_EPILOGUE_CFGS = (25, 26, 27, 28, 33, 34, 35, 36, 37, 38, 39, 40, 55, 56, 57, 58)   # register-epilogue tiles (W layout)
+REG_EPILOGUE_CFGS = K5_CFGS   # register-epilogue tiles (W layout)
 
 
 @pytest.mark.parametrize("K", [64, 448])
 def test_register_epilogue_configs_with_residual(lib, gpu, K, monkeypatch):
-    """Register-epilogue tiles (configurations 33-40 and 55-58 store each wavefront's block through its own LDS slots as whole
+    """Register-epilogue tiles (k_gemm5: each wavefront stores its block through its own LDS slots as whole
     row segments and add the residual there) on partial tiles in M and N with ldz > N, bias + GELU and
     bias + residual epilogues: bit-identical to configuration 6 (LDS-staged epilogue of the whole tile), rows
     sampled against the oracle, nothing written outside the view. K = 64 is a single slice."""
@@ -225,10 +226,10 @@ EPI_CASES = [(shops.SH_BIAS_FP16, shops.SH_ACT_GELU, True, 0), (shops.SH_BIAS_FP
 @pytest.mark.parametrize("case", range(len(EPI_CASES)))
 def test_epilogue_chain_same_bits_on_every_tile(lib, gpu, monkeypatch, case, splits):
     """Each epilogue combination on partial tiles (M, N not multiples of any tile), on the LDS-staged and the
-    register-epilogue tile configurations (6: k_gemm2; 23, 24: k_gemm4 staged; 25-28: k_gemm4 register epilogue,
-    32- and 64-k slices; 30-32: k_gemm2 64x64, 64x128, 128x64): every configuration stores the same bits (split or
-    not), nothing outside the output view
-    changes, and the result is within tolerance of the oracle's unfused sequence."""
+    register-epilogue tile configurations (k_gemm2 256x256 and its 64x64, 64x128, 128x64 tiles; every k_gemm5
+    tile: register epilogue, 32- and 64-k slices): every configuration stores the same bits (split or not),
+    nothing outside the output view changes, and the result is within tolerance of the oracle's unfused
+    sequence."""
     import torch
     bias_fmt, act, res, accumulate = EPI_CASES[case]
     M, N, K, ldz = 328, 200, 192, 208
@@ -242,7 +243,7 @@ def test_epilogue_chain_same_bits_on_every_tile(lib, gpu, monkeypatch, case, spl
     elif bias_fmt == shops.SH_BIAS_FP16:
         bias = to_dev(b32.astype(np.float16))
     outs = {}
-    for cfg_index in (6, 23, 24, 25, 26, 27, 28, 30, 31, 32):
+    for cfg_index in (K2_CFGS[0],) + K5_CFGS + K2_CFGS[-3:]:
         monkeypatch.setenv("SH_GEMM_CFG", str(cfg_index))
         Z = torch.full((M + 3, ldz), 7.0, dtype=torch.float16, device="cuda")
         Z[:M, :N] = to_dev(z0)
@@ -254,7 +255,7 @@ def test_epilogue_chain_same_bits_on_every_tile(lib, gpu, monkeypatch, case, spl
         assert (z[:M, N:] == 7.0).all() and (z[M:] == 7.0).all(), f"config {cfg_index} wrote outside the view"
         outs[cfg_index] = z[:M, :N].view(np.uint16).copy()
     for cfg_index, o in outs.items():
-        assert (o == outs[6]).all(), f"config {cfg_index} differs from config 6 in {(o != outs[6]).sum()} elements"
+        assert (o == outs[K2_CFGS[0]]).all(), f"config {cfg_index} differs from config {K2_CFGS[0]} in {(o != outs[K2_CFGS[0]]).sum()} elements"
     # the reference's unfused order: Z (+)= XW, + bias, GELU, + residual, each stored in fp16
     want = refs.gemm(x, w, z0 if accumulate else None)
     if bias is not None:
@@ -264,7 +265,7 @@ def test_epilogue_chain_same_bits_on_every_tile(lib, gpu, monkeypatch, case, spl
         want = refs.r16(refs.gelu(want))
     if res:
         want = want + r.astype(np.float32)
-    bad, err, _ = refs.close(outs[6].view(np.float16), want)
+    bad, err, _ = refs.close(outs[K2_CFGS[0]].view(np.float16), want)
     assert bad == 0, err
 
 
@@ -321,6 +322,24 @@ def test_splitk_on_two_streams_keeps_partials_apart(lib, gpu):
             assert np.array_equal(codes(outs[si][rep]), alone[si]), (si, rep)
         bad, err, _ = refs.close(to_np(outs[si][0]), refs.gemm(*ins[si]))
         assert bad == 0, err
+    # each stream holds its own workspace until sh_stream_release frees it; a later call on it allocates again
+    for st in streams:
+        assert lib.sh_stream_workspace_bytes(st.cuda_stream) >= 64 << 20
+    free0 = torch.cuda.mem_get_info()[0]
+    for st in streams:
+        assert lib.sh_stream_release(st.cuda_stream) == 0, shops.last_error()
+        assert lib.sh_stream_workspace_bytes(st.cuda_stream) == 0
+    assert torch.cuda.mem_get_info()[0] >= free0 + (100 << 20)               # two 64 MiB workspaces returned
+    assert lib.sh_stream_release(streams[0].cuda_stream) == 0                # nothing held: nothing to do
+    (M, N, K, s), (X, W) = shapes[0], dev[0]
+    Z = torch.zeros((M, N), dtype=torch.float16, device="cuda")
+    try:
+        lib.sh_set_stream(streams[0].cuda_stream)
+        assert lib.sh_gemm_splitk(A(X), A(W), A(Z), M, N, K, K, N, N, None, s, shops.SH_ALL) == 0, shops.last_error()
+    finally:
+        lib.sh_set_stream(prev)
+    torch.cuda.synchronize()
+    assert np.array_equal(codes(Z), alone[0])
 
 _ORDER_CHILD = r"""
 import os, sys
@@ -352,7 +371,7 @@ def test_tile_order_bands_store_identical_bits(lib, gpu, tmp_path):
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     outs = {}
     for band in (1, 3, 8):
-        env = dict(os.environ, SH_GEMM_GROUP=str(band), SH_GEMM_CFG="55", PYTHONPATH=root)
+        env = dict(os.environ, SH_GEMM_GROUP=str(band), SH_GEMM_CFG=str(KG2_CFGS[1]), PYTHONPATH=root)
         f = tmp_path / f"z{band}.npy"
         rc = subprocess.run([sys.executable, "-c", _ORDER_CHILD, str(f)], env=env, cwd=root, timeout=110,
                             capture_output=True, text=True)
@@ -361,7 +380,6 @@ def test_tile_order_bands_store_identical_bits(lib, gpu, tmp_path):
     assert np.array_equal(outs[1], outs[3]) and np.array_equal(outs[1], outs[8])
 
 
-KG2_CFGS = (38, 55)      # tiles with the in-workgroup split-K variant (k_gemm5 KG = 2)
 
 
 @pytest.mark.parametrize("M,N,K", [(1000, 760, 768), (520, 768, 3072), (8192, 768, 3072), (300, 256, 128)])
@@ -595,7 +613,7 @@ def test_xmcast_small_m_shapes(lib, gpu, M, N, K, mode, tm, acc):
 @pytest.mark.parametrize("splits", [1, 3])
 def test_k_tail_on_direct_to_lds_tiles(lib, gpu, monkeypatch, K, splits):
     """K % 64 != 0 with vector operands (K % 8 == 0) on the direct-to-LDS k_gemm2 tiles: the last, partial 64-k
-    slice reads zeros past K, so every k_gemm2 tile (128x128 to 128x256, 64x64 to 128x64; 2 or 3 stages) stores
+    slice reads zeros past K, so every k_gemm2 tile (128x128 to 256x256, 64x64 to 128x64; 2 or 3 stages) stores
     the same bits, within tolerance of the oracle, with a bias + GELU epilogue, and nothing outside the view
     changes. K = 8 is a single partial slice; K = 720 is the SmolVLA width (11 slices + 16)."""
     import torch
@@ -604,7 +622,7 @@ def test_k_tail_on_direct_to_lds_tiles(lib, gpu, monkeypatch, K, splits):
     b = data.normal((1, N), 93, std=0.3).astype(np.float16)
     X, W, Bb = to_dev(x), to_dev(w), to_dev(b)
     outs = {}
-    for cfg_index in (6, 7, 8, 9, 10, 11, 12, 29, 30, 31, 32):
+    for cfg_index in K2_CFGS:
         monkeypatch.setenv("SH_GEMM_CFG", str(cfg_index))
         Z = torch.full((M + 2, ldz), 7.0, dtype=torch.float16, device="cuda")
         e = shops.epi(bias=A(Bb), act=shops.SH_ACT_GELU, splits=splits)
@@ -612,9 +630,9 @@ def test_k_tail_on_direct_to_lds_tiles(lib, gpu, monkeypatch, K, splits):
         z = to_np(Z)
         assert (z[:M, N:] == 7.0).all() and (z[M:] == 7.0).all(), cfg_index
         outs[cfg_index] = z[:M, :N].copy()
-    ref = outs[6]
+    ref = outs[K2_CFGS[0]]
     for i, z in outs.items():
-        assert np.array_equal(z.view(np.uint16), ref.view(np.uint16)), f"config {i} differs from config 6"
+        assert np.array_equal(z.view(np.uint16), ref.view(np.uint16)), f"config {i} differs from config {K2_CFGS[0]}"
     want = refs.gelu(refs.r16(refs.r16(refs.gemm(x, w)) + b.astype(np.float32)))
     bad, err, _ = refs.close(ref, want)
     assert bad == 0, err

@@ -7,14 +7,13 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import codes, to_dev, to_np
+from conftest import K2_CFGS, REGSTAGED_CFGS, WT_CFGS, codes, to_dev, to_np
 from oracle import refs
 from softhier_mlir_amd import data, shops
 
 pytestmark = pytest.mark.gpu
 A = shops.addr
-WT_CFGS = range(41, 55)          # the W^T tile configurations of the table (k_gemm6)
-FALLBACK_CFGS = range(0, 6)      # register-staged tiles (both layouts)
+FALLBACK_CFGS = REGSTAGED_CFGS   # register-staged tiles (both layouts)
 
 
 def _wt(w):
@@ -32,9 +31,9 @@ def test_wt_config_matches_natural_layout_bitwise(lib, gpu, cfg_index, monkeypat
     x = data.normal((M, K), 31)
     w = data.normal((K, N), 32, std=1 / np.sqrt(K))
     X, W, WT = to_dev(x), to_dev(w), _wt(w)
-    ref_cfg = 6 if cfg_index >= 6 else cfg_index
+    ref_cfg = cfg_index if cfg_index in FALLBACK_CFGS else K2_CFGS[0]
     monkeypatch.setenv("SH_GEMM_CFG", str(ref_cfg))
-    if cfg_index < 6:
+    if cfg_index in FALLBACK_CFGS:
         K = 136                                   # K % 64 != 0: W^T calls take the register-staged tiles
         x, w = x[:, :K], w[:K]
         X, W, WT = to_dev(x), to_dev(w), _wt(w)

@@ -12,13 +12,13 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import codes, to_dev, to_np
+from conftest import K2_CFGS, K5_CFGS, codes, to_dev, to_np
 from oracle import refs
 from softhier_mlir_amd import data, shops
 
 pytestmark = pytest.mark.gpu
 A = shops.addr
-REG_CFGS = list(range(25, 29)) + list(range(33, 41)) + [55, 56, 57, 58]   # W layout tiles with the fold in registers
+REG_CFGS = list(K5_CFGS)      # W layout tiles with the fold in registers
 EPS = 1e-6
 
 
@@ -169,7 +169,7 @@ def test_fold_configs_and_partials_path_store_identical_bits(lib, gpu, act, monk
     C1 = _empty32(N + 1)                        # c one element into its buffer: 4-byte, not 16-byte aligned
     C1[1:N + 1] = C[:N]
     runs = {}
-    for cfg in REG_CFGS + ["partials6", "partials22", "partials33"]:
+    for cfg in REG_CFGS + [f"partials{K2_CFGS[0]}", f"partials{K2_CFGS[3]}", f"partials{K5_CFGS[0]}"]:
         Z = torch.full((M, N), 3.0, dtype=torch.float16, device="cuda")
         if str(cfg).startswith("partials"):
             monkeypatch.setenv("SH_GEMM_CFG", cfg[8:])
@@ -303,6 +303,18 @@ def test_fold_from_row_partials(lib, gpu, mean, act):
     assert bad == 0, err
     bad, err, _ = refs.close(to_np(Z), to_np(Z2), atol=2e-3, rtol=2e-3)
     assert bad == 0, err
+    # the same partials 8 bytes into a buffer (8-byte, not 16-byte aligned): read 8 bytes at a time, the same bits
+    Pst8 = _empty32(M * (D // 32) * 2 + 2)
+    Pst8[2:].copy_(Pst.reshape(-1))
+    assert (A(Pst8) + 8) % 16 == 8
+    Z8 = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    e8 = shops.epi(bias=A(Dd), bias_fmt=shops.SH_BIAS_FP32, act=act, ln_stats=A(Pst8) + 8, ln_c=A(C),
+                   ln_parts=D // 32, ln_eps=EPS)
+    assert lib.sh_gemm_ex(A(H), A(WP), A(Z8), M, N, D, D, N, N, None, e8) == 0, shops.last_error()
+    assert np.array_equal(codes(Z8), codes(Z))
+    e4 = shops.epi(bias=A(Dd), bias_fmt=shops.SH_BIAS_FP32, act=act, ln_stats=A(Pst8) + 4, ln_c=A(C),
+                   ln_parts=D // 32, ln_eps=EPS)
+    assert lib.sh_gemm_ex(A(H), A(WP), A(Z8), M, N, D, D, N, N, None, e4) == -1          # 4-byte aligned: refused
 
 
 def test_row_partials_argument_errors(lib, gpu):

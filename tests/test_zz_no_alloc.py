@@ -38,17 +38,20 @@ def test_noalloc_splitk_matches_splitk_on_two_calls(lib, gpu):
         assert bad == 0, err
 
 
-def test_noalloc_splitk_refuses_partials_beyond_its_scratch(lib, gpu):
+def test_noalloc_splitk_scratch_boundary(lib, gpu):
+    """The 16 MiB limit applies to launches that write fp32 partials: 4 K ranges of a 1024 x 1024 output need exactly
+    16 MiB and run (the bits of sh_gemm_splitk); 8 ranges need 32 MiB and are refused before any GPU work; two equal
+    K ranges run in one workgroup and write no partials, so a 1024 x 4096 output (32 MiB as partials) runs too."""
     import torch
-    M, N, K = 1024, 2048, 1024
-    X = torch.zeros((M, K), dtype=torch.float16, device="cuda")
-    W = torch.zeros((K, N), dtype=torch.float16, device="cuda")
-    Z = torch.full((M, N), 3.0, dtype=torch.float16, device="cuda")
-    # 4 x 1024 x 2048 x 4 B = 32 MiB of partials > 16 MiB
-    assert lib.sh_gemm_splitk_noalloc(A(X), A(W), A(Z), M, N, K, K, N, N, None, 4, shops.SH_ALL) == -1
+    x, w, Zr, Zn = _pair(lib, 1024, 1024, 1024, 4, 311)
+    assert np.array_equal(codes(Zn), codes(Zr))
+    assert refs.close(to_np(Zn), refs.gemm(x, w))[0] == 0
+    X, W = to_dev(x), to_dev(w)
+    Z = torch.full((1024, 1024), 3.0, dtype=torch.float16, device="cuda")
+    assert lib.sh_gemm_splitk_noalloc(A(X), A(W), A(Z), 1024, 1024, 1024, 1024, 1024, 1024, None, 8, shops.SH_ALL) == -1
     assert shops.last_error()[0] == -1
     torch.cuda.synchronize()
     assert (to_np(Z) == 3.0).all()                           # nothing ran
-    # 2 splits: 16 MiB exactly fits
-    assert lib.sh_gemm_splitk_noalloc(A(X), A(W), A(Z), M, N, K, K, N, N, None, 2, shops.SH_ALL) == 0, shops.last_error()
-    assert (to_np(Z) == 0.0).all()
+    x, w, Zr, Zn = _pair(lib, 1024, 4096, 1024, 2, 313)
+    assert np.array_equal(codes(Zn), codes(Zr))
+    assert refs.close(to_np(Zn), refs.gemm(x, w))[0] == 0
