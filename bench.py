@@ -174,7 +174,8 @@ def stack12(torch, enc, x, B: int, S: int, D: int, F: int, reps: int = 5, warmup
     """The 12-layer stack (layer l reads layer l-1's output, weights of layer l seeded 100 + l):
     `reps` forwards timed on the host clock between synchronisations, then one forward with HIP events around every
     layer (the first layer also computes its input's row statistics; the others read the row partials the layer
-    before wrote)."""
+    before wrote). As in Encoder.forward, each layer's later weights and the next layer's QKV weight are read into
+    the caches on a second stream while its attention runs (`enc.prefetch = False`: not)."""
     from softhier_mlir_amd import data, encoder
     layers = [encoder.LayerParams.from_host(data.encoder_params(D, F, seed=100 + l)) for l in range(12)]
     y = torch.empty_like(x)
@@ -193,7 +194,8 @@ def stack12(torch, enc, x, B: int, S: int, D: int, F: int, reps: int = 5, warmup
     ev[0].record()
     for i, lp in enumerate(layers):
         dst = y if (11 - i) % 2 == 0 else tmp
-        enc.layer_fused(cur, dst, lp, B, S, x_parts=i > 0)
+        pre = enc.prefetch_ranges(lp, layers[i + 1] if i < 11 else None) if enc.prefetch else None
+        enc.layer_fused(cur, dst, lp, B, S, x_parts=i > 0, prefetch=pre)
         ev[i + 1].record()
         cur = dst
     torch.cuda.synchronize()

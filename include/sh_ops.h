@@ -123,6 +123,11 @@ void sh_ln_fold(uint64_t wp, uint64_t c, uint64_t d, uint64_t w, uint64_t gamma,
 /* sh_ops.h:218 (sh_l1.inc.c:58-61): 1-D copy of `bytes` from src to dst in HBM (non-overlapping), enqueued on the
  * library stream (the reference's call is synchronous on its DM core; here it is ordered like every other op). */
 void sh_dma_copy(uint64_t dst, uint64_t src, uint32_t bytes);
+/* No counterpart in the reference: read [addr, addr + bytes) through the GPU's caches (L2 and the 256 MB Infinity
+ * Cache) on the library stream, writing nothing, so that a kernel launched later finds those bytes cached instead of
+ * in HBM. For callers that know which weights come next: the encoder stack issues it on a second stream for a
+ * layer's remaining weights while its attention runs. 0, -1 for a NULL address, SH_EHIP for a launch failure. */
+int sh_prefetch(uint64_t addr, uint64_t bytes);
 
 /* ---- fused attention (sh_ops.h:102-127, runtime/sh_attention.inc.c:55-243) ----------------------------
  * o = softmax(scale * q k^T) v per head; head h = columns [h*dh, (h+1)*dh). Flash-style on the GPU (online

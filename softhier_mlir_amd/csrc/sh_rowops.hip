@@ -798,6 +798,15 @@ __global__ __launch_bounds__(256) void k_pixel_shuffle1(uint16_t *dst, const uin
 }
 }  // namespace
 
+// One load of every 64-byte line of [base, base + 64 lines): the lines come into L2 and the Infinity Cache for the
+// kernels that read them next, and nothing is written (the empty asm keeps each load, and the wave waits for it).
+__global__ __launch_bounds__(256) void k_prefetch(const uint8_t *__restrict__ base, uint64_t lines) {
+    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < lines; i += (uint64_t)gridDim.x * 256u) {
+        const uint32_t v = *(const uint32_t *)(base + i * 64);
+        asm volatile("" ::"v"(v));
+    }
+}
+
 extern "C" {
 
 void sh_layernorm(uint64_t y, uint64_t x, uint64_t gamma, uint64_t beta, uint32_t rows, uint32_t cols, uint32_t ld, float eps, uint32_t) {
@@ -865,6 +874,17 @@ void sh_dma_copy(uint64_t dst, uint64_t src, uint32_t bytes) {
         hipLaunchKernelGGL(k_copy1, dim3(blocks), dim3(256), 0, st, (uint8_t *)dst, (const uint8_t *)src, (uint64_t)bytes);
     }
     sh_launch_ok("sh_dma_copy");
+}
+
+int sh_prefetch(uint64_t addr, uint64_t bytes) {
+    if (bytes == 0) return 0;
+    if (!addr) { sh_set_error(-1, "[sh_prefetch] NULL address"); return -1; }
+    sh_ensure_init();
+    // whole 64-byte lines: the first and last may reach outside the range, but never outside its pages
+    const uint64_t base = addr & ~uint64_t(63), lines = (addr + bytes - base + 63) / 64;
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((lines + 255) / 256, 8192);
+    hipLaunchKernelGGL(k_prefetch, dim3(blocks), dim3(256), 0, sh_stream(), (const uint8_t *)base, lines);
+    return sh_launch_ok("sh_prefetch") ? 0 : SH_EHIP;
 }
 
 void sh_softmax_rows(uint64_t y, uint64_t x, uint32_t rows, uint32_t cols, uint32_t ld, float scale, uint32_t) {

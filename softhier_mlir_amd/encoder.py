@@ -87,6 +87,8 @@ class Encoder:
         self.gemm_cfg = shops.cfg()          # tile hints 256^3 (library default), as the reference's default policy
         self.row_partials = True             # False: sh_row_stats before each folded GEMM (seven launches a layer)
         self.tap = None                      # optional tap(name) -> context manager around each op (timing)
+        self.prefetch = True                 # stacks: a layer's later weights pulled into the caches during attention
+        self._side: torch.cuda.Stream | None = None
 
     def _op(self, name: str):
         return self.tap(name) if self.tap is not None else contextlib.nullcontext()
@@ -186,15 +188,43 @@ class Encoder:
         return calls
 
     def layer_fused(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int,
-                    x_parts: bool = False) -> torch.Tensor:
+                    x_parts: bool = False, prefetch: list | None = None) -> torch.Tensor:
         """One fused layer. x_parts=True: x was stored by the previous layer's FFN-down, whose row partials are in
-        the encoder's `pst_x` buffer (the layer then skips sh_row_stats); the layer leaves out's in it."""
+        the encoder's `pst_x` buffer (the layer then skips sh_row_stats); the layer leaves out's in it.
+        prefetch: (address, bytes) ranges read into the caches on a second stream once the QKV GEMM is done."""
         for name, fn, args, what in self._fused_plan(x, out, p, B, S, x_parts):
             with self._op(name):
                 rc = fn(*args)
             if what is not None:
                 _check(rc, what)
+            if name == "qkv" and prefetch:
+                self._prefetch(prefetch)
         return out
+
+    def _prefetch(self, ranges: list) -> None:
+        """sh_prefetch of `ranges` on the encoder's second stream (default priority), ordered after the work enqueued
+        so far on the library stream: the reads run beside the next kernel (attention, which leaves room on every CU)
+        and only bring weights into L2 and the Infinity Cache, so nothing waits for them."""
+        main = torch.cuda.current_stream()
+        if self._side is None:
+            self._side = torch.cuda.Stream()
+        ev = torch.cuda.Event()
+        ev.record(main)
+        self._side.wait_event(ev)
+        prev = self.lib.sh_get_stream()
+        self.lib.sh_set_stream(self._side.cuda_stream)
+        try:
+            for a, n in ranges:
+                _check(self.lib.sh_prefetch(a, n), "sh_prefetch")
+        finally:
+            self.lib.sh_set_stream(prev)
+
+    @staticmethod
+    def prefetch_ranges(p: LayerParams, nxt: "LayerParams | None") -> list:
+        """The weights a fused layer reads after its QKV GEMM (out-proj W, folded FFN-up W', FFN-down W) and the next
+        layer's folded QKV W', as (address, bytes)."""
+        ts = [p["wo"], p["w1_ln"], p["w2"]] + ([nxt["wqkv_ln"]] if nxt is not None else [])
+        return [(shops.addr(t), t.numel() * t.element_size()) for t in ts]
 
     def capture(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int) -> "CapturedLayer":
         """Record one fused layer into a HIP graph (replay with `.replay()` on any stream). The layer runs once
@@ -248,14 +278,24 @@ class Encoder:
             if tmp is None or tmp.shape != x.shape or tmp.dtype != x.dtype or tmp.device != x.device:
                 tmp = torch.empty_like(x)
                 self._pingpong = tmp
+        # a stack's weights do not all fit in the Infinity Cache next to its activations: each layer's later weights
+        # and the next layer's QKV weight are read into the caches during its attention (eager library stream only)
+        pre = (sequence == "fused" and n > 1 and self.prefetch and not torch.cuda.is_current_stream_capturing()
+               and self.lib.sh_get_stream() == torch.cuda.current_stream().cuda_stream)
+        if pre:
+            for p in params:
+                p.fold(self.lib)
         cur = x
         for i, p in enumerate(params):          # ping-pong so that the last layer writes `out`
             dst = out if (n - 1 - i) % 2 == 0 else tmp
             if sequence == "fused":
-                step(cur, dst, p, B, S, x_parts=i > 0)   # layer i > 0 reads the partials layer i - 1 wrote
+                rng = self.prefetch_ranges(p, params[i + 1] if i + 1 < n else None) if pre else None
+                step(cur, dst, p, B, S, x_parts=i > 0, prefetch=rng)   # layer i > 0 reads the partials of layer i - 1
             else:
                 step(cur, dst, p, B, S)
             cur = dst
+        if pre and self._side is not None:      # later work on the library stream is ordered after the reads
+            torch.cuda.current_stream().wait_stream(self._side)
         return out
 
 

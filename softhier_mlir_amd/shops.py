@@ -65,7 +65,7 @@ _SIGS: dict[str, tuple] = {
     "sh_attention_head_masked": (i32, [u64, u64, u64, u64, u32, u32, u32, u32, u32, u32, f32, u64, u32]),
     "sh_attention_gqa": (i32, [u64, u64, u64, u64, u32, u32, u32, u32, u32, u32, u32, u32, f32, u64, u32]),
     "sh_pixel_shuffle": (None, [u64, u64, u32, u32, u32, u32]),
-    "sh_dma_copy": (None, [u64, u64, u32]),
+    "sh_dma_copy": (None, [u64, u64, u32]), "sh_prefetch": (i32, [u64, u64]),
     "sh_row_stats": (None, [u64, u64, u32, u32, u32, f32]),
     "sh_ln_fold": (None, [u64, u64, u64, u64, u64, u64, u64, u32, u32, u32, u32]),
     "sh_gemm_splitk": (i32, [u64, u64, u64, u32, u32, u32, u32, u32, u32, C.POINTER(sh_gemm_cfg), u32, u32]),

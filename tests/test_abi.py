@@ -211,6 +211,12 @@ def test_gemm_plan_reports_the_launched_split_count(lib):
             assert plan(256, 768, K, s) == launched(K, s), (K, s)
 
 
+def test_prefetch_argument_errors_without_gpu(lib):
+    assert lib.sh_prefetch(0, 64) == -1
+    assert shops.last_error()[0] == -1
+    assert lib.sh_prefetch(0, 0) == 0                    # an empty range is nothing to do, whatever its address
+
+
 def test_dma_copy_argument_errors_without_gpu(lib):
     lib.sh_last_error()
     lib.sh_dma_copy(0, 1 << 20, 64)                    # NULL destination: refused before any HIP call

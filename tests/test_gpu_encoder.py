@@ -66,6 +66,25 @@ def test_fused_stack_reference_lcg_layers(lib, gpu):
     assert np.isfinite(got).all()
 
 
+def test_stack_prefetch_changes_no_bits(lib, gpu):
+    """The stack with its weight prefetch (sh_prefetch on a second stream during each attention) stores exactly the
+    bits of the stack without it: the prefetch only reads."""
+    import torch
+    B, S, D, F, H = 2, 256, 768, 3072, 12
+    ps = [encoder.LayerParams.from_host(data.encoder_params(D, F, seed=300 + i)) for i in range(4)]
+    x = to_dev(data.normal((B * S, D), 9))
+    outs = []
+    for pre in (True, False):
+        enc = encoder.Encoder(D, F, H)
+        enc.prefetch = pre
+        outs.append(enc.forward(x, ps, B=B, S=S, sequence="fused").clone())
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    bad, err, _ = refs.close(to_np(outs[0]), refs.encoder_stack(data.normal((B * S, D), 9),
+                                                                [{k: v.cpu().numpy() for k, v in p.t.items()} for p in ps], H, B=B))
+    assert bad == 0, err
+
+
 def test_baseline_config5_twelve_layer_stack_b32(lib, gpu):
     """BASELINE config 5 as configured: the 12-layer stack at B = 32, S = 256 (layer l seeded 100 + l, input
     seed 7: the workload bench.py measures), every element of the last layer's output against the oracle's

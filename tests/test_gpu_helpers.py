@@ -72,3 +72,17 @@ def test_timer_arena_and_cycles(lib, gpu):
     c0 = lib.sh_cycles()
     c1 = lib.sh_cycles()
     assert (c1 - c0) % 2 ** 32 < 10 ** 9
+
+
+def test_prefetch_reads_ranges_and_writes_nothing(lib, gpu):
+    """sh_prefetch on ranges that start and end inside 64-byte lines (and a whole buffer) returns 0 and leaves every
+    byte as it was; an empty range does nothing."""
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(3)
+    t = torch.randint(-30000, 30000, (1 << 20,), dtype=torch.int16, device="cuda", generator=g)
+    before = t.clone()
+    for off, n in ((0, 2 << 20), (6, 1000), (130, 64 * 1001 + 5), ((1 << 20) - 7, 14)):
+        assert lib.sh_prefetch(A(t) + off, n) == 0, shops.last_error()
+    assert lib.sh_prefetch(A(t), 0) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(t, before)
