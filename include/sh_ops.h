@@ -291,6 +291,17 @@ int sh_gemm_tile_info(uint32_t i, uint32_t *out);
 int sh_attention_batched(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, uint32_t D, uint32_t H,
                          uint32_t ldq, uint32_t ldk, uint32_t ldv, uint32_t ldo,
                          uint64_t bsq, uint64_t bsk, uint64_t bsv, uint64_t bso, float scale, uint32_t sq);
+/* No counterpart in the reference: sh_attention_batched that also reads two ranges [pfN, pfN + pfN_bytes) (bytes 0:
+ * none) into the GPU's caches (L2 and the Infinity Cache) while it runs, writing nothing there: the same outputs, bit
+ * for bit. For callers that know which weights the next kernels read (the encoder stack: a layer's out-proj and FFN
+ * weights and the next layer's QKV weight, which do not all stay in the cache next to the activations); attention
+ * leaves memory bandwidth and room on every CU, so the reads cost it little and no second stream or event is
+ * needed. A head the one-pass kernel does not take reads the ranges after its kernel instead (sh_prefetch). -1 also
+ * for a NULL range with bytes > 0. */
+int sh_attention_batched_prefetch(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, uint32_t D, uint32_t H,
+                                  uint32_t ldq, uint32_t ldk, uint32_t ldv, uint32_t ldo,
+                                  uint64_t bsq, uint64_t bsk, uint64_t bsv, uint64_t bso, float scale, uint32_t sq,
+                                  uint64_t pf0, uint64_t pf0_bytes, uint64_t pf1, uint64_t pf1_bytes);
 
 /* LayerNorm with separate input / output leading dims (fused residual stream layouts). */
 void sh_layernorm_ld(uint64_t y, uint64_t x, uint64_t gamma, uint64_t beta, uint32_t rows, uint32_t cols,

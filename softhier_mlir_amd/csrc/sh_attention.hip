@@ -38,6 +38,10 @@ struct AttnArgs {
     const uint16_t *tok;            // token classes of the S positions (sh_ops.h:277-282), or null: no mask
     uint32_t grp;                   // query heads per key/value head (GQA); 1 for plain multi-head attention
     uint32_t xcds;                  // > 1: the query blocks of one head run on one XCD (see attn_item)
+    // sh_attention_batched_prefetch: two ranges of 64-byte lines (line-aligned bases, line counts) that k_flash3
+    // reads into the caches while it runs; zero counts: none
+    const uint8_t *pf0, *pf1;
+    uint32_t pfl0, pfl1;
 };
 
 // Work item of a workgroup: (query block, head, sequence). Dispatch deals workgroups round-robin over the XCDs,
@@ -529,7 +533,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a, ui
 // this drops the maximum pass (its score MFMAs, K fragment reads and K DMAs) and the refill of the ring between the
 // passes. Same LDS ring, fragment prefetch and occupancy as k_flash2.
 constexpr float kTau = 8.f;
-template <int DH, int NST>
+template <int DH, int NST, bool PF = false>
 __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, uint64_t *stamp) {
     constexpr int DC = DH / 8, NS = DH / 16, DT = DH / 32;
     constexpr int KCH = KB * DC;                     // 16-byte chunks per K (or V) block
@@ -537,6 +541,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
     constexpr uint32_t STAGE = 2u * KCH * 16u;       // K block then V block
     static_assert(KCH % 256 == 0 && NST == 2, "attention tiling (the key-block loop is unrolled by the two stages)");
     __shared__ uint4 smem[NST * 2 * KCH];
+    __shared__ uint4 pf_sink[PF ? 64 : 1];           // destination of the prefetch DMAs (never read)
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = lane >> 5, r32 = lane & 31;
     const int q4 = lane >> 4, iq = lane & 15;
@@ -587,6 +592,22 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
                 sh_lds_dma16_s(kbase, koff[r] - over * (uint32_t)a.ldk * 2, st + r * 4096 + wave_off);
                 sh_lds_dma16_s(vbase, voff[r] - over * (uint32_t)a.ldv * 2, st + KCH * 16 + r * 4096 + wave_off);
             }
+        }
+    };
+    // The caller's prefetch ranges (sh_attention_batched_prefetch): one 16-byte DMA per 64-byte line into the sink,
+    // a quarter of the lines with each of the first four key blocks, right after that block's next-block DMA, so
+    // the reads overlap the blocks' compute and the next block's wait (vmcnt 0) retires them; nothing is read back.
+    // (PF: a separate build, so the kernel without ranges keeps its registers)
+    const uint32_t pfl = PF ? a.pfl0 + a.pfl1 : 0u, pq = min(nkb, 4u), pfq = (pfl + pq - 1) / pq;
+    const uint64_t gthreads = (uint64_t)gridDim.x * gridDim.y * gridDim.z * 256u;
+    const uint64_t gid = (((uint64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * 256u + t;
+    const uint32_t sink = sh_lds_addr(pf_sink);
+    auto prefetch_part = [&](uint32_t kb) {
+        if (!PF || pfl == 0 || kb >= pq) return;
+        const uint64_t end = min(pfl, (kb + 1) * pfq);
+        for (uint64_t j = (uint64_t)kb * pfq + gid; j < end; j += gthreads) {
+            const uint8_t *p = j < a.pfl0 ? a.pf0 + j * 64 : a.pf1 + (j - a.pfl0) * 64;
+            sh_lds_dma16(p, sink);
         }
     };
 #pragma unroll
@@ -667,6 +688,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
         sh_wait_vmcnt<(NST - 2) * 2 * KR>();
         __syncthreads();
         issue(min(kb + NST - 1, nkb - 1), (st + NST - 1) % NST);
+        prefetch_part(kb);
         sh_f16v sacc[2];
         auto mask_tail = [&]() {
             if (ragged && kb == nkb - 1) {
@@ -839,12 +861,22 @@ int check_ref(uint32_t S, uint32_t dh, uint32_t sq) {          // sh_attention.i
 // points); the additive batched entry launches without them (no profiling work on the batched hot path).
 int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, uint32_t dh, uint32_t H,
         uint32_t ldq, uint32_t ldk, uint32_t ldv, uint32_t ldo, uint64_t bsq, uint64_t bsk, uint64_t bsv, uint64_t bso, float scale,
-        uint64_t tok = 0, uint32_t grp = 1, bool stamp = true) {
+        uint64_t tok = 0, uint32_t grp = 1, bool stamp = true, const uint64_t *pf = nullptr) {
     if (!q || !k || !v || !o) { sh_set_error(-1, "[sh_attention] NULL tensor address"); return -1; }
     if (B == 0 || S == 0 || H == 0 || dh == 0) return 0;
     if (H > 65535 || B > 65535) { sh_set_error(-1, "[sh_attention] H=%u or B=%u above 65535", H, B); return -1; }
     AttnArgs a{(const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)v, (uint16_t *)o,
                ldq, ldk, ldv, ldo, bsq, bsk, bsv, bso, S, dh, scale * 1.4426950408889634f, (const uint16_t *)tok, grp, 1};
+    if (pf) {                       // prefetch ranges (address, bytes) x 2 as whole 64-byte lines
+        for (int r = 0; r < 2; ++r) {
+            if (!pf[2 * r + 1]) continue;
+            if (!pf[2 * r]) { sh_set_error(-1, "[sh_attention_batched_prefetch] NULL prefetch address"); return -1; }
+            const uint64_t base = pf[2 * r] & ~uint64_t(63), lines = (pf[2 * r] + pf[2 * r + 1] - base + 63) / 64;
+            if (lines >= (1ull << 30)) { sh_set_error(-1, "[sh_attention_batched_prefetch] prefetch range above 64 GiB"); return -1; }
+            (r ? a.pf1 : a.pf0) = (const uint8_t *)base;
+            (r ? a.pfl1 : a.pfl0) = (uint32_t)lines;
+        }
+    }
     {
         static const int remap = [] { const char *e = getenv("SH_ATTN_XCD"); return (e && *e) ? atoi(e) : 1; }();
         const uint32_t X = (uint32_t)sh_num_xcds();
@@ -893,8 +925,14 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
         go(k_attn_rows, dim3(S, H, B), S * sizeof(float));
     } else if ((dh == 64 || dh == 128) && vec && impl != 2 && fold && (uint64_t)KB * (ldk > ldv ? ldk : ldv) * 2 < (1ull << 31)) {
         // (k_flash3 addresses a key block's rows as a scalar base plus 32-bit lane offsets)
-        if (dh == 64) go2(k_flash3<64, 2>, grid, 0);
-        else go2(k_flash3<128, 2>, grid, 0);
+        if (a.pfl0 | a.pfl1) {
+            if (dh == 64) go2(k_flash3<64, 2, true>, grid, 0);
+            else go2(k_flash3<128, 2, true>, grid, 0);
+            a.pfl0 = a.pfl1 = 0;                    // (this kernel reads the ranges itself: no pass after it)
+        } else {
+            if (dh == 64) go2(k_flash3<64, 2>, grid, 0);
+            else go2(k_flash3<128, 2>, grid, 0);
+        }
     } else if ((dh == 64 || dh == 128) && vec) {
         if (dh == 64) fold ? go2(k_flash2<64, 2, false, true>, grid, 0) : go2(k_flash2<64, 2, false, false>, grid, 0);
         else fold ? go2(k_flash2<128, 2, false, true>, grid, 0) : go2(k_flash2<128, 2, false, false>, grid, 0);
@@ -913,6 +951,10 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
         go(k_attn_rows, dim3(S, H, B), S * sizeof(float));
     }
     if (!sh_launch_ok("sh_attention")) return SH_EHIP;
+    if (a.pfl0 | a.pfl1) {                          // a kernel without the prefetch: the same reads after it
+        for (int r = 0; r < 2; ++r)
+            if (pf[2 * r + 1] && sh_prefetch(pf[2 * r], pf[2 * r + 1]) != 0) return SH_EHIP;
+    }
     g_prof.valid = events;         // a batched or captured call leaves no stamps: the profile then reads 0
     return 0;
 }
@@ -979,6 +1021,17 @@ int sh_attention_batched(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_
     if (H == 0 || dh * H != D) { sh_set_error(-1, "[sh_attention_batched] D=%u not divisible by H=%u", D, H); return -1; }
     if (sq && S % sq) { sh_set_error(-1, "[sh_attention_batched] sq=%u does not divide S=%u", sq, S); return -1; }
     return run(q, k, v, o, B, S, dh, H, ldq, ldk, ldv, ldo, bsq, bsk, bsv, bso, scale, 0, 1, false);
+}
+
+int sh_attention_batched_prefetch(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, uint32_t D, uint32_t H,
+                                  uint32_t ldq, uint32_t ldk, uint32_t ldv, uint32_t ldo,
+                                  uint64_t bsq, uint64_t bsk, uint64_t bsv, uint64_t bso, float scale, uint32_t sq,
+                                  uint64_t pf0, uint64_t pf0_bytes, uint64_t pf1, uint64_t pf1_bytes) {
+    const uint32_t dh = H ? D / H : 0;
+    if (H == 0 || dh * H != D) { sh_set_error(-1, "[sh_attention_batched_prefetch] D=%u not divisible by H=%u", D, H); return -1; }
+    if (sq && S % sq) { sh_set_error(-1, "[sh_attention_batched_prefetch] sq=%u does not divide S=%u", sq, S); return -1; }
+    const uint64_t pf[4] = {pf0, pf0_bytes, pf1, pf1_bytes};
+    return run(q, k, v, o, B, S, dh, H, ldq, ldk, ldv, ldo, bsq, bsk, bsv, bso, scale, 0, 1, false, pf);
 }
 
 int sh_attention_head_masked(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t S, uint32_t dh,

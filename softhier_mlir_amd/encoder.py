@@ -58,14 +58,24 @@ class LayerParams:
 
     def fold(self, lib) -> None:
         """The weight side of both LayerNorm folds (sh_ln_fold, enqueued on the library stream), once: `wqkv_ln`,
-        `cqkv`, `dqkv` for LN1 -> QKV and `w1_ln`, `c1`, `d1` for LN2 -> FFN-up (fp16 W', fp32 c and d)."""
+        `cqkv`, `dqkv` for LN1 -> QKV and `w1_ln`, `c1`, `d1` for LN2 -> FFN-up (fp16 W', fp32 c and d). The weights
+        the fused layer reads after its attention (`wo`, `w1_ln`, `w2`) then sit back to back in one allocation,
+        `tail`, which the stack reads into the caches during attention as one range."""
         if "w1_ln" in self.t:
             return
         A = shops.addr
+        wo, w1, w2 = self.t["wo"], self.t["w1"], self.t["w2"]
+        tail = torch.empty(wo.numel() + w1.numel() + w2.numel(), dtype=torch.float16, device=wo.device)
+        n0, n1 = wo.numel(), wo.numel() + w1.numel()
+        self.t["wo"] = tail[:n0].view(wo.shape)
+        self.t["wo"].copy_(wo)
+        self.t["w2"] = tail[n1:].view(w2.shape)
+        self.t["w2"].copy_(w2)
+        self.t["tail"] = tail
         for w, g, be, b, tag in (("wqkv", "g1", "be1", "bqkv", "qkv"), ("w1", "g2", "be2", "b1", "1")):
             W = self.t[w]
             K, N = W.shape
-            wp = torch.empty_like(W)
+            wp = tail[n0:n1].view(W.shape) if tag == "1" else torch.empty_like(W)
             c = torch.empty(N, dtype=torch.float32, device=W.device)
             d = torch.empty(N, dtype=torch.float32, device=W.device)
             lib.sh_last_error()                  # reads and clears: the check below sees this call's status only
@@ -87,8 +97,7 @@ class Encoder:
         self.gemm_cfg = shops.cfg()          # tile hints 256^3 (library default), as the reference's default policy
         self.row_partials = True             # False: sh_row_stats before each folded GEMM (seven launches a layer)
         self.tap = None                      # optional tap(name) -> context manager around each op (timing)
-        self.prefetch = True                 # stacks: a layer's later weights pulled into the caches during attention
-        self._side: torch.cuda.Stream | None = None
+        self.prefetch = True                 # stacks: a layer's later weights read into the caches by its attention
 
     def _op(self, name: str):
         return self.tap(name) if self.tap is not None else contextlib.nullcontext()
@@ -135,12 +144,15 @@ class Encoder:
         return out
 
     # -- fused sequence (additive entry points) ------------------------------------------------------------
-    def _fused_plan(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int, x_parts: bool) -> list:
+    def _fused_plan(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int, x_parts: bool,
+                    pf: tuple | None = None) -> list:
         """The layer's library calls with every argument converted once: (op name, function, args, what).
-        x_parts: the row partials of x are in the `pst_x` buffer (written by the GEMM that stored x)."""
+        x_parts: the row partials of x are in the `pst_x` buffer (written by the GEMM that stored x).
+        pf: two (address, bytes) ranges the attention call reads into the caches (sh_attention_batched_prefetch)."""
         p.fold(self.lib)
         x_parts = x_parts and self.row_partials
-        key = (x.data_ptr(), out.data_ptr(), B, S, x_parts, self.row_partials) + tuple(t.data_ptr() for t in p.t.values())
+        key = ((x.data_ptr(), out.data_ptr(), B, S, x_parts, self.row_partials, pf)
+               + tuple(t.data_ptr() for t in p.t.values()))
         hit = self._plans.get(key)
         if hit is not None:
             return hit
@@ -163,8 +175,9 @@ class Encoder:
             ("qkv", L.sh_gemm_ex, (A(x), A(p["wqkv_ln"]), A(qkv), rows, D3, D, D, D3, D3, cfg,
                                    shops.epi(bias=A(p["dqkv"]), bias_fmt=F32, ln_c=A(p["cqkv"]), **ln1)),
              "sh_gemm_ex qkv"),
-            ("attention", L.sh_attention_batched, (A(qkv), A(qkv, D), A(qkv, 2 * D), A(b["o"]), B, S, D, H, D3, D3, D3, D,
-                                                   S * D3, S * D3, S * D3, S * D, 1.0 / math.sqrt(D // H), 0), "sh_attention_batched"),
+            ("attention", L.sh_attention_batched_prefetch if pf else L.sh_attention_batched,
+             (A(qkv), A(qkv, D), A(qkv, 2 * D), A(b["o"]), B, S, D, H, D3, D3, D3, D, S * D3, S * D3, S * D3, S * D,
+              1.0 / math.sqrt(D // H), 0) + ((pf[0][0], pf[0][1], pf[1][0], pf[1][1]) if pf else ()), "sh_attention_batched"),
             ("out_proj", L.sh_gemm_ex, (A(b["o"]), A(p["wo"]), A(b["h"]), rows, D, D, D, D, D, cfg,
                                         shops.epi(bias=A(p["bo"]), residual=A(x), ldr=D, stats_out=sp(b["pst_h"]))),
              "sh_gemm_ex wo"),
@@ -188,43 +201,26 @@ class Encoder:
         return calls
 
     def layer_fused(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int,
-                    x_parts: bool = False, prefetch: list | None = None) -> torch.Tensor:
+                    x_parts: bool = False, prefetch: tuple | None = None) -> torch.Tensor:
         """One fused layer. x_parts=True: x was stored by the previous layer's FFN-down, whose row partials are in
         the encoder's `pst_x` buffer (the layer then skips sh_row_stats); the layer leaves out's in it.
-        prefetch: (address, bytes) ranges read into the caches on a second stream once the QKV GEMM is done."""
-        for name, fn, args, what in self._fused_plan(x, out, p, B, S, x_parts):
+        prefetch: two (address, bytes) ranges its attention reads into the caches (prefetch_ranges)."""
+        for name, fn, args, what in self._fused_plan(x, out, p, B, S, x_parts, prefetch):
             with self._op(name):
                 rc = fn(*args)
             if what is not None:
                 _check(rc, what)
-            if name == "qkv" and prefetch:
-                self._prefetch(prefetch)
         return out
 
-    def _prefetch(self, ranges: list) -> None:
-        """sh_prefetch of `ranges` on the encoder's second stream (default priority), ordered after the work enqueued
-        so far on the library stream: the reads run beside the next kernel (attention, which leaves room on every CU)
-        and only bring weights into L2 and the Infinity Cache, so nothing waits for them."""
-        main = torch.cuda.current_stream()
-        if self._side is None:
-            self._side = torch.cuda.Stream()
-        ev = torch.cuda.Event()
-        ev.record(main)
-        self._side.wait_event(ev)
-        prev = self.lib.sh_get_stream()
-        self.lib.sh_set_stream(self._side.cuda_stream)
-        try:
-            for a, n in ranges:
-                _check(self.lib.sh_prefetch(a, n), "sh_prefetch")
-        finally:
-            self.lib.sh_set_stream(prev)
-
-    @staticmethod
-    def prefetch_ranges(p: LayerParams, nxt: "LayerParams | None") -> list:
-        """The weights a fused layer reads after its QKV GEMM (out-proj W, folded FFN-up W', FFN-down W) and the next
-        layer's folded QKV W', as (address, bytes)."""
-        ts = [p["wo"], p["w1_ln"], p["w2"]] + ([nxt["wqkv_ln"]] if nxt is not None else [])
-        return [(shops.addr(t), t.numel() * t.element_size()) for t in ts]
+    def prefetch_ranges(self, p: LayerParams, nxt: "LayerParams | None") -> tuple:
+        """The weights a fused layer reads after its attention (out-proj W, folded FFN-up W', FFN-down W: one
+        allocation) and the next layer's folded QKV W', as two (address, bytes) ranges."""
+        p.fold(self.lib)
+        r0 = (shops.addr(p["tail"]), p["tail"].numel() * 2)
+        if nxt is None:
+            return r0, (0, 0)
+        nxt.fold(self.lib)
+        return r0, (shops.addr(nxt["wqkv_ln"]), nxt["wqkv_ln"].numel() * 2)
 
     def capture(self, x: torch.Tensor, out: torch.Tensor, p: LayerParams, B: int, S: int) -> "CapturedLayer":
         """Record one fused layer into a HIP graph (replay with `.replay()` on any stream). The layer runs once
@@ -278,13 +274,9 @@ class Encoder:
             if tmp is None or tmp.shape != x.shape or tmp.dtype != x.dtype or tmp.device != x.device:
                 tmp = torch.empty_like(x)
                 self._pingpong = tmp
-        # a stack's weights do not all fit in the Infinity Cache next to its activations: each layer's later weights
-        # and the next layer's QKV weight are read into the caches during its attention (eager library stream only)
-        pre = (sequence == "fused" and n > 1 and self.prefetch and not torch.cuda.is_current_stream_capturing()
-               and self.lib.sh_get_stream() == torch.cuda.current_stream().cuda_stream)
-        if pre:
-            for p in params:
-                p.fold(self.lib)
+        # a stack's weights do not all fit in the Infinity Cache next to its activations: each layer's attention reads
+        # the layer's later weights and the next layer's QKV weight into the caches
+        pre = sequence == "fused" and n > 1 and self.prefetch
         cur = x
         for i, p in enumerate(params):          # ping-pong so that the last layer writes `out`
             dst = out if (n - 1 - i) % 2 == 0 else tmp
@@ -294,8 +286,6 @@ class Encoder:
             else:
                 step(cur, dst, p, B, S)
             cur = dst
-        if pre and self._side is not None:      # later work on the library stream is ordered after the reads
-            torch.cuda.current_stream().wait_stream(self._side)
         return out
 
 

@@ -90,6 +90,8 @@ _SIGS: dict[str, tuple] = {
     "sh_attention_l1_bytes_q": (u32, [u32, u32, u32]), "sh_attention_l1_bytes": (u32, [u32, u32]),
     "sh_attention_q_block": (u32, [u32, u32, u32, u32]), "sh_attention_profile": (u32, [u32, u32, u32]),
     "sh_attention_batched": (i32, [u64, u64, u64, u64, u32, u32, u32, u32, u32, u32, u32, u32, u64, u64, u64, u64, f32, u32]),
+    "sh_attention_batched_prefetch": (i32, [u64, u64, u64, u64, u32, u32, u32, u32, u32, u32, u32, u32, u64, u64, u64, u64, f32,
+                                            u32, u64, u64, u64, u64]),
     # test helpers
     "sh_test_fill_int_fp16": (None, [u64, u32, u32, u32, u32, i32, i32]),
     "sh_test_fill_fp16": (None, [u64, u32, u32, u32, u32, i32, i32, f32]),

@@ -167,3 +167,27 @@ def test_profile_phase_stamps_are_monotone(lib, gpu, S):
     assert lib.sh_attention_batched(A(q), A(q), A(q), A(O), 1, S, D, H, D, D, D, D, 0, 0, 0, 0, 0.125, 0) == 0
     lib.sh_barrier_global()
     assert all(lib.sh_attention_profile(S, 64, p) == 0 for p in range(8))
+
+
+@pytest.mark.parametrize("dh,scale", [(64, 0.125), (128, 0.088), (64, 1.0)])
+def test_batched_prefetch_stores_the_bits_of_batched(lib, gpu, dh, scale):
+    """sh_attention_batched_prefetch with two ranges (unaligned ends, one of them larger than the lines the one-pass
+    kernel's threads cover in one pass) stores the bits of sh_attention_batched and leaves the ranges unchanged;
+    scale 1.0 does not fold into the queries, so the two-pass kernel runs and the ranges are read after it."""
+    import torch
+    B, S, H = 3, 320, 4
+    D = H * dh
+    q, k, v = (to_dev(data.normal((B * S, D), 40 + i)) for i in range(3))
+    O1, O2 = _zeros(B * S, D), _zeros(B * S, D)
+    g = torch.Generator(device="cuda").manual_seed(4)
+    r0 = torch.randint(-30000, 30000, (6 << 20,), dtype=torch.int16, device="cuda", generator=g)
+    r1 = torch.randint(-30000, 30000, (3 << 20,), dtype=torch.int16, device="cuda", generator=g)
+    keep = (r0.clone(), r1.clone())
+    args = (A(q), A(k), A(v), None, B, S, D, H, D, D, D, D, S * D, S * D, S * D, S * D, scale, 0)
+    assert lib.sh_attention_batched(*args[:3], A(O1), *args[4:]) == 0, shops.last_error()
+    assert lib.sh_attention_batched_prefetch(*args[:3], A(O2), *args[4:], A(r0) + 6, (12 << 20) - 20,
+                                             A(r1) + 130, 1000) == 0, shops.last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(O1.view(torch.int16), O2.view(torch.int16))
+    assert torch.equal(r0, keep[0]) and torch.equal(r1, keep[1])
+    assert lib.sh_attention_batched_prefetch(*args[:3], A(O2), *args[4:], 0, 64, 0, 0) == -1      # NULL range

@@ -67,8 +67,8 @@ def test_fused_stack_reference_lcg_layers(lib, gpu):
 
 
 def test_stack_prefetch_changes_no_bits(lib, gpu):
-    """The stack with its weight prefetch (sh_prefetch on a second stream during each attention) stores exactly the
-    bits of the stack without it: the prefetch only reads."""
+    """The stack with its weight prefetch (each layer's attention reads the layer's later weights and the next layer's
+    QKV weight into the caches) stores exactly the bits of the stack without it: the prefetch only reads."""
     import torch
     B, S, D, F, H = 2, 256, 768, 3072, 12
     ps = [encoder.LayerParams.from_host(data.encoder_params(D, F, seed=300 + i)) for i in range(4)]
