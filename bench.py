@@ -64,23 +64,49 @@ def parse():
     return ap.parse_args()
 
 
+_WARM: dict = {}
+
+
+def busy(torch, fn, seconds: float) -> None:
+    """Untimed warm-up before a timed region: a large fp16 product (8192^3 through torch.matmul, ~1.5 ms a launch)
+    back to back for `seconds` of wall time, then `fn` three times. On MI355X the same kernel runs up to ~20 %
+    slower until the GPU has been busy for ~20 ms, and again after ~50 ms idle (the clocks follow sustained load):
+    a few launches of a short kernel do not get there, and thousands of them would flood a kernel trace."""
+    if "a" not in _WARM:
+        g = torch.Generator(device="cuda").manual_seed(0)
+        _WARM["a"] = torch.randn((8192, 8192), dtype=torch.float16, device="cuda", generator=g)
+        _WARM["c"] = torch.empty_like(_WARM["a"])
+    a, c = _WARM["a"], _WARM["c"]
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(4):
+            torch.matmul(a, a, out=c)
+        torch.cuda.synchronize()
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+
+
 def traced_avg_us(op: str):
-    """(kernel, average us per launch) of `op` in the committed layer kernel trace
-    (profiles/encoder_layer_b32_s256_kernel_trace.md, rocprofv3 --kernel-trace): the trace's average of the same
-    back-to-back launches the roofline times (its `roofline_trace` line), else the op's in-layer average; or None."""
+    """(kernel, average us per launch, {figure: us}) of `op` in the committed layer kernel trace
+    (profiles/encoder_layer_b32_s256_kernel_trace.md, rocprofv3 --kernel-trace --stats): the `--stats` average over
+    every launch of the kernel in the traced command (its `roofline_trace ... stats_avg_us` line), else the op's
+    average in the timed layer steps; the trace's other figures for the op (in the timed steps, back to back) ride
+    along. None without the file."""
     f = ROOT / "profiles" / "encoder_layer_b32_s256_kernel_trace.md"
     if not f.exists():
         return None
-    kernel, avg, b2b = None, None, None
+    kernel, avg, figs = None, None, {}
     for line in f.read_text().splitlines():
         cells = [c.strip() for c in line.strip().strip("|").split("|")]
         if len(cells) >= 5 and cells[0] == op and cells[3].isdigit():
             kernel, avg = cells[1].strip("`"), float(cells[4])
-        if line.startswith(f"roofline_trace {op} back_to_back_avg_us:"):
-            b2b = float(line.split(":")[1])
+        if line.startswith(f"roofline_trace {op} "):
+            name, val = line[len(f"roofline_trace {op} "):].split(":")
+            figs[name.strip()] = float(val)
     if kernel is None:
         return None
-    return kernel, (b2b if b2b is not None else avg)
+    return kernel, figs.get("stats_avg_us", avg), figs
 
 
 def counted_traffic(op: str):
@@ -141,9 +167,7 @@ def rowops_bandwidth(lib, torch, B: int, S: int, D: int, F: int, H: int, reps: i
 
         def timed(fn):
             """(median us of single launches with events around each, us per launch of all sets back to back)"""
-            for st in sets:
-                fn(*st)
-            torch.cuda.synchronize()
+            busy(torch, lambda: [fn(*st) for st in sets], 0.15)
             times = []
             for _ in range(reps):
                 for st in sets:
@@ -190,7 +214,7 @@ def stack12(torch, enc, x, B: int, S: int, D: int, F: int, reps: int = 5, warmup
     for _ in range(max(1, warmup)):
         enc.forward(x, layers, B, S, out=y)             # warm-up (buffers, tile choices)
         enc.forward(x, layers[:1], B, S, out=y)
-    torch.cuda.synchronize()
+    busy(torch, lambda: enc.forward(x, layers, B, S, out=y), 0.25)
 
     def timed(ls):
         t0 = time.perf_counter()
@@ -225,9 +249,7 @@ def copy_curve(lib, torch) -> dict:
                  torch.empty(n // 2, dtype=torch.float16, device="cuda")) for _ in range(nsets)]
         res = {"MB": mb}
         for name, fn in (("library", lambda a, b: lib.sh_dma_copy(A(b), A(a), n)), ("hip_d2d", lambda a, b: b.copy_(a))):
-            for a, b in sets:
-                fn(a, b)
-            torch.cuda.synchronize()
+            busy(torch, lambda: [fn(a, b) for a, b in sets], 0.1)
             ts = []
             for _ in range(3 if mb < 512 else 2):
                 for a, b in sets:
@@ -261,8 +283,7 @@ def extra_configs(lib, torch, enc, x, lp, p, B: int, S: int, D: int, F: int, H: 
                                       Sl * D3, Sl * D3, Sl * D3, Sl * D, 1.0 / (D // H) ** 0.5, 0)
         if rc != 0:
             raise RuntimeError(f"sh_attention_batched failed: {shops.last_error()}")
-    for _ in range(3):
-        run()
+    busy(torch, run, 0.1)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(20):
@@ -294,9 +315,7 @@ def config_table(lib, torch) -> list:
     def gpu_us(fn, n=60):
         """Median of n single launches with events around each; the average of n launches back to back (events
         around all of them, dispatch pipelined) is kept for the record."""
-        for _ in range(5):
-            fn()
-        torch.cuda.synchronize()
+        busy(torch, fn, 0.1)
         ts = []
         for _ in range(n):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -476,7 +495,7 @@ def config_table(lib, torch) -> list:
 def library_gemm_table(lib, torch, B: int = 32, S: int = 256, D: int = 768, F: int = 3072) -> dict:
     """The layer's four GEMM shapes (M = B*S) timed three ways on the same operands: sh_gemm_ex with no epilogue,
     sh_gemm_ex with the layer's epilogue, and torch.matmul (hipBLASLt, no epilogue). Average of 50 launches back to
-    back with HIP events around them, after 10 warm-up launches; the order of the three is interleaved per shape."""
+    back with HIP events around them, after 0.15 s of warm-up launches; the order of the three is interleaved per shape."""
     from softhier_mlir_amd import shops
     A = shops.addr
     M = B * S
@@ -501,9 +520,7 @@ def library_gemm_table(lib, torch, B: int = 32, S: int = 256, D: int = 768, F: i
         }
         res = {}
         for key, fn in runs.items():
-            for _ in range(10):
-                fn()
-            torch.cuda.synchronize()
+            busy(torch, fn, 0.15)
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
             for _ in range(50):
@@ -605,7 +622,7 @@ def main() -> int:
 
     for _ in range(args.warmup):
         step(x, out, lp, B, S)
-    torch.cuda.synchronize()
+    busy(torch, step, 0.3)
 
     events: dict = {}
 
@@ -671,6 +688,7 @@ def main() -> int:
         graph = enc.capture(x, out, lp, B, S)
         for _ in range(args.warmup):
             graph.replay()
+        busy(torch, graph.replay, 0.2)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -716,6 +734,7 @@ def main() -> int:
             if tr is not None:          # the committed kernel trace's average for the same op, and its fraction
                 roofline.update({"trace_kernel": tr[0], "trace_avg_launch_us": tr[1],
                                  "trace_frac": round(c["flop"] / (tr[1] * 1e-6) / 1e12 / PEAK_TFLOPS, 4),
+                                 "trace_figures_us": tr[2],
                                  "trace_source": "profiles/encoder_layer_b32_s256_kernel_trace.md"})
         else:
             ach = c["bytes"] / (us * 1e-6) / 1e9
