@@ -52,7 +52,10 @@ __device__ __forceinline__ float sh_fast_rsq(float x) { return __builtin_amdgcn_
 // (packed fp16 multiply / fma / add, hardware fp16 exp2 and reciprocal): 3.5 VALU + 2 transcendental
 // instructions per element. Relative error is a few fp16 ulps where the result is not negligible. Overflow
 // needs no clamp: 2^t = inf gives x * rcp(inf) = 0, 2^t = 0 gives x. Every caller (row op, GEMM epilogue,
-// split-K reduction) uses this one function, so fused and unfused sequences store identical bits.
+// split-K reduction) uses this one function, so fused and unfused sequences store identical bits: each step
+// rounds to fp16 as written, which leaves the compiler no product to fuse with a later rounding (an fp32 form,
+// x * rcp(1 + e) in fp32 and then fp16, was compiled into a single-rounding fp16 fma in one kernel and two
+// roundings in another).
 #define SH_GELU_K0 (-2.3022082f)
 #define SH_GELU_K1 (-0.10294324f)
 __device__ __forceinline__ sh_h2 sh_gelu_h2(sh_h2 x) {
