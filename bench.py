@@ -53,6 +53,10 @@ def parse():
     ap.add_argument("--library-gemm", action="store_true",
                     help="instead of the layer line: the four encoder GEMM shapes through sh_gemm_ex (plain and with the "
                          "layer's epilogue) next to torch.matmul (hipBLASLt), one JSON line")
+    ap.add_argument("--torch-sdpa", action="store_true",
+                    help="instead of the layer line: batched attention (B=32 S=256, B=8 S=1024, 12 heads of 64) through "
+                         "sh_attention_batched next to torch's scaled_dot_product_attention (flash and memory-efficient "
+                         "backends only), one JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 3 plain device copies of 512 MiB (a known-size kernel for scaling HBM counters)")
     ap.add_argument("--stack", action="store_true",
@@ -539,6 +543,57 @@ def library_gemm_table(lib, torch, B: int = 32, S: int = 256, D: int = 768, F: i
     return out
 
 
+def torch_sdpa_table(lib, torch) -> dict:
+    """Batched attention through sh_attention_batched next to torch.nn.functional.scaled_dot_product_attention on
+    the same fp16 operands ([B, H, S, 64] contiguous for torch), restricted to its flash and memory-efficient
+    backends (a backend that is not available raises; no fallback to the math path). Average of 50 launches back to
+    back with HIP events around them, after the warm-up; the largest difference between the two outputs."""
+    from softhier_mlir_amd import shops
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    A = shops.addr
+    out = {}
+    for B, S in ((32, 256), (8, 1024)):
+        H, dh = 12, 64
+        D = H * dh
+        g = torch.Generator(device="cuda").manual_seed(3)
+        q = torch.randn((B, S, D), dtype=torch.float16, device="cuda", generator=g)
+        k, v = torch.randn_like(q), torch.randn_like(q)
+        o = torch.empty_like(q)
+
+        def lib_call():
+            rc = lib.sh_attention_batched(A(q), A(k), A(v), A(o), B, S, D, H, D, D, D, D, S * D, S * D, S * D, S * D,
+                                          0.125, 0)
+            if rc != 0:
+                raise RuntimeError(f"sh_attention_batched failed: {shops.last_error()}")
+        qh, kh, vh = (t.view(B, S, H, dh).transpose(1, 2).contiguous() for t in (q, k, v))
+
+        def timed(fn, n=50):
+            busy(torch, fn, 0.1)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(n):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            return round(e0.elapsed_time(e1) * 1e3 / n, 2)
+        res = {"sh_attention_batched_us": timed(lib_call)}
+        flop = 4 * B * H * S * S * dh
+        res["TFLOP/s_library"] = round(flop / (res["sh_attention_batched_us"] * 1e-6) / 1e12, 1)
+        for name, backend in (("flash", SDPBackend.FLASH_ATTENTION), ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
+            try:
+                with sdpa_kernel([backend]):
+                    sdpa = lambda: torch.nn.functional.scaled_dot_product_attention(qh, kh, vh, scale=0.125)  # noqa: E731
+                    got = sdpa()
+                    torch.cuda.synchronize()
+                    res[f"torch_sdpa_{name}_us"] = timed(sdpa)
+                    res[f"max_abs_diff_{name}_vs_library"] = round(
+                        float((got.transpose(1, 2).reshape(B, S, D).float() - o.float()).abs().max()), 5)
+            except RuntimeError as e:
+                res[f"torch_sdpa_{name}"] = f"unavailable: {str(e)[:120]}"
+        out[f"B{B}_S{S}"] = res
+    return out
+
+
 def cpu_baseline(B: int, S: int, D: int, F: int, H: int, p: dict, x) -> dict:
     """The oracle's numpy restatement of one encoder layer, timed on this host's cores (median of 5)."""
     import numpy as np
@@ -584,6 +639,9 @@ def main() -> int:
         return 0
     if args.library_gemm:
         print(json.dumps({"library_gemm": library_gemm_table(lib, torch, args.batch, args.seq)}), flush=True)
+        return 0
+    if args.torch_sdpa:
+        print(json.dumps({"torch_sdpa": torch_sdpa_table(lib, torch)}), flush=True)
         return 0
     if args.copy_curve:
         print(json.dumps(copy_curve(lib, torch)), flush=True)
