@@ -57,6 +57,10 @@ def parse():
                     help="instead of the layer line: batched attention (B=32 S=256, B=8 S=1024, 12 heads of 64) through "
                          "sh_attention_batched next to torch's scaled_dot_product_attention (flash and memory-efficient "
                          "backends only), one JSON line")
+    ap.add_argument("--torch-rowops", action="store_true",
+                    help="instead of the layer line: the row ops at the batched shapes, cold, through the library next to "
+                         "torch's own kernels for the same ops (layer_norm, softmax, tanh GELU, add, bias add, transpose "
+                         "copy), one JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 3 plain device copies of 512 MiB (a known-size kernel for scaling HBM counters)")
     ap.add_argument("--stack", action="store_true",
@@ -543,6 +547,98 @@ def library_gemm_table(lib, torch, B: int = 32, S: int = 256, D: int = 768, F: i
     return out
 
 
+def torch_rowops_table(lib, torch, B: int = 32, S: int = 256, D: int = 768, F: int = 3072, H: int = 12) -> dict:
+    """The row ops at the batched shapes through the library and through torch's own kernels for the same operation
+    (torch.nn.functional.layer_norm, torch.softmax, gelu(approximate="tanh"), torch.add, the broadcast bias add,
+    a transposed view copied into a contiguous output), cold: buffer sets rotated over >= 512 MiB as in the bench's
+    row-op section, after the warm-up; the median of single launches with HIP events around each and the average of
+    all sets back to back, and the largest difference between the two outputs of one set. Softmax runs unscaled
+    (torch's kernel has no scale)."""
+    from softhier_mlir_amd import shops
+    A = shops.addr
+    M = B * S
+    ops = {"layernorm": (M, D), "softmax": (H * M, S), "gelu": (M, F), "add": (M, D), "add_bias": (M, D), "transpose": (M, D)}
+    out = {}
+    for name, (r, c) in ops.items():
+        nbytes = 2 * 3 * r * c if name == "add" else 2 * 2 * r * c
+        nsets = max(2, int((512 << 20) // nbytes) + 1)
+        g = torch.Generator(device="cuda").manual_seed(5)
+        gamma = torch.rand((c,), dtype=torch.float16, device="cuda", generator=g) + 0.5
+        beta = torch.rand((c,), dtype=torch.float16, device="cuda", generator=g) - 0.5
+        sets = []
+        for _ in range(nsets):
+            x = torch.randn((r, c), dtype=torch.float16, device="cuda", generator=g)
+            y = torch.empty((c, r) if name == "transpose" else (r, c), dtype=torch.float16, device="cuda")
+            yt = torch.empty_like(y)
+            b = torch.randn((r, c), dtype=torch.float16, device="cuda", generator=g) if name == "add" else None
+            sets.append((x, y, yt, b))
+
+        def run_lib(x, y, yt, b):
+            if name == "layernorm":
+                lib.sh_layernorm(A(y), A(x), A(gamma), A(beta), r, c, c, 1e-6, shops.SH_ALL)
+            elif name == "softmax":
+                lib.sh_softmax_rows(A(y), A(x), r, c, c, 1.0, shops.SH_ALL)
+            elif name == "gelu":
+                lib.sh_gelu(A(y), A(x), r, c, c, shops.SH_ALL)
+            elif name == "add":
+                lib.sh_add(A(y), A(x), A(b), r, c, c, shops.SH_ALL)
+            elif name == "add_bias":
+                lib.sh_add_bias(A(y), A(x), A(beta), r, c, c, shops.SH_ALL)
+            else:
+                lib.sh_transpose(A(y), A(x), r, c, c, r, shops.SH_ALL)
+
+        def run_torch(x, y, yt, b):
+            if name == "layernorm":
+                torch.nn.functional.layer_norm(x, (c,), gamma, beta, 1e-6)   # (allocates its output)
+            elif name == "softmax":
+                torch.softmax(x, dim=-1, out=yt)
+            elif name == "gelu":
+                torch.nn.functional.gelu(x, approximate="tanh")       # (torch allocates its output: no out= form)
+            elif name == "add":
+                torch.add(x, b, out=yt)
+            elif name == "add_bias":
+                torch.add(x, beta, out=yt)
+            else:
+                yt.copy_(x.t())
+
+        def timed(fn):
+            busy(torch, lambda: [fn(*st) for st in sets], 0.15)
+            ts = []
+            for _ in range(3):
+                for st in sets:
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    fn(*st)
+                    e1.record()
+                    ts.append((e0, e1))
+            torch.cuda.synchronize()
+            ms = sorted(a.elapsed_time(b) for a, b in ts)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for st in sets:
+                fn(*st)
+            e1.record()
+            torch.cuda.synchronize()
+            return ms[len(ms) // 2] * 1e3, e0.elapsed_time(e1) * 1e3 / len(sets)
+
+        lu, lb = timed(run_lib)
+        tu, tb = timed(run_torch)
+        x, y, yt, b = sets[0]
+        run_lib(x, y, yt, b)
+        ref = {"layernorm": lambda: torch.nn.functional.layer_norm(x, (c,), gamma, beta, 1e-6),
+               "softmax": lambda: torch.softmax(x, dim=-1), "gelu": lambda: torch.nn.functional.gelu(x, approximate="tanh"),
+               "add": lambda: x + b, "add_bias": lambda: x + beta, "transpose": lambda: x.t().contiguous()}[name]()
+        torch.cuda.synchronize()
+        out[name] = {"shape": [r, c], "bytes": nbytes, "library_us": round(lu, 2), "library_us_batched": round(lb, 2),
+                     "torch_us": round(tu, 2), "torch_us_batched": round(tb, 2),
+                     "library_GB/s_batched": round(nbytes / (lb * 1e-6) / 1e9, 1),
+                     "torch_GB/s_batched": round(nbytes / (tb * 1e-6) / 1e9, 1),
+                     "max_abs_diff": round(float((y.float() - ref.float()).abs().max()), 5)}
+        del sets
+        torch.cuda.empty_cache()
+    return out
+
+
 def torch_sdpa_table(lib, torch) -> dict:
     """Batched attention through sh_attention_batched next to torch.nn.functional.scaled_dot_product_attention on
     the same fp16 operands ([B, H, S, 64] contiguous for torch), restricted to its flash and memory-efficient
@@ -639,6 +735,9 @@ def main() -> int:
         return 0
     if args.library_gemm:
         print(json.dumps({"library_gemm": library_gemm_table(lib, torch, args.batch, args.seq)}), flush=True)
+        return 0
+    if args.torch_rowops:
+        print(json.dumps({"torch_rowops": torch_rowops_table(lib, torch)}), flush=True)
         return 0
     if args.torch_sdpa:
         print(json.dumps({"torch_sdpa": torch_sdpa_table(lib, torch)}), flush=True)
