@@ -61,6 +61,10 @@ def parse():
                     help="instead of the layer line: the row ops at the batched shapes, cold, through the library next to "
                          "torch's own kernels for the same ops (layer_norm, softmax, tanh GELU, add, bias add, transpose "
                          "copy), one JSON line")
+    ap.add_argument("--torch-layer", action="store_true",
+                    help="instead of the layer line: the same encoder layer (weights, input, op order) as a torch eager "
+                         "forward (layer_norm, linear = hipBLASLt, flash scaled_dot_product_attention, tanh GELU), timed as "
+                         "the bench line times the library's, next to the library's fused layer, one JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 3 plain device copies of 512 MiB (a known-size kernel for scaling HBM counters)")
     ap.add_argument("--stack", action="store_true",
@@ -547,6 +551,61 @@ def library_gemm_table(lib, torch, B: int = 32, S: int = 256, D: int = 768, F: i
     return out
 
 
+def torch_layer_table(torch, enc, lp, p: dict, xh, B: int, S: int, D: int, F: int, H: int, steps: int) -> dict:
+    """The bench's encoder layer (the same weights, input and the reference's op order) as a torch eager forward in
+    fp16: F.layer_norm, F.linear (hipBLASLt) with the Q, K and V weights in one matrix, scaled_dot_product_attention on
+    its flash backend only (no math path), F.gelu(approximate="tanh"). Both it and the library's fused layer (its
+    steps chained as in the bench line) are timed over `steps` steps on the synchronised host clock after the same
+    warm-up; the largest difference between the two layers' outputs for the same input."""
+    import numpy as np
+    import torch.nn.functional as Fn
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from softhier_mlir_amd import encoder
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    wqkv = T(np.concatenate([p["wq"], p["wk"], p["wv"]], axis=1).T)          # F.linear takes [out, in]
+    bqkv = T(np.concatenate([p["bq"], p["bk"], p["bv"]], axis=1).reshape(-1))
+    wo, w1, w2 = T(p["wo"].T), T(p["w1"].T), T(p["w2"].T)
+    bo, b1, b2, g1, be1, g2, be2 = (T(p[k].reshape(-1)) for k in ("bo", "b1", "b2", "g1", "be1", "g2", "be2"))
+    dh = D // H
+    x = T(xh)
+
+    def layer(xin):
+        ln1 = Fn.layer_norm(xin, (D,), g1, be1, 1e-6)
+        qkv = Fn.linear(ln1, wqkv, bqkv)
+        q, k, v = (qkv[:, i * D:(i + 1) * D].reshape(B, S, H, dh).transpose(1, 2) for i in range(3))
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            o = Fn.scaled_dot_product_attention(q, k, v, scale=1.0 / dh ** 0.5)
+        h = xin + Fn.linear(o.transpose(1, 2).reshape(B * S, D), wo, bo)
+        f = Fn.gelu(Fn.linear(Fn.layer_norm(h, (D,), g2, be2, 1e-6), w1, b1), approximate="tanh")
+        return h + Fn.linear(f, w2, b2)
+
+    ours = torch.empty_like(x)
+    enc.layer_fused(x, ours, lp, B, S, x_parts=False)
+    theirs = layer(x)
+    torch.cuda.synchronize()
+    diff = float((ours.float() - theirs.float()).abs().max())
+    bufs, n = (x.clone(), torch.empty_like(x)), [0]
+
+    def lib_step():
+        i = n[0]
+        n[0] += 1
+        enc.layer_fused(bufs[i % 2], bufs[(i + 1) % 2], lp, B, S, x_parts=i > 0)
+    res = {}
+    for name, fn in (("library_fused", lib_step), ("torch_eager", lambda: layer(x))):
+        busy(torch, fn, 0.3)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        res[name] = {"ms_per_step": round(ms, 4),
+                     "TFLOP/s": round(encoder.flops_per_layer(B, S, D, F) / (ms * 1e-3) / 1e12, 1)}
+    res["max_abs_diff_library_vs_torch"] = round(diff, 5)
+    res["config"] = {"batch": B, "seq_len": S, "d_model": D, "ffn": F, "heads": H, "steps": steps}
+    return res
+
+
 def torch_rowops_table(lib, torch, B: int = 32, S: int = 256, D: int = 768, F: int = 3072, H: int = 12) -> dict:
     """The row ops at the batched shapes through the library and through torch's own kernels for the same operation
     (torch.nn.functional.layer_norm, torch.softmax, gelu(approximate="tanh"), torch.add, the broadcast bias add,
@@ -756,6 +815,9 @@ def main() -> int:
         print(json.dumps({"stack12": stack12(torch, enc, x, B, S, D, F, reps=args.steps, warmup=args.warmup)}), flush=True)
         return 0
     lp = encoder.LayerParams.from_host(p)
+    if args.torch_layer:
+        print(json.dumps({"torch_layer": torch_layer_table(torch, enc, lp, p, xh, B, S, D, F, H, args.steps)}), flush=True)
+        return 0
     if args.sequence == "fused":
         # one layer of the 12-layer stack as it runs there: each step reads the rows the previous step stored, and
         # the row partials its FFN-down wrote (five launches); the first step starts with sh_row_stats
