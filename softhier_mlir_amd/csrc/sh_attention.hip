@@ -702,13 +702,33 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
         if (biased) scores(stc, sacc, Biased{});
         else scores(stc, sacc, std::false_type{});   // (while every m is 0 the bias step would add zeros)
         mask_tail();
-        // the block's maximum for this lane's query (lanes r32 and r32 + 32 hold complementary keys)
-        float bm = -INFINITY;
+        // V^T fragment j: substep j / DT, d tile j % DT (consecutive MFMAs alternate accumulators)
+        auto vfrag = [&](int j) -> sh_h8 {
+            const uint32_t at = vaddr[j] + (uint32_t)st * STAGE;
+            const sh_s4 lo = sh_ds_read_tr(at);
+            const sh_s4 hi = sh_ds_read_tr(at + 8 * (DH * 2));
+            return __builtin_bit_cast(sh_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        };
+        sh_h8 pf[4];                                 // numerators p = 2^acc, fp16, as the P.V MFMA operands
+        auto expo = [&]() {
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
+            for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sacc[tt][r]);
-        bm = sh_max_xor32(bm);
+                for (int r = 0; r < 16; ++r) pf[2 * tt + (r >> 3)][r & 7] = (_Float16)sh_fast_exp2(sacc[tt][r]);
+        };
+        // The first V fragments are read now and the numerators formed before the maximum test (formed again in
+        // the rare case that m moves): the exponentials then hide those reads' latency and the maximum's chain,
+        // and each P.V MFMA finds its fragment, read two MFMAs earlier, in registers.
+        constexpr int VA = 2;
+        sh_h8 vr[VA + 1];
+#pragma unroll
+        for (int j = 0; j < VA; ++j) vr[j] = vfrag(j);
+        expo();
+        // the block's maximum for this lane's query (lanes r32 and r32 + 32 hold complementary keys), two chains
+        float b0 = -INFINITY, b1 = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) { b0 = fmaxf(b0, sacc[0][r]); b1 = fmaxf(b1, sacc[1][r]); }
+        const float bm = sh_max_xor32(fmaxf(b0, b1));
         // m starts at 0; the first block moves it when its maximum is more than kTau away on either side, a later one
         // when its maximum exceeds m by more than kTau (every block holds a valid key: bm is finite)
         const bool move = kb == 0 ? fabsf(bm) > kTau : bm > kTau;
@@ -725,25 +745,12 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
             biased = true;
             scores(stc, sacc, Biased{});
             mask_tail();
+            expo();
         }
-        sh_h8 pf[4];                                 // numerators p = 2^acc, fp16, as the P.V MFMA operands
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) pf[2 * tt + (r >> 3)][r & 7] = (_Float16)sh_fast_exp2(sacc[tt][r]);
         if (kb == 0) {
             attn_stamp(stamp, last, 3);
             attn_stamp(stamp, last, 4);
         }
-        // V^T fragment j: substep j / DT, d tile j % DT (consecutive MFMAs alternate accumulators); read one ahead
-        auto vfrag = [&](int j) -> sh_h8 {
-            const uint32_t at = vaddr[j] + (uint32_t)st * STAGE;
-            const sh_s4 lo = sh_ds_read_tr(at);
-            const sh_s4 hi = sh_ds_read_tr(at + 8 * (DH * 2));
-            return __builtin_bit_cast(sh_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-        };
-        sh_h8 vq[2];
-        vq[0] = vfrag(0);
 #pragma unroll
         for (int sp = 0; sp < 4; ++sp) {
             const uint4 w = __builtin_bit_cast(uint4, pf[sp]);
@@ -754,8 +761,9 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
         }
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-            if (j + 1 < NJ) vq[(j + 1) & 1] = vfrag(j + 1);
-            oacc[j % DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vq[j & 1], pf[j / DT], oacc[j % DT], 0, 0, 0);
+            if (j + VA < NJ) vr[(j + VA) % (VA + 1)] = vfrag(j + VA);
+            __builtin_amdgcn_sched_barrier(0);       // (the read goes out before this MFMA, not after it)
+            oacc[j % DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vr[j % (VA + 1)], pf[j / DT], oacc[j % DT], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
