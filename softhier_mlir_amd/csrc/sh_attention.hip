@@ -533,7 +533,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a, ui
 // this drops the maximum pass (its score MFMAs, K fragment reads and K DMAs) and the refill of the ring between the
 // passes. Same LDS ring, fragment prefetch and occupancy as k_flash2.
 constexpr float kTau = 8.f;
-template <int DH, int NST, bool PF = false>
+template <int DH, int NST, bool PF = false, bool ST = true>
 __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, uint64_t *stamp) {
     constexpr int DC = DH / 8, NS = DH / 16, DT = DH / 32;
     constexpr int KCH = KB * DC;                     // 16-byte chunks per K (or V) block
@@ -557,8 +557,9 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
     const bool ragged = S % KB != 0;                 // the last key block is partial
     // stamps (profile): 0-2 start, 3-4 first key block done (the reference m set), 5 all blocks done, 6 stored;
     // 7 first workgroup
-    const bool last = stamp && t == 0 && qb == gridDim.x - 1 && h == gridDim.y - 1 && b == gridDim.z - 1;
-    attn_stamp(stamp, stamp && t == 0 && qb == 0 && h == 0 && b == 0, 7);
+    // (ST = false: a launch without a stamp buffer; the stamp code is compiled out)
+    const bool last = ST && stamp && t == 0 && qb == gridDim.x - 1 && h == gridDim.y - 1 && b == gridDim.z - 1;
+    attn_stamp(stamp, ST && stamp && t == 0 && qb == 0 && h == 0 && b == 0, 7);
     attn_stamp(stamp, last, 0);
     attn_stamp(stamp, last, 1);
     attn_stamp(stamp, last, 2);
@@ -934,12 +935,12 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
     } else if ((dh == 64 || dh == 128) && vec && impl != 2 && fold && (uint64_t)KB * (ldk > ldv ? ldk : ldv) * 2 < (1ull << 31)) {
         // (k_flash3 addresses a key block's rows as a scalar base plus 32-bit lane offsets)
         if (a.pfl0 | a.pfl1) {
-            if (dh == 64) go2(k_flash3<64, 2, true>, grid, 0);
-            else go2(k_flash3<128, 2, true>, grid, 0);
+            if (dh == 64) sp ? go2(k_flash3<64, 2, true, true>, grid, 0) : go2(k_flash3<64, 2, true, false>, grid, 0);
+            else sp ? go2(k_flash3<128, 2, true, true>, grid, 0) : go2(k_flash3<128, 2, true, false>, grid, 0);
             a.pfl0 = a.pfl1 = 0;                    // (this kernel reads the ranges itself: no pass after it)
         } else {
-            if (dh == 64) go2(k_flash3<64, 2>, grid, 0);
-            else go2(k_flash3<128, 2>, grid, 0);
+            if (dh == 64) sp ? go2(k_flash3<64, 2, false, true>, grid, 0) : go2(k_flash3<64, 2, false, false>, grid, 0);
+            else sp ? go2(k_flash3<128, 2, false, true>, grid, 0) : go2(k_flash3<128, 2, false, false>, grid, 0);
         }
     } else if ((dh == 64 || dh == 128) && vec) {
         if (dh == 64) fold ? go2(k_flash2<64, 2, false, true>, grid, 0) : go2(k_flash2<64, 2, false, false>, grid, 0);

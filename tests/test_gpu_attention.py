@@ -169,6 +169,24 @@ def test_profile_phase_stamps_are_monotone(lib, gpu, S):
     assert all(lib.sh_attention_profile(S, 64, p) == 0 for p in range(8))
 
 
+@pytest.mark.parametrize("S,dh", [(256, 64), (320, 64), (1024, 128)])
+def test_stamped_call_stores_the_bits_of_the_batched_call(lib, gpu, S, dh):
+    """sh_attention (a stamped launch: the build that writes the phase stamps) and sh_attention_batched with B=1 (the
+    build without any stamp code) store the same bits, ragged last key block included."""
+    import torch
+    H = 768 // dh
+    D = H * dh
+    q, k, v = (to_dev(data.normal((S, D), 60 + i)) for i in range(3))
+    O1, O2 = _zeros(S, D), _zeros(S, D)
+    sc = 1 / dh ** 0.5
+    assert lib.sh_attention(A(q), A(k), A(v), A(O1), S, D, H, D, D, D, D, sc, ALL) == 0, shops.last_error()
+    lib.sh_barrier_global()
+    assert lib.sh_attention_profile(S, dh, 6) > 0
+    assert lib.sh_attention_batched(A(q), A(k), A(v), A(O2), 1, S, D, H, D, D, D, D, 0, 0, 0, 0, sc, 0) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(O1.view(torch.int16), O2.view(torch.int16))
+
+
 @pytest.mark.parametrize("dh,scale", [(64, 0.125), (128, 0.088), (64, 1.0)])
 def test_batched_prefetch_stores_the_bits_of_batched(lib, gpu, dh, scale):
     """sh_attention_batched_prefetch with two ranges (unaligned ends, one of them larger than the lines the one-pass
