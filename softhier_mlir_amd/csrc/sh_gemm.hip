@@ -1052,13 +1052,16 @@ __global__ __launch_bounds__(256 * KG, MINW) void k_gemm5(GemmArgs a) {
         }
     };
 
-    const LnRows<FM> lnw = ln_rows<FM>(a, m0 + wm * TM);      // (before the first DMAs: no wait on them)
     if (KT > 0) {
 #pragma unroll
         for (int s = 0; s < NST - 1; ++s)
 #pragma unroll
             for (int d = 0; d < C::LOADS; ++d) dma(d, min(s, KT - 1), s);
     }
+    // the rows' fold factors: their partials are loaded after the first DMAs, so the two latencies overlap (loads
+    // complete in issue order, so the wait for the partials also sees those DMAs land)
+    __builtin_amdgcn_sched_barrier(0);
+    const LnRows<FM> lnw = ln_rows<FM>(a, m0 + wm * TM);
     for (int kt = 0; kt < KT; ++kt) {
         sh_wait_vmcnt<(NST - 2) * C::LOADS>();           // slice kt landed (this wave's share) ...
         sh_wait_lgkm0();                                 // ... and this wave's reads of slice kt - 1 are done
@@ -1282,13 +1285,16 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINW) void k_gemm6(GemmArgs a) {
         }
     };
 
-    const LnRows<FM> lnw = ln_rows<FM>(a, m0 + wm * TM);      // (before the first DMAs: no wait on them)
     if (KT > 0) {
 #pragma unroll
         for (int s = 0; s < NST - 1; ++s)
 #pragma unroll
             for (int d = 0; d < C::LOADS; ++d) dma(d, min(s, KT - 1), s);
     }
+    // the rows' fold factors: their partials are loaded after the first DMAs, so the two latencies overlap (loads
+    // complete in issue order, so the wait for the partials also sees those DMAs land)
+    __builtin_amdgcn_sched_barrier(0);
+    const LnRows<FM> lnw = ln_rows<FM>(a, m0 + wm * TM);
     for (int kt = 0; kt < KT; ++kt) {
         sh_wait_vmcnt<(NST - 2) * C::LOADS>();           // slice kt landed (this wave's share) ...
         sh_wait_lgkm0();                                 // ... and this wave's reads of slice kt - 1 are done
