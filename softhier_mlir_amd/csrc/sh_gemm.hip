@@ -916,8 +916,27 @@ struct Cfg5 {
 // (first range + second, as the reduction adds two partials) and runs the unsplit epilogue: the bits of the
 // two-partial path without the partials' HBM traffic or the reduction launch. One workgroup holds a CU, with two
 // wavefronts per SIMD where a tile grid of one workgroup per CU would leave one.
-template <int BM, int BN, int SK, int NST, bool WT, int MINW, bool SPLIT, bool PRE, int KG = 1>
-__global__ __launch_bounds__(256 * KG, MINW) void k_gemm5(GemmArgs a) {
+// EPI (unsplit builds of the encoder's tiles): the epilogue a call has, fixed at compile time so its flag tests
+// and the code behind them drop out (the same arithmetic and bits as EPI = 0, which reads every flag from the
+// arguments): 1 = LayerNorm fold with the fp32 row d, then GELU; 2 = LayerNorm fold with d; 3 = fp16 bias, residual
+// and row partials. gemm_epi_kind picks it for a call; the arguments' own fields still hold the pointers.
+enum { EPI_ANY = 0, EPI_FOLD_GELU = 1, EPI_FOLD = 2, EPI_BIAS_RES_STATS = 3 };
+template <int EPI>
+__device__ __forceinline__ GemmArgs gemm_epi_spec(const GemmArgs &in) {
+    GemmArgs a = in;
+    if constexpr (EPI == EPI_FOLD_GELU || EPI == EPI_FOLD) {
+        a.accumulate = 0; a.res = nullptr; a.bias_fp32 = 1; a.stats_out = nullptr;
+        a.act = EPI == EPI_FOLD_GELU ? SH_ACT_GELU : SH_ACT_NONE;
+    } else if constexpr (EPI == EPI_BIAS_RES_STATS) {
+        a.accumulate = 0; a.ln_stats = nullptr; a.ln_parts = 0; a.bias_fp32 = 0; a.act = SH_ACT_NONE;
+    }
+    return a;
+}
+
+template <int BM, int BN, int SK, int NST, bool WT, int MINW, bool SPLIT, bool PRE, int KG = 1, int EPI = EPI_ANY>
+__global__ __launch_bounds__(256 * KG, MINW) void k_gemm5(GemmArgs a_in) {
+    static_assert(EPI == EPI_ANY || (!SPLIT && KG == 1 && !WT), "epilogue builds are unsplit");
+    const GemmArgs a = gemm_epi_spec<EPI>(a_in);
     using C = Cfg5<BM, BN, SK, NST, WT>;
     constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, NS = C::NS, XCPR = C::XCPR;
     static_assert(KG == 1 || (KG == 2 && !SPLIT && 2 * C::LDS <= 160 * 1024 && 16 * FN * 1024 <= (int)C::LDS), "k groups");
@@ -1027,8 +1046,10 @@ __global__ __launch_bounds__(256 * KG, MINW) void k_gemm5(GemmArgs a) {
     constexpr bool PRE_B = PRE && FM * FN <= 12, PRE_RES = PRE && FM * FN <= 6 && (!STAGED || (MINW == 1 && KG == 1));
     uint4 bq[PRE_B ? FN : 1][2], rq[PRE_RES ? FM : 1][PRE_RES ? FN : 1][2];
     // (a GEMM that also writes row partials adds the residual in the chain, before them)
-    const bool stage_res = STAGED && !PRE_RES && !a.stats_out;
-    const bool pre_ok = PRE_B && grp == 0 && !a.accumulate && !(a.bias && a.bias_fp32) && (PRE_RES || stage_res || !a.res);
+    const bool has_stats = EPI == EPI_BIAS_RES_STATS ? true : EPI != EPI_ANY ? false : a.stats_out != nullptr;
+    const bool has_res = EPI == EPI_BIAS_RES_STATS ? true : EPI != EPI_ANY ? false : a.res != nullptr;
+    const bool stage_res = STAGED && !PRE_RES && !has_stats;
+    const bool pre_ok = PRE_B && grp == 0 && !a.accumulate && !(a.bias && a.bias_fp32) && (PRE_RES || stage_res || !has_res);
     auto prefetch = [&]() {
 #pragma unroll
         for (int j = 0; j < (PRE_B ? FN : 0); ++j)
@@ -1147,7 +1168,7 @@ __global__ __launch_bounds__(256 * KG, MINW) void k_gemm5(GemmArgs a) {
         } else {
             chain_chunks<BM, BN, FM, FN>(an, qc, m0, n0, wm, wn);
         }
-        if (a.stats_out) stats_zt<FM, FN>(a, qc, m0 + wm * TM, n0 + wn * TN);
+        if (has_stats) stats_zt<FM, FN>(a, qc, m0 + wm * TM, n0 + wn * TN);
         if constexpr (STAGED) {
             // every stage but slice KT - 1's holds no slice any more (only the clamped tail DMAs, each wavefront's
             // into its own slots): their last reads were slices <= KT - 2, finished before slice KT - 1's barrier
@@ -1509,6 +1530,7 @@ struct KCfg {
     bool wt = false; KernelFn wt_vec[2] = {nullptr, nullptr}, wt_scalar[2] = {nullptr, nullptr};
     bool reg = false;            // the unsplit epilogue applies a LayerNorm fold and writes row partials from registers
     KernelFn kg2 = nullptr;      // in-workgroup split-K over two equal K ranges (512 threads, two rings: 2 x lds bytes)
+    KernelFn epi[4] = {nullptr, nullptr, nullptr, nullptr};      // unsplit builds with the epilogue fixed (k_gemm5 EPI)
 };
 
 #define SH_KCFG(BM, BN, EFF) { BM, BN, 2, false, { k_gemm<BM, BN, true, false>, k_gemm<BM, BN, true, true> }, \
@@ -1532,6 +1554,20 @@ struct KCfg {
                                              { nullptr, nullptr }, Cfg5<BM, BN, SK, NST, false>::LDS, EFF, false, 256, \
                                              false, { nullptr, nullptr }, false, { nullptr, nullptr }, { nullptr, nullptr }, true, \
                                              k_gemm5<BM, BN, SK, NST, false, 1, false, true, 2> }
+// the same with the epilogue builds (the encoder's tiles)
+#define SH_KCFG5_EPI(BM, BN, SK, NST, W) { nullptr, k_gemm5<BM, BN, SK, NST, false, W, false, true, 1, EPI_FOLD_GELU>, \
+                                           k_gemm5<BM, BN, SK, NST, false, W, false, true, 1, EPI_FOLD>, \
+                                           k_gemm5<BM, BN, SK, NST, false, W, false, true, 1, EPI_BIAS_RES_STATS> }
+#define SH_KCFG5E(BM, BN, SK, NST, W, EFF) { BM, BN, NST, true, { k_gemm5<BM, BN, SK, NST, false, W, false, true>, \
+                                               k_gemm5<BM, BN, SK, NST, false, W, true, true> }, \
+                                             { nullptr, nullptr }, Cfg5<BM, BN, SK, NST, false>::LDS, EFF, false, 256, \
+                                             false, { nullptr, nullptr }, false, { nullptr, nullptr }, { nullptr, nullptr }, true, \
+                                             nullptr, SH_KCFG5_EPI(BM, BN, SK, NST, W) }
+#define SH_KCFG5KE(BM, BN, SK, NST, W, EFF) { BM, BN, NST, true, { k_gemm5<BM, BN, SK, NST, false, W, false, true>, \
+                                                k_gemm5<BM, BN, SK, NST, false, W, true, true> }, \
+                                              { nullptr, nullptr }, Cfg5<BM, BN, SK, NST, false>::LDS, EFF, false, 256, \
+                                              false, { nullptr, nullptr }, false, { nullptr, nullptr }, { nullptr, nullptr }, true, \
+                                              k_gemm5<BM, BN, SK, NST, false, 1, false, true, 2>, SH_KCFG5_EPI(BM, BN, SK, NST, W) }
 // eff = sustained fraction of the MFMA peak per CU measured for each tile on MI355X (tile-time model of
 // est_time below); it only ranks the configurations.
 KCfg g_cfgs[] = {
@@ -1552,7 +1588,7 @@ KCfg g_cfgs[] = {
     // LDS-lean tiles with MFMA / read / DMA interleaving (k_gemm5)
     SH_KCFG5(256, 192, 64, 2, 1, 0.38f),
     SH_KCFG5(128, 192, 64, 3, 1, 0.36f),
-    SH_KCFG5K(128, 192, 64, 2, 2, 0.36f),
+    SH_KCFG5KE(128, 192, 64, 2, 2, 0.36f),
     SH_KCFG5(128, 256, 64, 2, 1, 0.36f),
     // W^T operand (sh_gemm_ex_wt): 4 / 8 wavefronts, up to 256 x 384 tiles (k_gemm6)
     SH_KCFG6(256, 384, 2, 4, 64, 2, 2, false, false, 0.50f),
@@ -1569,13 +1605,16 @@ KCfg g_cfgs[] = {
     SH_KCFG6(128, 64, 2, 2, 32, 4, 2, false, true, 0.16f),
     SH_KCFG6(64, 128, 2, 2, 32, 4, 2, false, true, 0.16f),
     SH_KCFG6(128, 128, 2, 2, 32, 4, 2, true, true, 0.25f),
-    SH_KCFG5K(128, 192, 32, 4, 2, 0.36f),       // two workgroups per CU with a deeper ring of 32-k slices
+    SH_KCFG5KE(128, 192, 32, 4, 2, 0.36f),      // two workgroups per CU with a deeper ring of 32-k slices
     SH_KCFG5(128, 128, 32, 4, 2, 0.30f),
-    SH_KCFG5(128, 192, 32, 4, 1, 0.36f),        // one workgroup per CU: residual and bias loaded during the last slice
+    SH_KCFG5E(128, 192, 32, 4, 1, 0.36f),       // one workgroup per CU: residual and bias loaded during the last slice
 };
 #undef SH_KCFG
 #undef SH_KCFG2
 #undef SH_KCFG5
+#undef SH_KCFG5E
+#undef SH_KCFG5KE
+#undef SH_KCFG5_EPI
 #undef SH_KCFG5K
 #undef SH_KCFG6
 constexpr int kNumCfg = sizeof(g_cfgs) / sizeof(g_cfgs[0]);
@@ -1686,6 +1725,8 @@ void set_attrs(KCfg &c) {
         if (c.wt_scalar[v]) (void)hipFuncSetAttribute((const void *)c.wt_scalar[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
     }
     if (c.kg2) (void)hipFuncSetAttribute((const void *)c.kg2, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(2 * c.lds));
+    for (int k = 1; k < 4; ++k)
+        if (c.epi[k]) (void)hipFuncSetAttribute((const void *)c.epi[k], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
     c.attr_set = true;
 }
 
@@ -1743,6 +1784,22 @@ void tune_file_append(const TuneKey &k, int cfg) {
     fclose(f);
 }
 
+// The k_gemm5 epilogue build (EPI) for an unsplit call's epilogue, or 0 for the build that reads every flag:
+// the LayerNorm fold with its fp32 d row and GELU or nothing after it, or fp16 bias + residual + row partials.
+// SH_GEMM_EPI=0 keeps every call on the general build (tests compare the two).
+int gemm_epi_kind(const GemmArgs &a) {
+    if (a.accumulate || !a.bias || env_int("SH_GEMM_EPI", 1) == 0) return EPI_ANY;
+    if (a.ln_stats && a.bias_fp32 && !a.res && !a.stats_out)
+        return a.act == SH_ACT_GELU ? EPI_FOLD_GELU : a.act == SH_ACT_NONE ? EPI_FOLD : EPI_ANY;
+    if (!a.ln_stats && !a.bias_fp32 && a.res && a.stats_out && a.act == SH_ACT_NONE) return EPI_BIAS_RES_STATS;
+    return EPI_ANY;
+}
+// The kernel an unsplit, vector-path call of tile configuration c launches.
+KernelFn unsplit_kernel(const KCfg &c, const GemmArgs &a) {
+    const int ek = gemm_epi_kind(a);
+    return ek != EPI_ANY && c.epi[ek] ? c.epi[ek] : c.vec[0];
+}
+
 int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st, bool wt) {
     const bool reg_only = call.ln_stats != nullptr || call.stats_out != nullptr;
     static const int enabled = env_int("SH_GEMM_TUNE", 1);
@@ -1776,9 +1833,10 @@ int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st, bool wt) {
                 set_attrs(c);
                 set_grid(a, c);
                 const dim3 grid(grid_of(a));
-                if (round == 0) hipLaunchKernelGGL(c.vec[0], grid, dim3(c.threads), c.lds, st, a);     // warm-up
+                const KernelFn kf = unsplit_kernel(c, a);     // (the build the call itself would launch)
+                if (round == 0) hipLaunchKernelGGL(kf, grid, dim3(c.threads), c.lds, st, a);     // warm-up
                 (void)hipEventRecord(e0, st);
-                for (int rep = 0; rep < 2; ++rep) hipLaunchKernelGGL(c.vec[0], grid, dim3(c.threads), c.lds, st, a);
+                for (int rep = 0; rep < 2; ++rep) hipLaunchKernelGGL(kf, grid, dim3(c.threads), c.lds, st, a);
                 (void)hipEventRecord(e1, st);
                 float ms = 0.f;
                 ok = hipEventSynchronize(e1) == hipSuccess && hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
@@ -1903,6 +1961,7 @@ int launch(const GemmReq &r, const char *name) {
     KernelFn fn = kg2 ? c.kg2
                 : r.wt ? (c.v2 ? c.vec[split] : vec ? c.wt_vec[split] : c.wt_scalar[split])
                        : (c.v2 && !fast) ? c.tail[split] : (vec || c.v2) ? c.vec[split] : c.scalar[split];   // !fast: K % 64 != 0
+    if (!kg2 && !split && !r.wt && fast && c.v2) fn = unsplit_kernel(c, a);
     set_attrs(c);
     if (split) {
         const size_t ws = (size_t)splits * r.M * r.N * sizeof(float);

@@ -273,6 +273,42 @@ def test_row_partials_match_float64_and_agree_across_tiles(lib, gpu, monkeypatch
     assert refs.close(z0.view(np.float16), want)[0] == 0
 
 
+@pytest.mark.parametrize("cfg", [16, 32, 34])
+def test_epilogue_builds_store_the_bits_of_the_general_build(lib, gpu, cfg, monkeypatch):
+    """The tiles with epilogue builds (the epilogue fixed at compile time: fold + GELU, fold, bias + residual + row
+    partials) store the bits of the build that reads every flag from its arguments (SH_GEMM_EPI=0), outputs and row
+    partials alike, on partial tiles in M, and with the fold reading given statistics or row partials."""
+    import torch
+    M, N, K = 520, 768, 448
+    a, wh, bh, r = _producer(M, N, K, 170)
+    X, WH, BH, R = to_dev(a), to_dev(wh), to_dev(bh), to_dev(r)
+    _, w, g, be, b = _problem(M, N, N, 180)
+    W, G, BE, Bb = to_dev(w), to_dev(g), to_dev(be), to_dev(b)
+    monkeypatch.setenv("SH_GEMM_CFG", str(cfg))
+    out = {}
+    for gen in ("1", "0"):
+        monkeypatch.setenv("SH_GEMM_EPI", gen)
+        H = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        Pst = _empty32(M, N // 32, 2)
+        e = shops.epi(bias=A(BH), residual=A(R), ldr=N, stats_out=A(Pst))
+        assert lib.sh_gemm_ex(A(X), A(WH), A(H), M, N, K, K, N, N, None, e) == 0, shops.last_error()
+        WP, C, Dd, S = _fold(lib, H, W, G, BE, Bb, M, N, N)
+        zs = []
+        for act in (0, 1):
+            for given in (True, False):
+                Z = torch.empty((M, N), dtype=torch.float16, device="cuda")
+                e = (shops.epi(bias=A(Dd), bias_fmt=shops.SH_BIAS_FP32, act=act, ln_stats=A(S), ln_c=A(C)) if given else
+                     shops.epi(bias=A(Dd), bias_fmt=shops.SH_BIAS_FP32, act=act, ln_stats=A(Pst), ln_c=A(C),
+                               ln_parts=N // 32, ln_eps=EPS))
+                assert lib.sh_gemm_ex(A(H), A(WP), A(Z), M, N, N, N, N, N, None, e) == 0, shops.last_error()
+                zs.append(codes(Z))
+        out[gen] = (codes(H), to_np(Pst).view(np.uint32), zs)
+    assert np.array_equal(out["1"][0], out["0"][0])
+    assert np.array_equal(out["1"][1], out["0"][1])
+    for z1, z0 in zip(out["1"][2], out["0"][2]):
+        assert np.array_equal(z1, z0)
+
+
 @pytest.mark.parametrize("mean,act", [(0.7, 0), (0.7, 1), (60.0, 0)])
 def test_fold_from_row_partials(lib, gpu, mean, act):
     """The consumer of row partials (ln_parts = K / 32): H from a GEMM that wrote its partials, then the folded
