@@ -37,6 +37,13 @@ __device__ __forceinline__ float sh_dev_h2f(uint16_t h) {
 __device__ __forceinline__ uint16_t sh_dev_f2h(float f) {   // v_cvt_f16_f32: round to nearest even
     return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
+// The same for a value that must be rounded to fp32 first: without the empty asm the compiler may fold the
+// conversion into the fp32 multiply-add that produced the value (v_fma_mix*, one rounding instead of two) in one
+// build and not in another, and two kernels would then store different bits for the same operands.
+__device__ __forceinline__ uint16_t sh_dev_f2h_rr(float f) {
+    asm volatile("" : "+v"(f));
+    return sh_dev_f2h(f);
+}
 // Correctly rounded fp16 addition of packed pairs (v_pk_add_f16, round to nearest even). For fp16 operands
 // this equals rounding their fp32 sum to fp16: fp32 keeps 24 >= 2*11 + 2 significand bits, which makes the
 // double rounding exact (Figueroa, "When is double rounding innocuous?", SIGNUM 1995).

@@ -195,10 +195,10 @@ __device__ __forceinline__ uint32_t comp(const uint4 &q, int i) { return i == 0 
 // z = r16(z_old + p) [accumulate]; z = r16(z + bias); z = r16(gelu(z)); z = r16(z + residual).
 __device__ __forceinline__ uint16_t epi_chain(const GemmArgs &a, uint16_t p, uint32_t gm, uint32_t gn) {
     float v = sh_dev_h2f(p);
-    if (a.accumulate) v = sh_dev_h2f(sh_dev_f2h(v + sh_dev_h2f(a.z[(uint64_t)gm * a.ldz + gn])));
+    if (a.accumulate) v = sh_dev_h2f(sh_dev_f2h_rr(v + sh_dev_h2f(a.z[(uint64_t)gm * a.ldz + gn])));
     if (a.bias && !a.ln_stats) {
         const float b = a.bias_fp32 ? ((const float *)a.bias)[gn] : sh_dev_h2f(((const uint16_t *)a.bias)[gn]);
-        v = sh_dev_h2f(sh_dev_f2h(v + b));
+        v = sh_dev_h2f(sh_dev_f2h_rr(v + b));
     }
     if (a.act == SH_ACT_GELU) { const uint16_t h = sh_dev_f2h(v); v = sh_dev_h2f((uint16_t)sh_gelu_u32(h | ((uint32_t)h << 16))); }
     if (a.res) v += sh_dev_h2f(a.res[(uint64_t)gm * a.ldr + gn]);
@@ -222,7 +222,7 @@ __device__ __forceinline__ uint4 epi_chain8(const GemmArgs &a, uint4 q, const ui
                 const uint4 &bb = p < 2 ? b0 : b1;
                 const float lo = (float)h.x + __uint_as_float(comp(bb, (2 * p) & 3));
                 const float hi = (float)h.y + __uint_as_float(comp(bb, (2 * p + 1) & 3));
-                w[p] = __builtin_bit_cast(uint32_t, sh_h2{(_Float16)lo, (_Float16)hi});
+                w[p] = (uint32_t)sh_dev_f2h_rr(lo) | ((uint32_t)sh_dev_f2h_rr(hi) << 16);
             }
         } else {
 #pragma unroll
@@ -638,8 +638,8 @@ __device__ __forceinline__ void swap_halves(uint32_t &x, uint32_t &y) {
     y = r[1];
 }
 
-__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
-    return (uint32_t)sh_dev_f2h(lo) | ((uint32_t)sh_dev_f2h(hi) << 16);
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {     // (fp32 values rounded to fp16 once more)
+    return (uint32_t)sh_dev_f2h_rr(lo) | ((uint32_t)sh_dev_f2h_rr(hi) << 16);
 }
 
 // The LayerNorm fold on a wavefront's Z^T accumulators (block (i, j) of lane l: the row of ln's entry i, columns
@@ -927,8 +927,13 @@ __device__ __forceinline__ GemmArgs gemm_epi_spec(const GemmArgs &in) {
     if constexpr (EPI == EPI_FOLD_GELU || EPI == EPI_FOLD) {
         a.accumulate = 0; a.res = nullptr; a.bias_fp32 = 1; a.stats_out = nullptr;
         a.act = EPI == EPI_FOLD_GELU ? SH_ACT_GELU : SH_ACT_NONE;
+        __builtin_assume(a.bias != nullptr);      // (the launch picks these builds only for calls that have them)
+        __builtin_assume(a.ln_stats != nullptr);
     } else if constexpr (EPI == EPI_BIAS_RES_STATS) {
         a.accumulate = 0; a.ln_stats = nullptr; a.ln_parts = 0; a.bias_fp32 = 0; a.act = SH_ACT_NONE;
+        __builtin_assume(a.bias != nullptr);
+        __builtin_assume(a.res != nullptr);
+        __builtin_assume(a.stats_out != nullptr);
     }
     return a;
 }
@@ -1493,7 +1498,7 @@ __global__ __launch_bounds__(64) void k_splitk_reduce(GemmArgs a, ShDiv div, uin
         for (int e = 0; e < W; ++e) v[e] = ln_apply(a, st, v[e], gn + e);
     }
 #pragma unroll
-    for (int e = 0; e < W; ++e) out[e] = epi_chain(a, sh_dev_f2h(v[e]), gm, gn + e);
+    for (int e = 0; e < W; ++e) out[e] = epi_chain(a, sh_dev_f2h_rr(v[e]), gm, gn + e);
     if (VEC && a.stats_out) {                        // 4 consecutive threads hold the 32 columns of one partial
         float x[W], sum = 0.f;
 #pragma unroll
