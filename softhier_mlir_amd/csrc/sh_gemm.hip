@@ -639,7 +639,8 @@ __device__ __forceinline__ void swap_halves(uint32_t &x, uint32_t &y) {
 }
 
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {     // (fp32 values rounded to fp16 once more)
-    return (uint32_t)sh_dev_f2h_rr(lo) | ((uint32_t)sh_dev_f2h_rr(hi) << 16);
+    asm volatile("" : "+v"(lo), "+v"(hi));           // (as sh_dev_f2h_rr: no conversion folded into the producer)
+    return __builtin_bit_cast(uint32_t, sh_h2{(_Float16)lo, (_Float16)hi});
 }
 
 // The LayerNorm fold on a wavefront's Z^T accumulators (block (i, j) of lane l: the row of ln's entry i, columns
