@@ -920,8 +920,10 @@ struct Cfg5 {
 // EPI (unsplit builds of the encoder's tiles): the epilogue a call has, fixed at compile time so its flag tests
 // and the code behind them drop out (the same arithmetic and bits as EPI = 0, which reads every flag from the
 // arguments): 1 = LayerNorm fold with the fp32 row d, then GELU; 2 = LayerNorm fold with d; 3 = fp16 bias, residual
-// and row partials. gemm_epi_kind picks it for a call; the arguments' own fields still hold the pointers.
-enum { EPI_ANY = 0, EPI_FOLD_GELU = 1, EPI_FOLD = 2, EPI_BIAS_RES_STATS = 3 };
+// and row partials; 4 = fp16 bias; 5 = fp16 bias, then GELU; 6 = fp16 bias and residual. gemm_epi_kind picks it for
+// a call; the arguments' own fields still hold the pointers.
+enum { EPI_ANY = 0, EPI_FOLD_GELU = 1, EPI_FOLD = 2, EPI_BIAS_RES_STATS = 3, EPI_BIAS = 4, EPI_BIAS_GELU = 5,
+       EPI_BIAS_RES = 6, EPI_KINDS = 7 };
 template <int EPI>
 __device__ __forceinline__ GemmArgs gemm_epi_spec(const GemmArgs &in) {
     GemmArgs a = in;
@@ -935,6 +937,12 @@ __device__ __forceinline__ GemmArgs gemm_epi_spec(const GemmArgs &in) {
         __builtin_assume(a.bias != nullptr);
         __builtin_assume(a.res != nullptr);
         __builtin_assume(a.stats_out != nullptr);
+    } else if constexpr (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU || EPI == EPI_BIAS_RES) {
+        a.accumulate = 0; a.ln_stats = nullptr; a.ln_parts = 0; a.bias_fp32 = 0; a.stats_out = nullptr;
+        a.act = EPI == EPI_BIAS_GELU ? SH_ACT_GELU : SH_ACT_NONE;
+        __builtin_assume(a.bias != nullptr);
+        if constexpr (EPI == EPI_BIAS_RES) __builtin_assume(a.res != nullptr);
+        else a.res = nullptr;
     }
     return a;
 }
@@ -1053,7 +1061,7 @@ __global__ __launch_bounds__(256 * KG, MINW) void k_gemm5(GemmArgs a_in) {
     uint4 bq[PRE_B ? FN : 1][2], rq[PRE_RES ? FM : 1][PRE_RES ? FN : 1][2];
     // (a GEMM that also writes row partials adds the residual in the chain, before them)
     const bool has_stats = EPI == EPI_BIAS_RES_STATS ? true : EPI != EPI_ANY ? false : a.stats_out != nullptr;
-    const bool has_res = EPI == EPI_BIAS_RES_STATS ? true : EPI != EPI_ANY ? false : a.res != nullptr;
+    const bool has_res = (EPI == EPI_BIAS_RES_STATS || EPI == EPI_BIAS_RES) ? true : EPI != EPI_ANY ? false : a.res != nullptr;
     const bool stage_res = STAGED && !PRE_RES && !has_stats;
     const bool pre_ok = PRE_B && grp == 0 && !a.accumulate && !(a.bias && a.bias_fp32) && (PRE_RES || stage_res || !has_res);
     auto prefetch = [&]() {
@@ -1536,7 +1544,7 @@ struct KCfg {
     bool wt = false; KernelFn wt_vec[2] = {nullptr, nullptr}, wt_scalar[2] = {nullptr, nullptr};
     bool reg = false;            // the unsplit epilogue applies a LayerNorm fold and writes row partials from registers
     KernelFn kg2 = nullptr;      // in-workgroup split-K over two equal K ranges (512 threads, two rings: 2 x lds bytes)
-    KernelFn epi[4] = {nullptr, nullptr, nullptr, nullptr};      // unsplit builds with the epilogue fixed (k_gemm5 EPI)
+    KernelFn epi[EPI_KINDS] = {};     // unsplit builds with the epilogue fixed (k_gemm5 EPI)
 };
 
 #define SH_KCFG(BM, BN, EFF) { BM, BN, 2, false, { k_gemm<BM, BN, true, false>, k_gemm<BM, BN, true, true> }, \
@@ -1563,7 +1571,10 @@ struct KCfg {
 // the same with the epilogue builds (the encoder's tiles)
 #define SH_KCFG5_EPI(BM, BN, SK, NST, W) { nullptr, k_gemm5<BM, BN, SK, NST, false, W, false, true, 1, EPI_FOLD_GELU>, \
                                            k_gemm5<BM, BN, SK, NST, false, W, false, true, 1, EPI_FOLD>, \
-                                           k_gemm5<BM, BN, SK, NST, false, W, false, true, 1, EPI_BIAS_RES_STATS> }
+                                           k_gemm5<BM, BN, SK, NST, false, W, false, true, 1, EPI_BIAS_RES_STATS>, \
+                                           k_gemm5<BM, BN, SK, NST, false, W, false, true, 1, EPI_BIAS>, \
+                                           k_gemm5<BM, BN, SK, NST, false, W, false, true, 1, EPI_BIAS_GELU>, \
+                                           k_gemm5<BM, BN, SK, NST, false, W, false, true, 1, EPI_BIAS_RES> }
 #define SH_KCFG5E(BM, BN, SK, NST, W, EFF) { BM, BN, NST, true, { k_gemm5<BM, BN, SK, NST, false, W, false, true>, \
                                                k_gemm5<BM, BN, SK, NST, false, W, true, true> }, \
                                              { nullptr, nullptr }, Cfg5<BM, BN, SK, NST, false>::LDS, EFF, false, 256, \
@@ -1731,7 +1742,7 @@ void set_attrs(KCfg &c) {
         if (c.wt_scalar[v]) (void)hipFuncSetAttribute((const void *)c.wt_scalar[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
     }
     if (c.kg2) (void)hipFuncSetAttribute((const void *)c.kg2, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(2 * c.lds));
-    for (int k = 1; k < 4; ++k)
+    for (int k = 1; k < EPI_KINDS; ++k)
         if (c.epi[k]) (void)hipFuncSetAttribute((const void *)c.epi[k], hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
     c.attr_set = true;
 }
@@ -1791,14 +1802,18 @@ void tune_file_append(const TuneKey &k, int cfg) {
 }
 
 // The k_gemm5 epilogue build (EPI) for an unsplit call's epilogue, or 0 for the build that reads every flag:
-// the LayerNorm fold with its fp32 d row and GELU or nothing after it, or fp16 bias + residual + row partials.
-// SH_GEMM_EPI=0 keeps every call on the general build (tests compare the two).
+// the LayerNorm fold with its fp32 d row and GELU or nothing after it; fp16 bias + residual + row partials; fp16
+// bias alone, with GELU after it, or with a residual. SH_GEMM_EPI=0 keeps every call on the general build (tests
+// compare the two).
 int gemm_epi_kind(const GemmArgs &a) {
     if (a.accumulate || !a.bias || env_int("SH_GEMM_EPI", 1) == 0) return EPI_ANY;
     if (a.ln_stats && a.bias_fp32 && !a.res && !a.stats_out)
         return a.act == SH_ACT_GELU ? EPI_FOLD_GELU : a.act == SH_ACT_NONE ? EPI_FOLD : EPI_ANY;
-    if (!a.ln_stats && !a.bias_fp32 && a.res && a.stats_out && a.act == SH_ACT_NONE) return EPI_BIAS_RES_STATS;
-    return EPI_ANY;
+    if (a.ln_stats || a.bias_fp32) return EPI_ANY;
+    if (a.res && a.stats_out) return a.act == SH_ACT_NONE ? EPI_BIAS_RES_STATS : EPI_ANY;
+    if (a.stats_out) return EPI_ANY;
+    if (a.res) return a.act == SH_ACT_NONE ? EPI_BIAS_RES : EPI_ANY;
+    return a.act == SH_ACT_GELU ? EPI_BIAS_GELU : a.act == SH_ACT_NONE ? EPI_BIAS : EPI_ANY;
 }
 // The kernel an unsplit, vector-path call of tile configuration c launches.
 KernelFn unsplit_kernel(const KCfg &c, const GemmArgs &a) {

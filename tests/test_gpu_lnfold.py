@@ -276,8 +276,9 @@ def test_row_partials_match_float64_and_agree_across_tiles(lib, gpu, monkeypatch
 @pytest.mark.parametrize("cfg", [16, 32, 34])
 def test_epilogue_builds_store_the_bits_of_the_general_build(lib, gpu, cfg, monkeypatch):
     """The tiles with epilogue builds (the epilogue fixed at compile time: fold + GELU, fold, bias + residual + row
-    partials) store the bits of the build that reads every flag from its arguments (SH_GEMM_EPI=0), outputs and row
-    partials alike, on partial tiles in M, and with the fold reading given statistics or row partials."""
+    partials, fp16 bias, bias + GELU, bias + residual) store the bits of the build that reads every flag from its
+    arguments (SH_GEMM_EPI=0), outputs and row partials alike, on partial tiles in M, and with the fold reading given
+    statistics or row partials."""
     import torch
     M, N, K = 520, 768, 448
     a, wh, bh, r = _producer(M, N, K, 170)
@@ -302,6 +303,11 @@ def test_epilogue_builds_store_the_bits_of_the_general_build(lib, gpu, cfg, monk
                                ln_parts=N // 32, ln_eps=EPS))
                 assert lib.sh_gemm_ex(A(H), A(WP), A(Z), M, N, N, N, N, N, None, e) == 0, shops.last_error()
                 zs.append(codes(Z))
+        for e in (shops.epi(bias=A(BH)), shops.epi(bias=A(BH), act=shops.SH_ACT_GELU),        # fp16 bias builds
+                  shops.epi(bias=A(BH), residual=A(R), ldr=N)):
+            Z = torch.empty((M, N), dtype=torch.float16, device="cuda")
+            assert lib.sh_gemm_ex(A(X), A(WH), A(Z), M, N, K, K, N, N, None, e) == 0, shops.last_error()
+            zs.append(codes(Z))
         out[gen] = (codes(H), to_np(Pst).view(np.uint32), zs)
     assert np.array_equal(out["1"][0], out["0"][0])
     assert np.array_equal(out["1"][1], out["0"][1])
