@@ -920,10 +920,10 @@ struct Cfg5 {
 // EPI (unsplit builds of the encoder's tiles): the epilogue a call has, fixed at compile time so its flag tests
 // and the code behind them drop out (the same arithmetic and bits as EPI = 0, which reads every flag from the
 // arguments): 1 = LayerNorm fold with the fp32 row d, then GELU; 2 = LayerNorm fold with d; 3 = fp16 bias, residual
-// and row partials; 4 = fp16 bias; 5 = fp16 bias, then GELU; 6 = fp16 bias and residual. gemm_epi_kind picks it for
-// a call; the arguments' own fields still hold the pointers.
+// and row partials; 4 = fp16 bias; 5 = fp16 bias, then GELU; 6 = fp16 bias and residual; 7 = none (the product
+// alone). gemm_epi_kind picks it for a call; the arguments' own fields still hold the pointers.
 enum { EPI_ANY = 0, EPI_FOLD_GELU = 1, EPI_FOLD = 2, EPI_BIAS_RES_STATS = 3, EPI_BIAS = 4, EPI_BIAS_GELU = 5,
-       EPI_BIAS_RES = 6, EPI_KINDS = 7 };
+       EPI_BIAS_RES = 6, EPI_PLAIN = 7, EPI_KINDS = 8 };
 template <int EPI>
 __device__ __forceinline__ GemmArgs gemm_epi_spec(const GemmArgs &in) {
     GemmArgs a = in;
@@ -943,6 +943,9 @@ __device__ __forceinline__ GemmArgs gemm_epi_spec(const GemmArgs &in) {
         __builtin_assume(a.bias != nullptr);
         if constexpr (EPI == EPI_BIAS_RES) __builtin_assume(a.res != nullptr);
         else a.res = nullptr;
+    } else if constexpr (EPI == EPI_PLAIN) {
+        a.accumulate = 0; a.ln_stats = nullptr; a.ln_parts = 0; a.bias = nullptr; a.bias_fp32 = 0; a.stats_out = nullptr;
+        a.act = SH_ACT_NONE; a.res = nullptr;
     }
     return a;
 }
@@ -1574,7 +1577,8 @@ struct KCfg {
                                            k_gemm5<BM, BN, SK, NST, false, W, false, true, 1, EPI_BIAS_RES_STATS>, \
                                            k_gemm5<BM, BN, SK, NST, false, W, false, true, 1, EPI_BIAS>, \
                                            k_gemm5<BM, BN, SK, NST, false, W, false, true, 1, EPI_BIAS_GELU>, \
-                                           k_gemm5<BM, BN, SK, NST, false, W, false, true, 1, EPI_BIAS_RES> }
+                                           k_gemm5<BM, BN, SK, NST, false, W, false, true, 1, EPI_BIAS_RES>, \
+                                           k_gemm5<BM, BN, SK, NST, false, W, false, true, 1, EPI_PLAIN> }
 #define SH_KCFG5E(BM, BN, SK, NST, W, EFF) { BM, BN, NST, true, { k_gemm5<BM, BN, SK, NST, false, W, false, true>, \
                                                k_gemm5<BM, BN, SK, NST, false, W, true, true> }, \
                                              { nullptr, nullptr }, Cfg5<BM, BN, SK, NST, false>::LDS, EFF, false, 256, \
@@ -1803,10 +1807,11 @@ void tune_file_append(const TuneKey &k, int cfg) {
 
 // The k_gemm5 epilogue build (EPI) for an unsplit call's epilogue, or 0 for the build that reads every flag:
 // the LayerNorm fold with its fp32 d row and GELU or nothing after it; fp16 bias + residual + row partials; fp16
-// bias alone, with GELU after it, or with a residual. SH_GEMM_EPI=0 keeps every call on the general build (tests
-// compare the two).
+// bias alone, with GELU after it, or with a residual; none. SH_GEMM_EPI=0 keeps every call on the general build
+// (tests compare the two).
 int gemm_epi_kind(const GemmArgs &a) {
-    if (a.accumulate || !a.bias || env_int("SH_GEMM_EPI", 1) == 0) return EPI_ANY;
+    if (a.accumulate || env_int("SH_GEMM_EPI", 1) == 0) return EPI_ANY;
+    if (!a.bias) return !a.ln_stats && !a.res && !a.stats_out && a.act == SH_ACT_NONE ? EPI_PLAIN : EPI_ANY;
     if (a.ln_stats && a.bias_fp32 && !a.res && !a.stats_out)
         return a.act == SH_ACT_GELU ? EPI_FOLD_GELU : a.act == SH_ACT_NONE ? EPI_FOLD : EPI_ANY;
     if (a.ln_stats || a.bias_fp32) return EPI_ANY;

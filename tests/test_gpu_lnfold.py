@@ -276,7 +276,7 @@ def test_row_partials_match_float64_and_agree_across_tiles(lib, gpu, monkeypatch
 @pytest.mark.parametrize("cfg", [16, 32, 34])
 def test_epilogue_builds_store_the_bits_of_the_general_build(lib, gpu, cfg, monkeypatch):
     """The tiles with epilogue builds (the epilogue fixed at compile time: fold + GELU, fold, bias + residual + row
-    partials, fp16 bias, bias + GELU, bias + residual) store the bits of the build that reads every flag from its
+    partials, fp16 bias, bias + GELU, bias + residual, none) store the bits of the build that reads every flag from its
     arguments (SH_GEMM_EPI=0), outputs and row partials alike, on partial tiles in M, and with the fold reading given
     statistics or row partials."""
     import torch
@@ -304,7 +304,7 @@ def test_epilogue_builds_store_the_bits_of_the_general_build(lib, gpu, cfg, monk
                 assert lib.sh_gemm_ex(A(H), A(WP), A(Z), M, N, N, N, N, N, None, e) == 0, shops.last_error()
                 zs.append(codes(Z))
         for e in (shops.epi(bias=A(BH)), shops.epi(bias=A(BH), act=shops.SH_ACT_GELU),        # fp16 bias builds
-                  shops.epi(bias=A(BH), residual=A(R), ldr=N)):
+                  shops.epi(bias=A(BH), residual=A(R), ldr=N), shops.epi()):                 # and none
             Z = torch.empty((M, N), dtype=torch.float16, device="cuda")
             assert lib.sh_gemm_ex(A(X), A(WH), A(Z), M, N, K, K, N, N, None, e) == 0, shops.last_error()
             zs.append(codes(Z))
