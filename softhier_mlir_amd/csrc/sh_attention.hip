@@ -533,7 +533,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a, ui
 // this drops the maximum pass (its score MFMAs, K fragment reads and K DMAs) and the refill of the ring between the
 // passes. Same LDS ring, fragment prefetch and occupancy as k_flash2.
 constexpr float kTau = 8.f;
-template <int DH, int NST, bool PF = false, bool ST = true>
+template <int DH, int NST, bool PF = false, bool ST = true, bool RAG = true>
 __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, uint64_t *stamp) {
     constexpr int DC = DH / 8, NS = DH / 16, DT = DH / 32;
     constexpr int KCH = KB * DC;                     // 16-byte chunks per K (or V) block
@@ -554,7 +554,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
     uint16_t *O = a.o + b * a.bso + (uint64_t)h * DH;
     const uint32_t qw0 = qb * QPB + wave * QPW, myq = qw0 + r32;
     const uint32_t nkb = (S + KB - 1) / KB;
-    const bool ragged = S % KB != 0;                 // the last key block is partial
+    const bool ragged = RAG && S % KB != 0;       // the last key block is partial (RAG = false: S % 64 == 0, no tail code)
     // stamps (profile): 0-2 start, 3-4 first key block done (the reference m set), 5 all blocks done, 6 stored;
     // 7 first workgroup
     // (ST = false: a launch without a stamp buffer; the stamp code is compiled out)
@@ -938,9 +938,12 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
             if (dh == 64) sp ? go2(k_flash3<64, 2, true, true>, grid, 0) : go2(k_flash3<64, 2, true, false>, grid, 0);
             else sp ? go2(k_flash3<128, 2, true, true>, grid, 0) : go2(k_flash3<128, 2, true, false>, grid, 0);
             a.pfl0 = a.pfl1 = 0;                    // (this kernel reads the ranges itself: no pass after it)
-        } else {
+        } else if (sp || S % KB != 0) {
             if (dh == 64) sp ? go2(k_flash3<64, 2, false, true>, grid, 0) : go2(k_flash3<64, 2, false, false>, grid, 0);
             else sp ? go2(k_flash3<128, 2, false, true>, grid, 0) : go2(k_flash3<128, 2, false, false>, grid, 0);
+        } else {                                    // (whole key blocks: the build without the ragged-tail code)
+            if (dh == 64) go2((k_flash3<64, 2, false, false, false>), grid, 0);
+            else go2((k_flash3<128, 2, false, false, false>), grid, 0);
         }
     } else if ((dh == 64 || dh == 128) && vec) {
         if (dh == 64) fold ? go2(k_flash2<64, 2, false, true>, grid, 0) : go2(k_flash2<64, 2, false, false>, grid, 0);
