@@ -935,8 +935,13 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
     } else if ((dh == 64 || dh == 128) && vec && impl != 2 && fold && (uint64_t)KB * (ldk > ldv ? ldk : ldv) * 2 < (1ull << 31)) {
         // (k_flash3 addresses a key block's rows as a scalar base plus 32-bit lane offsets)
         if (a.pfl0 | a.pfl1) {
-            if (dh == 64) sp ? go2(k_flash3<64, 2, true, true>, grid, 0) : go2(k_flash3<64, 2, true, false>, grid, 0);
-            else sp ? go2(k_flash3<128, 2, true, true>, grid, 0) : go2(k_flash3<128, 2, true, false>, grid, 0);
+            if (sp || S % KB != 0) {
+                if (dh == 64) sp ? go2(k_flash3<64, 2, true, true>, grid, 0) : go2(k_flash3<64, 2, true, false>, grid, 0);
+                else sp ? go2(k_flash3<128, 2, true, true>, grid, 0) : go2(k_flash3<128, 2, true, false>, grid, 0);
+            } else {
+                if (dh == 64) go2((k_flash3<64, 2, true, false, false>), grid, 0);
+                else go2((k_flash3<128, 2, true, false, false>), grid, 0);
+            }
             a.pfl0 = a.pfl1 = 0;                    // (this kernel reads the ranges itself: no pass after it)
         } else if (sp || S % KB != 0) {
             if (dh == 64) sp ? go2(k_flash3<64, 2, false, true>, grid, 0) : go2(k_flash3<64, 2, false, false>, grid, 0);
