@@ -115,18 +115,6 @@ __device__ __forceinline__ void sh_wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt");
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
-// The same for a count known only after loop unrolling (a switch the compiler folds to one s_waitcnt); n < 32.
-__device__ __forceinline__ void sh_wait_vmcnt_n(int n) {
-#define SH_VMC(N) case N: sh_wait_vmcnt<N>(); break;
-    switch (n) {
-        SH_VMC(0) SH_VMC(1) SH_VMC(2) SH_VMC(3) SH_VMC(4) SH_VMC(5) SH_VMC(6) SH_VMC(7)
-        SH_VMC(8) SH_VMC(9) SH_VMC(10) SH_VMC(11) SH_VMC(12) SH_VMC(13) SH_VMC(14) SH_VMC(15)
-        SH_VMC(16) SH_VMC(17) SH_VMC(18) SH_VMC(19) SH_VMC(20) SH_VMC(21) SH_VMC(22) SH_VMC(23)
-        SH_VMC(24) SH_VMC(25) SH_VMC(26) SH_VMC(27) SH_VMC(28) SH_VMC(29) SH_VMC(30) SH_VMC(31)
-        default: sh_wait_vmcnt<0>(); break;
-    }
-#undef SH_VMC
-}
 // s_waitcnt lgkmcnt(0) with vmcnt / expcnt left unconstrained.
 __device__ __forceinline__ void sh_wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
