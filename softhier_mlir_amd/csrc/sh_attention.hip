@@ -19,6 +19,7 @@
 // per-query kernel.
 #include "sh_common.h"
 #include <hip/hip_ext.h>
+#include <algorithm>
 #include <chrono>
 #include <type_traits>
 
@@ -38,6 +39,7 @@ struct AttnArgs {
     const uint16_t *tok;            // token classes of the S positions (sh_ops.h:277-282), or null: no mask
     uint32_t grp;                   // query heads per key/value head (GQA); 1 for plain multi-head attention
     uint32_t xcds;                  // > 1: the query blocks of one head run on one XCD (see attn_item)
+    uint64_t mx, mgx, mgy;          // with xcds > 1: ceil(2^32 / d) for d = xcds, gridDim.x, gridDim.y (attn_item)
     // sh_attention_batched_prefetch: two ranges of 64-byte lines (line-aligned bases, line counts) that k_flash3
     // reads into the caches while it runs; zero counts: none
     const uint8_t *pf0, *pf1;
@@ -48,13 +50,17 @@ struct AttnArgs {
 // and every query block of a head reads the same K / V, so with `xcds` > 1 the flat block id L is remapped to
 // keep a head's query blocks on one XCD, back to back (L % X picks the XCD, L / X the position in its queue),
 // and the second block's K / V reads hit that XCD's L2. Needs (heads x sequences) % X == 0.
+// (the quotients by multiply-high with the host's ceil(2^32 / d), exact for n d < 2^32, which the host checks: scalar
+// instructions where a division would take ~10 vector ones)
+__device__ __forceinline__ uint32_t attn_div(uint32_t n, uint64_t m) { return (uint32_t)(((uint64_t)n * m) >> 32); }
 __device__ __forceinline__ void attn_item(const AttnArgs &a, uint32_t &qb, uint32_t &h, uint32_t &b) {
     qb = blockIdx.x; h = blockIdx.y; b = blockIdx.z;
     if (a.xcds > 1) {
         const uint32_t gx = gridDim.x, gy = gridDim.y;
         const uint32_t L = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
-        const uint32_t j = L / a.xcds, hb = (j / gx) * a.xcds + L % a.xcds;
-        qb = j % gx; h = hb % gy; b = hb / gy;
+        const uint32_t j = attn_div(L, a.mx), jx = attn_div(j, a.mgx);
+        const uint32_t hb = jx * a.xcds + (L - j * a.xcds), hy = attn_div(hb, a.mgy);
+        qb = j - jx * gx; h = hb - hy * gy; b = hy;
     }
 }
 constexpr uint32_t kLlmPad = 0xFFFFu;   // SH_LLM_PAD: a padding position
@@ -618,10 +624,18 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
     sh_h8 qf[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) qf[s] = __builtin_bit_cast(sh_h8, ld8<true>(Q, a.ldq, myq, 16 * s + 8 * g, S, DH));
+    // (c q as a multiply-add with +0, which reads the fp16 value directly and equals the product but for the sign
+    // of a zero, which no score or exponential sees; the empty asm keeps each fp32 value rounded to fp32 before
+    // one paired fp16 conversion, so the multiply-add is not fused into a single-rounding conversion)
 #pragma unroll
     for (int s = 0; s < NS; ++s)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qf[s][e] = (_Float16)((float)qf[s][e] * a.c);
+        for (int e = 0; e < 8; e += 2) {
+            float lo = __builtin_fmaf((float)qf[s][e], a.c, 0.f), hi = __builtin_fmaf((float)qf[s][e + 1], a.c, 0.f);
+            asm volatile("" : "+v"(lo), "+v"(hi));
+            qf[s][e] = (_Float16)lo;
+            qf[s][e + 1] = (_Float16)hi;
+        }
     // operands of the bias step (k elements 0 and 1 of lane group 0): ones for every key, -m_hi, -m_lo of this
     // lane's query (set from the running maximum)
     sh_h8 kbias = {}, qbias = {};
@@ -889,7 +903,14 @@ int run(uint64_t q, uint64_t k, uint64_t v, uint64_t o, uint32_t B, uint32_t S, 
     {
         static const int remap = [] { const char *e = getenv("SH_ATTN_XCD"); return (e && *e) ? atoi(e) : 1; }();
         const uint32_t X = (uint32_t)sh_num_xcds();
-        if (remap && X > 1 && sh_cdiv(S, QPB) > 1 && ((uint64_t)H * B) % X == 0) a.xcds = X;
+        const uint64_t gx = sh_cdiv(S, QPB), blocks = gx * H * B, dmax = std::max<uint64_t>(std::max<uint64_t>(X, gx), H);
+        if (remap && X > 1 && gx > 1 && ((uint64_t)H * B) % X == 0 && blocks * dmax < (1ull << 32)) {
+            auto magic = [](uint64_t d) { return ((1ull << 32) + d - 1) / d; };
+            a.xcds = X;
+            a.mx = magic(X);
+            a.mgx = magic(gx);
+            a.mgy = magic(H);
+        }
     }
     hipStream_t st = sh_stream();
     if (!g_prof.e0) {
