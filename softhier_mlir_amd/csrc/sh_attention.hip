@@ -676,9 +676,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
         }
     };
 
-    sh_f16v oacc[DT];
-#pragma unroll
-    for (int i = 0; i < DT; ++i) oacc[i] = sh_f16v{};
+    sh_f16v oacc[DT];                                // (set by the first block's P.V MFMAs, which start from zero)
     float lsum = 0.f;                                // this lane's keys' fp16 numerators, summed in fp32
     float mrun = 0.f;                                // reference m of this lane's query (c s units)
     bool biased = false;                             // some lane's m left 0 (wave-uniform): the bias step is needed
@@ -697,9 +695,11 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
     using Stage0 = std::integral_constant<int, 0>;
     using Stage1 = std::integral_constant<int, 1>;
     using Biased = std::true_type;
-    // key block kb, held in ring stage kb % 2 (= the compile-time stage of stc)
-    auto step = [&](uint32_t kb, auto stc) {
+    // key block kb, held in ring stage kb % 2 (= the compile-time stage of stc); first_c: kb == 0, a separate build
+    // of the step (O and l hold nothing yet: no rescale, and its P.V MFMAs start from a zero accumulator operand)
+    auto step = [&](uint32_t kb, auto stc, auto first_c) {
         constexpr int st = decltype(stc)::value;
+        constexpr bool first = decltype(first_c)::value;
         sh_wait_vmcnt<(NST - 2) * 2 * KR>();
         __syncthreads();
         issue(min(kb + NST - 1, nkb - 1), (st + NST - 1) % NST);
@@ -746,15 +746,17 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
         const float bm = sh_max_xor32(fmaxf(b0, b1));
         // m starts at 0; the first block moves it when its maximum is more than kTau away on either side, a later one
         // when its maximum exceeds m by more than kTau (every block holds a valid key: bm is finite)
-        const bool move = kb == 0 ? fabsf(bm) > kTau : bm > kTau;
+        const bool move = first ? fabsf(bm) > kTau : bm > kTau;
         if (__ballot(move) != 0) {                   // wave-uniform: m moves, O and l rescale, scores again
             const float shift = move ? bm : 0.f;
-            // before the first block O and l are still zero: nothing to rescale (2^-shift overflows to +inf for a
+            // before the first block O and l are still empty: nothing to rescale (2^-shift overflows to +inf for a
             // first-block maximum below -128, and 0 x inf would be NaN)
-            const float sc = kb == 0 ? 1.f : sh_fast_exp2(-shift);
+            if constexpr (!first) {
+                const float sc = sh_fast_exp2(-shift);
 #pragma unroll
-            for (int i = 0; i < DT; ++i) oacc[i] *= sc;
-            lsum *= sc;
+                for (int i = 0; i < DT; ++i) oacc[i] *= sc;
+                lsum *= sc;
+            }
             mrun += shift;
             set_bias(mrun);
             biased = true;
@@ -762,7 +764,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
             mask_tail();
             expo();
         }
-        if (kb == 0) {
+        if constexpr (first) {
             attn_stamp(stamp, last, 3);
             attn_stamp(stamp, last, 4);
         }
@@ -778,13 +780,15 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
         for (int j = 0; j < NJ; ++j) {
             if (j + VA < NJ) vr[(j + VA) % (VA + 1)] = vfrag(j + VA);
             __builtin_amdgcn_sched_barrier(0);       // (the read goes out before this MFMA, not after it)
-            oacc[j % DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vr[j % (VA + 1)], pf[j / DT], oacc[j % DT], 0, 0, 0);
+            if (first && j < DT) oacc[j % DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vr[j % (VA + 1)], pf[j / DT], sh_f16v{}, 0, 0, 0);
+            else oacc[j % DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vr[j % (VA + 1)], pf[j / DT], oacc[j % DT], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    for (uint32_t kb = 0; kb < nkb; kb += 2) {
-        step(kb, Stage0{});
-        if (kb + 1 < nkb) step(kb + 1, Stage1{});
+    step(0u, Stage0{}, std::true_type{});            // (S > 0: the host launches no empty sequence)
+    for (uint32_t kb = 1; kb < nkb; kb += 2) {
+        step(kb, Stage1{}, std::false_type{});
+        if (kb + 1 < nkb) step(kb + 1, Stage0{}, std::false_type{});
     }
     sh_wait_vmcnt<0>();      // clamped tail loads land before the LDS is reused below
     __syncthreads();
