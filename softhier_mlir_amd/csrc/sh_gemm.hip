@@ -816,7 +816,10 @@ __device__ __forceinline__ void store_all(const GemmArgs &a, const uint4 (&q)[FM
 // the reads of 16 consecutive chunks stay a permutation of one line.
 // The slots may span NSTG free stages of the ring: slot s is slot s % NSLOT of stage (first + s / NSLOT) mod nst,
 // stages stage_bytes apart from `ring` (the ring base plus the wavefront's offset in a slot).
-template <int TM, int TN, int FM, int FN, int NSLOT, int SSTRIDE, int NSTG = 1>
+// OFF32: Z and the residual span less than 4 GiB from their bases, and rows and leading dimensions are below 2^24
+// (the launch checks both): each lane's store and load addresses are the tensor's base (scalar registers) plus a
+// 32-bit byte offset from a 24-bit multiply-add, instead of 64-bit address arithmetic.
+template <int TM, int TN, int FM, int FN, int NSLOT, int SSTRIDE, int NSTG = 1, bool OFF32 = false>
 __device__ __forceinline__ void store_wave_staged(const GemmArgs &a, const uint4 (&q)[FM][FN][2], uint32_t rbase, uint32_t cbase,
                                                   char *ring, uint32_t first, uint32_t nst, uint32_t stage_bytes) {
     constexpr int CPRW = TN / 8, HALF = 32 * CPRW, STEPS = HALF / 64;
@@ -835,7 +838,10 @@ __device__ __forceinline__ void store_wave_staged(const GemmArgs &a, const uint4
         for (int u = 0; u < STEPS; ++u) {                // residual row chunks first: their latency overlaps the staging
             const int lin = u * 64 + lane, row = lin / CPRW, c = lin % CPRW;
             const uint32_t gm = min(rbase + 32 * i + row, a.M - 1), gn = min(cbase + 8 * c, a.N - 8);
-            rq[u] = a.res ? *(const uint4 *)(a.res + (uint64_t)gm * a.ldr + gn) : zero4();
+            if constexpr (OFF32)
+                rq[u] = a.res ? *(const uint4 *)((const char *)a.res + (__umul24(gm, (uint32_t)a.ldr) + gn) * 2u) : zero4();
+            else
+                rq[u] = a.res ? *(const uint4 *)(a.res + (uint64_t)gm * a.ldr + gn) : zero4();
         }
 #pragma unroll
         for (int j = 0; j < FN; ++j)
@@ -850,7 +856,11 @@ __device__ __forceinline__ void store_wave_staged(const GemmArgs &a, const uint4
             uint4 v = *(const uint4 *)(slot(u) + (phys(lin) % 64) * 16);
             if (a.res) v = make_uint4(sh_hadd2(v.x, rq[u].x), sh_hadd2(v.y, rq[u].y), sh_hadd2(v.z, rq[u].z), sh_hadd2(v.w, rq[u].w));
             const uint32_t gm = rbase + 32 * i + row, gn = cbase + 8 * c;
-            if (gm < a.M && gn < a.N) *(uint4 *)(a.z + (uint64_t)gm * a.ldz + gn) = v;
+            if constexpr (OFF32) {
+                if (gm < a.M && gn < a.N) *(uint4 *)((char *)a.z + (__umul24(gm, (uint32_t)a.ldz) + gn) * 2u) = v;
+            } else {
+                if (gm < a.M && gn < a.N) *(uint4 *)(a.z + (uint64_t)gm * a.ldz + gn) = v;
+            }
         }
     }
 }
@@ -1193,7 +1203,7 @@ __global__ __launch_bounds__(256 * KG, MINW) void k_gemm5(GemmArgs a_in) {
             constexpr int NSTG = (4 * TN + 64 * C::LOADS - 1) / (64 * C::LOADS);      // stages the block needs
             GemmArgs as = a;
             if (!stage_res) as.res = nullptr;        // already added in the chain
-            store_wave_staged<TM, TN, FM, FN, C::LOADS, 4096, NSTG>(as, qc, m0 + wm * TM, n0 + wn * TN,
+            store_wave_staged<TM, TN, FM, FN, C::LOADS, 4096, NSTG, EPI != EPI_ANY>(as, qc, m0 + wm * TM, n0 + wn * TN,
                                                                      (char *)smem + (size_t)wave * 1024, (uint32_t)(KT % NST),
                                                                      (uint32_t)NST, (uint32_t)C::STAGE);
         } else {
@@ -1823,7 +1833,10 @@ int gemm_epi_kind(const GemmArgs &a) {
 // The kernel an unsplit, vector-path call of tile configuration c launches.
 KernelFn unsplit_kernel(const KCfg &c, const GemmArgs &a) {
     const int ek = gemm_epi_kind(a);
-    return ek != EPI_ANY && c.epi[ek] ? c.epi[ek] : c.vec[0];
+    // (the epilogue builds address Z and the residual with 32-bit byte offsets from their bases)
+    const bool off32 = ((uint64_t)a.M * a.ldz + a.N) * 2 < (1ull << 32) && (!a.res || ((uint64_t)a.M * a.ldr + a.N) * 2 < (1ull << 32)) &&
+                       a.M < (1u << 24) && a.ldz < (1u << 24) && a.ldr < (1u << 24);
+    return ek != EPI_ANY && c.epi[ek] && off32 ? c.epi[ek] : c.vec[0];
 }
 
 int tuned_cfg(const GemmArgs &call, int heur, hipStream_t st, bool wt) {
