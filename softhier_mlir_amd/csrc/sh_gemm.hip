@@ -1008,10 +1008,26 @@ __global__ __launch_bounds__(256 * KG, MINW) void k_gemm5(GemmArgs a_in) {
     const uint64_t wadv = WT ? (uint64_t)SK : (uint64_t)SK * a.ldw;
     const uint32_t lds0 = sh_lds_addr(ring);
     const uint32_t wave_off = (uint32_t)wave * 1024u;
+    // epilogue builds (the launch checks the leading dimensions): the same addresses as a wave-uniform base per operand
+    // (scalar registers, advanced by the slice) plus each lane's 32-bit byte offset from it, which is >= 0 since the
+    // clamped rows and columns never fall below the tile's first (no 64-bit vector add per DMA)
+    constexpr bool OFF32 = EPI != EPI_ANY;
+    const char *const xb = (const char *)(a.x + (uint64_t)m0 * a.ldx + kbeg);
+    const char *const wb = WT ? (const char *)(a.w + (uint64_t)n0 * a.ldw + kbeg) : (const char *)(a.w + (uint64_t)kbeg * a.ldw + n0);
+    uint32_t xo[C::XR], wo[C::WR];
+#pragma unroll
+    for (int r = 0; r < C::XR; ++r) xo[r] = (uint32_t)((const char *)xs[r] - xb);
+#pragma unroll
+    for (int r = 0; r < C::WR; ++r) wo[r] = (uint32_t)((const char *)ws[r] - wb);
     auto dma = [&](int d, int src, int stage) {          // DMA instruction d of slice `src` into `stage`
         const uint32_t st = lds0 + (uint32_t)stage * (uint32_t)C::STAGE;
-        if (d < C::XR) sh_lds_dma16(xs[d] + (uint64_t)src * SK, st + d * 4096 + wave_off);
-        else sh_lds_dma16(ws[d - C::XR] + (uint64_t)src * wadv, st + C::XCH * 16 + (d - C::XR) * 4096 + wave_off);
+        if constexpr (OFF32) {
+            if (d < C::XR) sh_lds_dma16_s(xb + (uint64_t)src * SK * 2, xo[d], st + d * 4096 + wave_off);
+            else sh_lds_dma16_s(wb + (uint64_t)src * wadv * 2, wo[d - C::XR], st + C::XCH * 16 + (d - C::XR) * 4096 + wave_off);
+        } else {
+            if (d < C::XR) sh_lds_dma16(xs[d] + (uint64_t)src * SK, st + d * 4096 + wave_off);
+            else sh_lds_dma16(ws[d - C::XR] + (uint64_t)src * wadv, st + C::XCH * 16 + (d - C::XR) * 4096 + wave_off);
+        }
     };
 
     // fragment reads: instruction r of substep s (X fragments first, then W fragments, one or two each)
@@ -1833,9 +1849,9 @@ int gemm_epi_kind(const GemmArgs &a) {
 // The kernel an unsplit, vector-path call of tile configuration c launches.
 KernelFn unsplit_kernel(const KCfg &c, const GemmArgs &a) {
     const int ek = gemm_epi_kind(a);
-    // (the epilogue builds address Z and the residual with 32-bit byte offsets from their bases)
+    // (the epilogue builds address Z, the residual and their operand DMAs with 32-bit byte offsets from scalar bases)
     const bool off32 = ((uint64_t)a.M * a.ldz + a.N) * 2 < (1ull << 32) && (!a.res || ((uint64_t)a.M * a.ldr + a.N) * 2 < (1ull << 32)) &&
-                       a.M < (1u << 24) && a.ldz < (1u << 24) && a.ldr < (1u << 24);
+                       a.M < (1u << 24) && a.ldz < (1u << 24) && a.ldr < (1u << 24) && a.ldx < (1u << 22) && a.ldw < (1u << 22);
     return ek != EPI_ANY && c.epi[ek] && off32 ? c.epi[ek] : c.vec[0];
 }
 
