@@ -26,6 +26,8 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
+#include <utility>
 #include <map>
 #include <tuple>
 
@@ -906,6 +908,12 @@ __device__ __forceinline__ uint32_t xswz(uint32_t m) { return SK == 32 ? sx4(m) 
 // (substep s, lane group g -> 8-k chunk 2 s + g), so every configuration stores the same bits.
 // PRE: the epilogue's bias row and residual are loaded into registers at the start of the last slice, so the
 // epilogue does not wait a memory latency after the last MFMA (register budget permitting).
+// f(std::integral_constant<int, I>{}) for I = 0 .. N - 1, unrolled at compile time
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F &f, std::integer_sequence<int, I...>) { (f(std::integral_constant<int, I>{}), ...); }
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) { static_for_impl(f, std::make_integer_sequence<int, N>{}); }
+
 template <int BM, int BN, int SK, int NST, bool WT>
 struct Cfg5 {
     static constexpr int TM = BM / 2, TN = BN / 2, FM = TM / 32, FN = TN / 32, NS = SK / 16;
@@ -1126,14 +1134,17 @@ __global__ __launch_bounds__(256 * KG, MINW) void k_gemm5(GemmArgs a_in) {
     // complete in issue order, so the wait for the partials also sees those DMAs land)
     __builtin_amdgcn_sched_barrier(0);
     const LnRows<FM> lnw = ln_rows<FM>(a, m0 + wm * TM);
-    for (int kt = 0; kt < KT; ++kt) {
+    // slice kt, held in ring stage st = kt % NST, fixed at compile time: the loop below is unrolled by the ring's
+    // stages, so every fragment read is a per-lane register plus an immediate offset (no vector add per read)
+    auto slice = [&](int kt, auto stc) __attribute__((always_inline)) {
+        constexpr int st = decltype(stc)::value, nst = (st + NST - 1) % NST;
         sh_wait_vmcnt<(NST - 2) * C::LOADS>();           // slice kt landed (this wave's share) ...
         sh_wait_lgkm0();                                 // ... and this wave's reads of slice kt - 1 are done
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();                    // every share landed; the stage of slice kt - 1 is free
         __builtin_amdgcn_sched_barrier(0);
         if (PRE_B && kt == KT - 1 && pre_ok) prefetch();
-        const int st = kt % NST, nsrc = min(kt + NST - 1, KT - 1), nst = (kt + NST - 1) % NST;
+        const int nsrc = min(kt + NST - 1, KT - 1);
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             const int cur = s & 1, prv = cur ^ 1;
@@ -1152,7 +1163,13 @@ __global__ __launch_bounds__(256 * KG, MINW) void k_gemm5(GemmArgs a_in) {
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-    }
+    };
+    int kt0 = 0;
+    for (; kt0 + NST <= KT; kt0 += NST)
+        static_for<NST>([&](auto stc) __attribute__((always_inline)) { slice(kt0 + decltype(stc)::value, stc); });
+    static_for<NST - 1>([&](auto stc) __attribute__((always_inline)) {
+        if (kt0 + decltype(stc)::value < KT) slice(kt0 + decltype(stc)::value, stc);
+    });
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
