@@ -1047,6 +1047,21 @@ __global__ __launch_bounds__(256 * KG, MINW) void k_gemm5(GemmArgs a_in) {
         if constexpr (WT) return wf[buf][j];
         else return __builtin_bit_cast(sh_h8, __builtin_shufflevector(wl[buf][j], wh[buf][j], 0, 1, 2, 3, 4, 5, 6, 7));
     };
+    // [K, N] layout: each transpose read's LDS address in stage 0, per (substep, column block, half), formed once;
+    // a read adds its stage as an immediate offset
+    uint32_t wra[WT ? 1 : NS][WT ? 1 : FN][2];
+    if constexpr (!WT) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    const uint32_t n = (uint32_t)(wn * TN + j * 32 + 16 * (q & 1) + 4 * (iq & 3));
+                    const uint32_t k = 16 * s + 8 * g + (iq >> 2) + 4 * half;
+                    wra[s][j][half] = lds0 + C::XCH * 16 + k * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k)) + 2 * (n & 7);
+                }
+    }
     auto read = [&](int stage, int s, int r, int buf) {
         const uint32_t sb = (uint32_t)stage * (uint32_t)C::STAGE;
         const uint32_t c = (uint32_t)(2 * s + g);
@@ -1061,10 +1076,7 @@ __global__ __launch_bounds__(256 * KG, MINW) void k_gemm5(GemmArgs a_in) {
             wf[buf][j] = __builtin_bit_cast(sh_h8, W[n * XCPR + (c ^ xswz<SK>(n))]);
         } else {
             const int j = (r - FM) >> 1, half = (r - FM) & 1;
-            const uint32_t wbase = lds0 + sb + C::XCH * 16;
-            const uint32_t n = (uint32_t)(wn * TN + j * 32 + 16 * (q & 1) + 4 * (iq & 3));
-            const uint32_t k = 16 * s + 8 * g + (iq >> 2) + 4 * half;
-            const sh_s4 v = sh_ds_read_tr(wbase + k * (BN * 2) + 16 * ((n >> 3) ^ fw<BN>(k)) + 2 * (n & 7));
+            const sh_s4 v = sh_ds_read_tr(wra[WT ? 0 : s][WT ? 0 : j][half] + sb);
             if (!half) wl[buf][j] = v;
             else wh[buf][j] = v;
         }
