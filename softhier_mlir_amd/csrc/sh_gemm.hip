@@ -647,7 +647,7 @@ __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {     // (fp32 v
 
 // The LayerNorm fold on a wavefront's Z^T accumulators (block (i, j) of lane l: the row of ln's entry i, columns
 // ncol + 32 j + 8 q + 4 g + e in register 4 q + e), in place, before they are rounded.
-template <int FM, int FN>
+template <int FM, int FN, bool OFF32 = false>
 __device__ __forceinline__ void ln_fold_zt(const GemmArgs &a, sh_f16v (&acc)[FM][FN], const LnRows<FM> &ln, uint32_t ncol) {
     const int lane = threadIdx.x & 63, g = lane >> 5;
     const float *rr = ln.r, *rm = ln.rm;
@@ -658,7 +658,9 @@ __device__ __forceinline__ void ln_fold_zt(const GemmArgs &a, sh_f16v (&acc)[FM]
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const uint32_t n = min(ncol + 32 * j + 8 * q + 4 * g, a.N - 4);
-            const float4 c4 = *(const float4 *)(a.ln_c + n), d4 = *(const float4 *)(d + n);
+            // (OFF32: scalar base plus a 32-bit byte offset, N < 2^24)
+            const float4 c4 = OFF32 ? *(const float4 *)((const char *)a.ln_c + n * 4u) : *(const float4 *)(a.ln_c + n);
+            const float4 d4 = OFF32 ? *(const float4 *)((const char *)d + n * 4u) : *(const float4 *)(d + n);
             cj[4 * q] = c4.x; cj[4 * q + 1] = c4.y; cj[4 * q + 2] = c4.z; cj[4 * q + 3] = c4.w;
             dj[4 * q] = d4.x; dj[4 * q + 1] = d4.y; dj[4 * q + 2] = d4.z; dj[4 * q + 3] = d4.w;
         }
@@ -674,7 +676,7 @@ __device__ __forceinline__ void ln_fold_zt(const GemmArgs &a, sh_f16v (&acc)[FM]
 // and M2 = sum (v - s / 32)^2 (two passes in fp32; lanes g = 0, 1 hold 16 values each), written as a float2 to
 // stats_out[row][block] (the consumer combines a row's blocks with ln_row). Stores the same bits in every
 // register-epilogue tile (the same 32 values, the same order).
-template <int FM, int FN>
+template <int FM, int FN, bool OFF32 = false>
 __device__ __forceinline__ void stats_zt(const GemmArgs &a, const uint4 (&q)[FM][FN][2], uint32_t rbase, uint32_t cbase) {
     const int lane = threadIdx.x & 63, g = lane >> 5, r32 = lane & 31;
     const uint32_t P = a.N / 32;
@@ -701,7 +703,12 @@ __device__ __forceinline__ void stats_zt(const GemmArgs &a, const uint4 (&q)[FM]
             for (int e = 0; e < 16; ++e) { const float d = x[e] - mb; m2 = fmaf(d, d, m2); }
             m2 += __shfl_xor(m2, 32, 64);
             const uint32_t col = cbase + 32 * j;
-            if (g == 0 && row < a.M && col < a.N) ((float2 *)a.stats_out)[(uint64_t)row * P + col / 32] = make_float2(sum, m2);
+            if (g == 0 && row < a.M && col < a.N) {
+                if constexpr (OFF32)           // (M N / 4 bytes of partials < 4 GiB: the launch checks it)
+                    *(float2 *)((char *)a.stats_out + (__umul24(row, P) + col / 32) * 8u) = make_float2(sum, m2);
+                else
+                    ((float2 *)a.stats_out)[(uint64_t)row * P + col / 32] = make_float2(sum, m2);
+            }
         }
     }
 }
@@ -1119,7 +1126,8 @@ __global__ __launch_bounds__(256 * KG, MINW) void k_gemm5(GemmArgs a_in) {
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
                 const uint32_t gc = min(n0 + wn * TN + 32 * j + 16 * p + 8 * g, a.N - 8);
-                bq[j][p] = a.bias ? *(const uint4 *)((const uint16_t *)a.bias + gc) : zero4();
+                if constexpr (OFF32) bq[j][p] = a.bias ? *(const uint4 *)((const char *)a.bias + gc * 2u) : zero4();
+                else bq[j][p] = a.bias ? *(const uint4 *)((const uint16_t *)a.bias + gc) : zero4();
             }
         if constexpr (PRE_RES) {
 #pragma unroll
@@ -1218,7 +1226,7 @@ __global__ __launch_bounds__(256 * KG, MINW) void k_gemm5(GemmArgs a_in) {
     if constexpr (SPLIT) {
         store_partials_zt<BM, BN, FM, FN>(a, acc, m0, n0, split, wm, wn);
     } else {
-        if (a.ln_stats) ln_fold_zt<FM, FN>(a, acc, lnw, n0 + wn * TN);
+        if (a.ln_stats) ln_fold_zt<FM, FN, OFF32>(a, acc, lnw, n0 + wn * TN);
         uint4 qc[FM][FN][2];
 #pragma unroll
         for (int i = 0; i < FM; ++i)
@@ -1240,7 +1248,7 @@ __global__ __launch_bounds__(256 * KG, MINW) void k_gemm5(GemmArgs a_in) {
         } else {
             chain_chunks<BM, BN, FM, FN>(an, qc, m0, n0, wm, wn);
         }
-        if (has_stats) stats_zt<FM, FN>(a, qc, m0 + wm * TM, n0 + wn * TN);
+        if (has_stats) stats_zt<FM, FN, OFF32>(a, qc, m0 + wm * TM, n0 + wn * TN);
         if constexpr (STAGED) {
             // every stage but slice KT - 1's holds no slice any more (only the clamped tail DMAs, each wavefront's
             // into its own slots): their last reads were slices <= KT - 2, finished before slice KT - 1's barrier
@@ -1880,7 +1888,8 @@ KernelFn unsplit_kernel(const KCfg &c, const GemmArgs &a) {
     const int ek = gemm_epi_kind(a);
     // (the epilogue builds address Z, the residual and their operand DMAs with 32-bit byte offsets from scalar bases)
     const bool off32 = ((uint64_t)a.M * a.ldz + a.N) * 2 < (1ull << 32) && (!a.res || ((uint64_t)a.M * a.ldr + a.N) * 2 < (1ull << 32)) &&
-                       a.M < (1u << 24) && a.ldz < (1u << 24) && a.ldr < (1u << 24) && a.ldx < (1u << 22) && a.ldw < (1u << 22);
+                       a.M < (1u << 24) && a.N < (1u << 24) && a.ldz < (1u << 24) && a.ldr < (1u << 24) && a.ldx < (1u << 22) &&
+                       a.ldw < (1u << 22) && (uint64_t)a.M * a.N / 4 < (1ull << 32);
     return ek != EPI_ANY && c.epi[ek] && off32 ? c.epi[ek] : c.vec[0];
 }
 
