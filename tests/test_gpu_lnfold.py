@@ -315,6 +315,39 @@ def test_epilogue_builds_store_the_bits_of_the_general_build(lib, gpu, cfg, monk
         assert np.array_equal(z1, z0)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("cfg", [16, 32])
+def test_epilogue_builds_give_way_to_the_general_build_past_their_address_range(lib, gpu, cfg, monkeypatch):
+    """The epilogue builds address X, W, Z and the residual with 32-bit offsets from scalar bases, so the launch uses
+    them only for leading dimensions of X below 2^22 and of Z below 2^24; past that the general build runs. The same
+    product with fp16 bias and residual, with X and Z stored compactly, at leading dimensions just inside those limits
+    and just past them, stores the same bits every time (and meets the oracle)."""
+    import torch
+    M, N, K = 2, 192, 64
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    w = (rng.standard_normal((K, N)) * 0.1).astype(np.float16)
+    b = (rng.standard_normal((1, N)) * 0.1).astype(np.float16)
+    r = rng.standard_normal((M, N)).astype(np.float16)
+    W, Bb, R = to_dev(w), to_dev(b), to_dev(r)
+    monkeypatch.setenv("SH_GEMM_CFG", str(cfg))
+    got = []
+    for ldx, ldz in ((K, N), ((1 << 22) - 64, (1 << 24) - 192), ((1 << 22) + 64, N), (K, (1 << 24) + 192)):
+        X = torch.zeros((M, ldx), dtype=torch.float16, device="cuda")
+        X[:, :K] = torch.from_numpy(x).cuda()
+        Z = torch.zeros((M, ldz), dtype=torch.float16, device="cuda")
+        e = shops.epi(bias=A(Bb), residual=A(R), ldr=N)
+        assert lib.sh_gemm_ex(A(X), A(W), A(Z), M, N, K, ldx, N, ldz, None, e) == 0, shops.last_error()
+        got.append(codes(Z[:, :N].contiguous()))
+        del X, Z
+    for z in got[1:]:
+        assert np.array_equal(z, got[0])
+    want = (refs.r16(refs.r16(refs.r16(x.astype(np.float32) @ w.astype(np.float32)) + b.astype(np.float32))
+            + r.astype(np.float32)))
+    have = got[0].view(np.float16).astype(np.float32)
+    assert np.all(np.abs(have - want) <= 2e-2 + 1e-2 * np.abs(want))
+
+
 @pytest.mark.parametrize("mean,act", [(0.7, 0), (0.7, 1), (60.0, 0)])
 def test_fold_from_row_partials(lib, gpu, mean, act):
     """The consumer of row partials (ln_parts = K / 32): H from a GEMM that wrote its partials, then the folded
