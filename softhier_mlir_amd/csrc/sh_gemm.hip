@@ -34,13 +34,6 @@
 namespace {
 
 constexpr int BK = 64;
-#ifndef SH_GEMM_DMA_FRONT
-#define SH_GEMM_DMA_FRONT 0
-#endif
-#ifndef SH_GEMM_DMA_SPAN_NUM
-#define SH_GEMM_DMA_SPAN_NUM 1
-#define SH_GEMM_DMA_SPAN_DEN 1
-#endif
 
 struct GemmArgs {
     const uint16_t *x, *w;
@@ -573,10 +566,6 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs a) {
         const uint32_t st = lds0 + (uint32_t)(kt % STAGES) * (uint32_t)C::STAGE;
         const uint4 *X = (const uint4 *)((const char *)smem + (uint32_t)(kt % STAGES) * (uint32_t)C::STAGE);
         const uint32_t wbase = st + C::XCH * 16;
-#if SH_GEMM_DMA_FRONT
-#pragma unroll
-        for (int d = 0; d < C::LOADS; ++d) issue_one(d, kn, kst);
-#endif
         // fragments of k-substep s (16 k): A from X rows (one 16-byte read), B from two transpose reads
         auto load_frags = [&](int s, sh_h8 (&af)[C::FM], sh_h8 (&bf)[C::FN]) {
 #pragma unroll
@@ -608,13 +597,9 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs a) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[s & 1][i], bf[s & 1][j], acc[i][j], 0, 0, 0);
                     // DMA d goes out after MFMA number floor(d * MT / LOADS): loads trickle under the MFMAs
                     const int gi = s * NM + i * C::FN + j;
-#if !SH_GEMM_DMA_FRONT
 #pragma unroll
                     for (int d = 0; d < C::LOADS; ++d)
-                        if ((d * MT * SH_GEMM_DMA_SPAN_NUM) / (C::LOADS * SH_GEMM_DMA_SPAN_DEN) == gi) { __builtin_amdgcn_sched_barrier(0); issue_one(d, kn, kst); __builtin_amdgcn_sched_barrier(0); }
-#else
-                    (void)gi;
-#endif
+                        if (d * MT / C::LOADS == gi) { __builtin_amdgcn_sched_barrier(0); issue_one(d, kn, kst); __builtin_amdgcn_sched_barrier(0); }
                 }
             __builtin_amdgcn_sched_barrier(0);
         }
