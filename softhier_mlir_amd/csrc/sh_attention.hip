@@ -530,11 +530,12 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash2(AttnArgs a, ui
 
 // One-pass variant of k_flash2 (the default for aligned dh 64 / 128 heads whose scale folds, |c| <= 1, without a
 // token mask): each key block's scores come out of the MFMAs already shifted by the query's reference m (the FOLD
-// bias step: ones x (-m_hi, -m_lo)), so p = 2^acc. m starts at 0 and moves to a block's maximum when that maximum
-// exceeds m by more than kTau (log2 units), or, for the first block, lies more than kTau below it; only then are O
-// and l rescaled by 2^-shift and the block's scores computed again with the new bias (a wave-uniform branch, rare
-// for attention inputs of moderate scale). m thus stays within kTau of the running maximum: numerators are at most
-// 2^kTau and the largest is at least 2^-kTau, well inside fp16's normal range, and the row sums are the sums of the
+// bias step: ones x (-m_hi, -m_lo)), so p = 2^acc. m starts at 0 and moves to the first block's maximum when that
+// lies more than kTau (log2 units) from 0; a later block is first tested by its numerators' sum per lane (32 keys,
+// formed for the row sum anyway), and only when that exceeds 32 x 2^kTau is its maximum formed and m moved for the
+// queries whose maximum exceeds m by more than kTau. Only then are O and l rescaled by 2^-shift and the block's scores
+// computed again with the new bias (a wave-uniform branch, rare for attention inputs of moderate scale). Numerators
+// are thus at most 32 x 2^kTau and the largest is at least 2^-kTau, well inside fp16's normal range, and the row sums are the sums of the
 // same fp16 numerators the P.V product uses, so O / l is the softmax with every p rounded once. Against k_flash2
 // this drops the maximum pass (its score MFMAs, K fragment reads and K DMAs) and the refill of the ring between the
 // passes. Same LDS ring, fragment prefetch and occupancy as k_flash2.
@@ -739,15 +740,45 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
 #pragma unroll
         for (int j = 0; j < VA; ++j) vr[j] = vfrag(j);
         expo();
-        // the block's maximum for this lane's query (lanes r32 and r32 + 32 hold complementary keys), two chains
-        float b0 = -INFINITY, b1 = -INFINITY;
+        // this lane's sum of the block's fp16 numerators (fp32 sums, four chains): the row sum's share and, for a
+        // later block, the test whether m must move
+        auto psum = [&]() -> float {
+            float c[4];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) { b0 = fmaxf(b0, sacc[0][r]); b1 = fmaxf(b1, sacc[1][r]); }
-        const float bm = sh_max_xor32(fmaxf(b0, b1));
-        // m starts at 0; the first block moves it when its maximum is more than kTau away on either side, a later one
-        // when its maximum exceeds m by more than kTau (every block holds a valid key: bm is finite)
-        const bool move = first ? fabsf(bm) > kTau : bm > kTau;
-        if (__ballot(move) != 0) {                   // wave-uniform: m moves, O and l rescale, scores again
+            for (int sp = 0; sp < 4; ++sp) {
+                const uint4 w = __builtin_bit_cast(uint4, pf[sp]);
+                c[sp] = __builtin_amdgcn_fdot2(__builtin_bit_cast(sh_h2, w.x), one2, 0.f, false);
+                c[sp] = __builtin_amdgcn_fdot2(__builtin_bit_cast(sh_h2, w.y), one2, c[sp], false);
+                c[sp] = __builtin_amdgcn_fdot2(__builtin_bit_cast(sh_h2, w.z), one2, c[sp], false);
+                c[sp] = __builtin_amdgcn_fdot2(__builtin_bit_cast(sh_h2, w.w), one2, c[sp], false);
+            }
+            return (c[0] + c[1]) + (c[2] + c[3]);
+        };
+        // the block's maximum for this lane's query (lanes r32 and r32 + 32 hold complementary keys), two chains
+        auto block_max = [&]() -> float {
+            float b0 = -INFINITY, b1 = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) { b0 = fmaxf(b0, sacc[0][r]); b1 = fmaxf(b1, sacc[1][r]); }
+            return sh_max_xor32(fmaxf(b0, b1));
+        };
+        float blk = 0.f, bm = 0.f;
+        // m starts at 0; the first block moves it when its maximum is more than kTau away on either side (every
+        // block holds a valid key: bm is finite). A later block is tested by its numerators' sum, which the row sum
+        // needs anyway: only when some lane's 32 numerators sum past 32 x 2^kTau (so one of them exceeds 2^kTau, and
+        // its query's maximum exceeds m by more than kTau) is the maximum formed, and m moves for the queries whose
+        // maximum exceeds m by more than kTau, as the first rule would move them.
+        bool test;
+        if constexpr (first) {
+            bm = block_max();
+            test = __ballot(fabsf(bm) > kTau) != 0;
+        } else {
+            blk = psum();
+            test = __ballot(blk > 32.f * 256.f) != 0;
+            static_assert(kTau == 8.f, "the sum threshold is 32 x 2^kTau");
+            if (test) bm = block_max();
+        }
+        if (test) {                                  // wave-uniform: m may move, O and l rescale, scores again
+            const bool move = first ? fabsf(bm) > kTau : bm > kTau;
             const float shift = move ? bm : 0.f;
             // before the first block O and l are still empty: nothing to rescale (2^-shift overflows to +inf for a
             // first-block maximum below -128, and 0 x inf would be NaN)
@@ -763,18 +794,14 @@ __global__ __launch_bounds__(256, DH == 64 ? 3 : 2) void k_flash3(AttnArgs a, ui
             scores(stc, sacc, Biased{});
             mask_tail();
             expo();
+            if constexpr (!first) blk = psum();
         }
         if constexpr (first) {
             attn_stamp(stamp, last, 3);
             attn_stamp(stamp, last, 4);
-        }
-#pragma unroll
-        for (int sp = 0; sp < 4; ++sp) {
-            const uint4 w = __builtin_bit_cast(uint4, pf[sp]);
-            lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(sh_h2, w.x), one2, lsum, false);
-            lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(sh_h2, w.y), one2, lsum, false);
-            lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(sh_h2, w.z), one2, lsum, false);
-            lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(sh_h2, w.w), one2, lsum, false);
+            lsum = psum();
+        } else {
+            lsum += blk;
         }
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
